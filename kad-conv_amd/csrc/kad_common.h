@@ -1,0 +1,58 @@
+// Shared definitions for the KAD-Conv gfx950 HIP library.
+//
+// Conventions used by every kernel in this library:
+//  * Feature maps handed between kernels are NHWC with a channel stride that is
+//    a multiple of 8 elements (16 bytes for fp16/bf16); the stride's padding
+//    channels hold zeros, so 16-byte vector loads never need a tail case.
+//  * Per-pixel side tensors (offsets, masks) are fp32, addressed through
+//    explicit (image, pixel, channel) strides so both pixel-major [N, P, C] and
+//    torchvision's plane-major [N, C, P] layouts are read in place.
+//  * Accumulation is fp32 everywhere; fp16/bf16 only at storage and MFMA inputs.
+//  * Entry points never allocate, never synchronise, and launch on the stream
+//    they are given; they return 0 or a negative KAD_E* code and record a
+//    message retrievable with kad_last_error() (thread-local).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kadconv_hip.h"
+
+namespace kad {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16_t;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef int intx4 __attribute__((ext_vector_type(4)));
+
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(half_t v) { return (float)v; }
+__device__ __forceinline__ float to_f32(bf16_t v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ half_t from_f32<half_t>(float v) { return (half_t)v; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) { return (bf16_t)v; }
+
+// Logistic function built on the HIP device expf.
+__device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }
+
+__host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ inline int round_up(int a, int b) { return ceil_div(a, b) * b; }
+
+inline int dtype_size(int dtype) {
+  return dtype == KAD_F32 ? 4 : 2;
+}
+
+}  // namespace kad
+
+#define KAD_CHECK_ARG(cond, ...) \
+  do { if (!(cond)) return ::kad::fail(KAD_EINVAL, __VA_ARGS__); } while (0)

@@ -98,6 +98,116 @@ typedef struct kad_dcn_args {
  * as called at KAD-Conv/kadconv/kad_conv.py:66-67. */
 int kad_dcn_fwd(const kad_dcn_args *a, void *stream);
 
+/* Plain 3x3 convolution on the same NHWC machinery (offset/mask ignored, may
+ * be NULL): DSC's offset branch `conv_offset` (KAD-Conv/kadconv/kad_conv.py:55-56,64),
+ * run by cuDNN in the reference fast path (acceleration/kadc_fused_sm75.py:1414-1421).
+ * `out` is always fp32 here (offsets feed the sampling coordinates); weights
+ * are packed with kad_dcn_pack_weights; post_* and relu apply as in kad_dcn_fwd. */
+int kad_conv3x3_fwd(const kad_dcn_args *a, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* 1x1 convolution GEMM with fused input average pool and bias/SiLU epilogue */
+/* ------------------------------------------------------------------------ */
+
+/* Elements of the packed weight buffer: [roundup(roundup(Cout,8),128)][roundup(Cin,32)], dtype. */
+int64_t kad_gemm_wpack_elems(int cin, int cout);
+
+/* Pack fp32 weights [Cout][Cin] (device) for kad_gemm1x1_fwd. */
+int kad_gemm_pack_weights(const float *w, void *wpack, int cin, int cout, int dtype, void *stream);
+
+typedef struct kad_gemm_args {
+  const void *x;          /* NCHW [N][Cin][H][W] or NHWC [N][H][W][x_cs], dtype */
+  const void *wpack;      /* kad_gemm_pack_weights output */
+  const float *bias;      /* [Cout] or NULL */
+  void *out;              /* NCHW [N][Cout][H/pool][W/pool] or NHWC [...][out_cs] (pad channels written 0) */
+  int n, cin, cout, h, w;
+  int pool;               /* s >= 1: avg_pool2d(kernel=s, stride=s, floor) applied to x first */
+  int in_layout, x_cs;
+  int out_layout, out_cs;
+  int act;                /* 0 = none, 1 = SiLU */
+  int dtype;
+} kad_gemm_args;
+
+/* out = act(W * avgpool_s(x) + b).  Stands in for the per-branch
+ * `avg_pool2d` + `nn.Conv2d(dim, c, 1)` of KADConv (kad_conv.py:101,115;
+ * reference fast path kadc_fused_parallel.py:74-103 with cuDNN) and for the
+ * fused 1x1 conv + bias + SiLU (KAD-CNet/inference/acceleration/kadc_gemm_silu.cpp:1-33
+ * -> kadc_gemm_silu.cu:125-176; acceleration/kadc_fused_sm75.py:504-532,616-629). */
+int kad_gemm1x1_fwd(const kad_gemm_args *a, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* LCSA mask                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* Elements of the fp32 LCSA parameter block for C channels:
+ * w1[C][11] | b1[C] | bn_a[C] | bn_b[C] | w3[C][11] | b3[C] | w4[9][C] | b4[9]. */
+int64_t kad_lcsa_params_elems(int c);
+
+/* Row means rowm[N][H][C] (over w) and column means colm[N][W][C] (over h) of
+ * an NHWC map: LCSA's pool_h / pool_w (kad_conv.py:26-27,39); reference
+ * Triton k_reduce_hw / k_reduce_hconv_bn_relu (acceleration/kadc_fused_sm75.py:800-888). */
+int kad_axial_means(const void *x, float *rowm, float *colm, int n, int c, int h, int w, int x_cs, int dtype,
+                    void *stream);
+
+/* mask[N][H][W][9] = sigmoid(LCSA(x)) from the axial means (kad_conv.py:28-39,65);
+ * reference k_hconv_bn_relu + k_vconv_pointwise9 (acceleration/kadc_fused_sm75.py:812-1080). */
+int kad_lcsa_mask(const float *rowm, const float *colm, const float *params, float *mask, int n, int c, int h,
+                  int w, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Squeeze-excitation                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* Rows of the partial-sum buffer kad_se_pool writes per image (1 for NCHW). */
+int kad_se_pool_tiles(int h, int w, int layout);
+
+/* partial[N][tiles][C] = per-tile channel sums of x (NCHW or NHWC).
+ * Reference: GAP inside the DCN kernel / k_gap_only (kadc_dcn16_kernel.cu:270-300;
+ * acceleration/kadc_fused_sm75.py:1195-1201). */
+int kad_se_pool(const void *x, float *partial, int n, int c, int h, int w, int layout, int x_cs, int dtype,
+                void *stream);
+
+/* att[N][C] = sigmoid(W2 relu(W1 (inv_count * sum_t partial[n][t]) + b1) + b2);
+ * W1 [hid][C], W2 [C][hid] fp32.  KADConv's `fc` (kad_conv.py:105-109,117);
+ * reference k_se_mlp (acceleration/kadc_fused_sm75.py:1518-1542) and
+ * gap_se_kernel (kadc_dcn16_kernel.cu:439-497). */
+int kad_se_mlp(const float *partial, int tiles, float inv_count, const float *w1, const float *b1, const float *w2,
+               const float *b2, float *att, int n, int c, int hid, void *stream);
+
+/* out = x * att[n][c] (NCHW, or NHWC with channel stride x_cs).
+ * Reference k_apply_tiled (acceleration/kadc_fused_sm75.py:1203-1217). */
+int kad_channel_scale(const void *x, const float *att, void *out, int n, int c, int h, int w, int layout, int x_cs,
+                      int dtype, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* Branch merge: bilinear upsample + channel attention + concat + residual   */
+/* ------------------------------------------------------------------------ */
+/* NCHW [N][C][H][W] -> NHWC [N][H][W][out_cs], channels >= C written 0: the
+ * layout the DSC kernels read.  The reference keeps NCHW throughout and has no
+ * counterpart; this is the entry used when a caller hands over NCHW tensors. */
+int kad_to_nhwc(const void *x, void *out, int n, int c, int h, int w, int out_cs, int dtype, void *stream);
+
+#define KAD_MAX_BRANCHES 4
+
+typedef struct kad_merge_args {
+  void *out;               /* [N][C][H][W] (NCHW) or [N][H][W][C] (NHWC), dtype */
+  const void *residual;    /* same layout as out, or NULL */
+  const float *gate;       /* [C] per-channel output multiplier, or NULL */
+  int n, c, h, w, layout, dtype, nbranch;
+  const void *br_z[KAD_MAX_BRANCHES];    /* NHWC [N][h_b][w_b][cs_b], dtype */
+  const float *br_att[KAD_MAX_BRANCHES]; /* [N][c_b] or NULL */
+  int br_c[KAD_MAX_BRANCHES], br_c_off[KAD_MAX_BRANCHES];
+  int br_h[KAD_MAX_BRANCHES], br_w[KAD_MAX_BRANCHES], br_cs[KAD_MAX_BRANCHES];
+  float br_coeff[KAD_MAX_BRANCHES];
+} kad_merge_args;
+
+/* out[n, c] = gate[c] * (residual + sum over branches b with c in [c_off_b, c_off_b + c_b):
+ *   coeff_b * att_b[n, c - c_off_b] * bilinear_up(z_b)[c - c_off_b]).
+ * KADConv's tail `F.interpolate(..., align_corners=False)`, `torch.cat` and `+ x`
+ * (kad_conv.py:117-121); reference k_upsample_bilinear_att + k_cat_residual_att0
+ * (acceleration/kadc_fused_sm75.py:1245-1331). */
+int kad_branch_merge(const kad_merge_args *a, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,7 @@
 // Error reporting and ABI identification for libkadconv_hip.so.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 #include "kad_common.h"
 
@@ -8,18 +9,14 @@ namespace kad {
 
 static thread_local char g_last_error[512] = "";
 
-void set_error(const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
-  va_end(ap);
-}
-
 int fail(int code, const char* fmt, ...) {
+  // format into a scratch buffer first: callers may pass the previous message as an argument
+  char buf[sizeof(g_last_error)];
   va_list ap;
   va_start(ap, fmt);
-  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
+  memcpy(g_last_error, buf, sizeof(buf));
   return code;
 }
 

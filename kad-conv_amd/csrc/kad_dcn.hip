@@ -42,8 +42,10 @@ template <typename T> struct DcnOps;
 
 template <> struct DcnOps<half_t> {
   typedef half8_t frag;
+  template <bool PLAIN>
   static __device__ __forceinline__ frag gather(const half_t* base, const SampleInfo& s, int cs, int ch, bool ok) {
     if (!ok) return frag{};
+    if (PLAIN) return *(const frag*)(base + (int64_t)s.idx[0] * cs + ch) * (half_t)s.w[0];
     const half_t* p0 = base + (int64_t)s.idx[0] * cs + ch;
     const half_t* p1 = base + (int64_t)s.idx[1] * cs + ch;
     const half_t* p2 = base + (int64_t)s.idx[2] * cs + ch;
@@ -63,8 +65,13 @@ template <> struct DcnOps<half_t> {
 
 template <> struct DcnOps<bf16_t> {
   typedef bf16x8_t frag;
+  template <bool PLAIN>
   static __device__ __forceinline__ frag gather(const bf16_t* base, const SampleInfo& s, int cs, int ch, bool ok) {
     if (!ok) return frag{};
+    if (PLAIN) {
+      frag v = *(const frag*)(base + (int64_t)s.idx[0] * cs + ch);
+      return s.w[0] != 0.f ? v : frag{};
+    }
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.f;
@@ -89,13 +96,14 @@ struct f32x8 { floatx4 lo, hi; };
 
 template <> struct DcnOps<float> {
   typedef f32x8 frag;
+  template <bool PLAIN>
   static __device__ __forceinline__ frag gather(const float* base, const SampleInfo& s, int cs, int ch, bool ok) {
     frag r;
     r.lo = floatx4{0.f, 0.f, 0.f, 0.f};
     r.hi = r.lo;
     if (!ok) return r;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < (PLAIN ? 1 : 4); ++c) {
       const float* p = base + (int64_t)s.idx[c] * cs + ch;
       floatx4 a = *(const floatx4*)p;
       floatx4 b = *(const floatx4*)(p + 4);
@@ -122,7 +130,9 @@ template <> struct DcnOps<float> {
 };
 
 // ---- kernel ------------------------------------------------------------------------
-template <typename T, int NBF>
+// PLAIN = true computes an ordinary 3x3 convolution (integer taps, no
+// offsets or mask): used for DSC's offset branch, conv_offset (kad_conv.py:55-56).
+template <typename T, typename OutT, int NBF, bool PLAIN>
 __global__ __launch_bounds__(DCN_THREADS) void dcn_fwd_kernel(kad_dcn_args a, int ho, int wo, int tiles,
                                                              int nchunk, int cout_pad) {
   typedef DcnOps<T> Ops;
@@ -147,7 +157,14 @@ __global__ __launch_bounds__(DCN_THREADS) void dcn_fwd_kernel(kad_dcn_args a, in
     SampleInfo s;
     s.idx[0] = s.idx[1] = s.idx[2] = s.idx[3] = 0;
     s.w[0] = s.w[1] = s.w[2] = s.w[3] = 0.f;
-    if (p < P) {
+    if (p < P && PLAIN) {
+      const int oy = p / wo, ox = p - (p / wo) * wo;
+      const int iy = oy * a.stride - a.pad + k / 3, ix = ox * a.stride - a.pad + (k - (k / 3) * 3);
+      if (iy >= 0 && iy < a.h && ix >= 0 && ix < a.w) {
+        s.idx[0] = iy * a.w + ix;
+        s.w[0] = 1.f;
+      }
+    } else if (p < P) {
       const int oy = p / wo, ox = p - (p / wo) * wo;
       const int ky = k / 3, kx = k - (k / 3) * 3;
       const float dy = a.offset[n * a.off_sn + (int64_t)p * a.off_sp + (2 * k) * a.off_sc];
@@ -200,13 +217,13 @@ __global__ __launch_bounds__(DCN_THREADS) void dcn_fwd_kernel(kad_dcn_args a, in
         if (co < cout_pad)
           bf[b] = Ops::load_b(wp + ((int64_t)(co * nchunk + c) * 9 + k) * 32 + grp * 8);
         else
-          bf[b] = Ops::gather(nullptr, si[0][0], 0, 0, false);
+          bf[b] = Ops::template gather<true>(nullptr, si[0][0], 0, 0, false);
       }
 #pragma unroll
       for (int m = 0; m < DCN_WM; ++m) {
         const int pl = wave * (16 * DCN_WM) + m * 16 + row;
         const SampleInfo s = si[k][pl];
-        frag af = Ops::gather(xb, s, a.x_cs, ch, ch_ok);
+        frag af = Ops::template gather<PLAIN>(xb, s, a.x_cs, ch, ch_ok);
 #pragma unroll
         for (int b = 0; b < NBF; ++b) acc[m][b] = Ops::mma(af, bf[b], acc[m][b]);
       }
@@ -233,11 +250,11 @@ __global__ __launch_bounds__(DCN_THREADS) void dcn_fwd_kernel(kad_dcn_args a, in
         if (a.relu) v = fmaxf(v, 0.f);
         v *= scl;
         if (co_ok && p < P) {
-          const T o = from_f32<T>(v);
+          const OutT o = from_f32<OutT>(v);
           if (a.out_layout == KAD_NHWC)
-            ((T*)a.out)[((int64_t)n * P + p) * a.out_cs + co] = o;
+            ((OutT*)a.out)[((int64_t)n * P + p) * a.out_cs + co] = o;
           else
-            ((T*)a.out)[((int64_t)n * a.cout + co) * P + p] = o;
+            ((OutT*)a.out)[((int64_t)n * a.cout + co) * P + p] = o;
           gsum[b] += to_f32(o);
         }
       }
@@ -278,13 +295,13 @@ __global__ void dcn_pack_kernel(const float* w, T* out, int cin, int cout, int n
   }
 }
 
-template <typename T, int NBF>
+template <typename T, typename OutT, int NBF, bool PLAIN>
 static int launch_dcn(const kad_dcn_args& a, hipStream_t st, int ho, int wo) {
   const int tiles = kad_dcn_tiles(ho, wo);
   const int nchunk = ceil_div(a.cin, 32);
   const int cout_pad = round_up(a.cout, 16);
   dim3 grid(tiles, ceil_div(a.cout, NBF * 16), a.n);
-  hipLaunchKernelGGL((dcn_fwd_kernel<T, NBF>), grid, dim3(DCN_THREADS), 0, st, a, ho, wo, tiles, nchunk, cout_pad);
+  hipLaunchKernelGGL((dcn_fwd_kernel<T, OutT, NBF, PLAIN>), grid, dim3(DCN_THREADS), 0, st, a, ho, wo, tiles, nchunk, cout_pad);
   return check_launch("kad_dcn_fwd");
 }
 
@@ -292,14 +309,14 @@ template <typename T>
 static int dispatch_dcn(const kad_dcn_args& a, hipStream_t st, int ho, int wo) {
   const int nbf = ceil_div(a.cout, 16);
   switch (nbf < 8 ? nbf : 8) {
-    case 1: return launch_dcn<T, 1>(a, st, ho, wo);
-    case 2: return launch_dcn<T, 2>(a, st, ho, wo);
-    case 3: return launch_dcn<T, 3>(a, st, ho, wo);
-    case 4: return launch_dcn<T, 4>(a, st, ho, wo);
-    case 5: return launch_dcn<T, 5>(a, st, ho, wo);
-    case 6: return launch_dcn<T, 6>(a, st, ho, wo);
-    case 7: return launch_dcn<T, 7>(a, st, ho, wo);
-    default: return launch_dcn<T, 8>(a, st, ho, wo);
+    case 1: return launch_dcn<T, T, 1, false>(a, st, ho, wo);
+    case 2: return launch_dcn<T, T, 2, false>(a, st, ho, wo);
+    case 3: return launch_dcn<T, T, 3, false>(a, st, ho, wo);
+    case 4: return launch_dcn<T, T, 4, false>(a, st, ho, wo);
+    case 5: return launch_dcn<T, T, 5, false>(a, st, ho, wo);
+    case 6: return launch_dcn<T, T, 6, false>(a, st, ho, wo);
+    case 7: return launch_dcn<T, T, 7, false>(a, st, ho, wo);
+    default: return launch_dcn<T, T, 8, false>(a, st, ho, wo);
   }
 }
 
@@ -330,22 +347,56 @@ extern "C" int kad_dcn_pack_weights(const float* w, void* wpack, int cin, int co
   return check_launch("kad_dcn_pack_weights");
 }
 
-extern "C" int kad_dcn_fwd(const kad_dcn_args* a, void* stream) {
-  KAD_CHECK_ARG(a, "kad_dcn_fwd: null args");
-  KAD_CHECK_ARG(a->x && a->offset && a->wpack && a->out, "kad_dcn_fwd: null tensor pointer");
+static int validate_dcn(const kad_dcn_args* a, bool need_offset, int* ho_out, int* wo_out) {
+  KAD_CHECK_ARG(a, "null args");
+  KAD_CHECK_ARG(a->x && a->wpack && a->out && (a->offset || !need_offset), "null tensor pointer");
   KAD_CHECK_ARG(a->n > 0 && a->cin > 0 && a->cout > 0 && a->h > 0 && a->w > 0,
-                "kad_dcn_fwd: bad shape n=%d cin=%d cout=%d h=%d w=%d", a->n, a->cin, a->cout, a->h, a->w);
-  KAD_CHECK_ARG(a->stride >= 1 && a->pad >= 0, "kad_dcn_fwd: bad stride=%d pad=%d", a->stride, a->pad);
+                "bad shape n=%d cin=%d cout=%d h=%d w=%d", a->n, a->cin, a->cout, a->h, a->w);
+  KAD_CHECK_ARG(a->stride >= 1 && a->pad >= 0, "bad stride=%d pad=%d", a->stride, a->pad);
   KAD_CHECK_ARG(a->x_cs % 8 == 0 && a->x_cs >= round_up(a->cin, 8),
-                "kad_dcn_fwd: x channel stride %d must be a multiple of 8 and >= roundup(cin=%d, 8)", a->x_cs, a->cin);
+                "x channel stride %d must be a multiple of 8 and >= roundup(cin=%d, 8)", a->x_cs, a->cin);
   KAD_CHECK_ARG(a->out_layout == KAD_NCHW || (a->out_layout == KAD_NHWC && a->out_cs >= a->cout),
-                "kad_dcn_fwd: bad output layout %d / channel stride %d", a->out_layout, a->out_cs);
+                "bad output layout %d / channel stride %d", a->out_layout, a->out_cs);
   const int ho = (a->h + 2 * a->pad - 3) / a->stride + 1;
   const int wo = (a->w + 2 * a->pad - 3) / a->stride + 1;
-  KAD_CHECK_ARG(ho > 0 && wo > 0, "kad_dcn_fwd: empty output");
-  KAD_CHECK_ARG((int64_t)a->h * a->w < (1ll << 31) && (int64_t)ho * wo * 9 < (1ll << 31), "kad_dcn_fwd: image too large");
+  KAD_CHECK_ARG(ho > 0 && wo > 0, "empty output");
+  KAD_CHECK_ARG((int64_t)a->h * a->w < (1ll << 31) && (int64_t)ho * wo * 9 < (1ll << 31), "image too large");
   const uintptr_t align = (uintptr_t)a->x | (uintptr_t)a->wpack;
-  KAD_CHECK_ARG(align % 16 == 0, "kad_dcn_fwd: x and wpack must be 16-byte aligned");
+  KAD_CHECK_ARG(align % 16 == 0, "x and wpack must be 16-byte aligned");
+  *ho_out = ho;
+  *wo_out = wo;
+  return KAD_OK;
+}
+
+template <typename T>
+static int dispatch_conv3x3(const kad_dcn_args& a, hipStream_t st, int ho, int wo) {
+  const int nbf = ceil_div(a.cout, 16);
+  switch (nbf < 8 ? nbf : 8) {
+    case 1: return launch_dcn<T, float, 1, true>(a, st, ho, wo);
+    case 2: return launch_dcn<T, float, 2, true>(a, st, ho, wo);
+    case 3: return launch_dcn<T, float, 3, true>(a, st, ho, wo);
+    case 4: return launch_dcn<T, float, 4, true>(a, st, ho, wo);
+    default: return launch_dcn<T, float, 8, true>(a, st, ho, wo);
+  }
+}
+
+extern "C" int kad_conv3x3_fwd(const kad_dcn_args* a, void* stream) {
+  int ho = 0, wo = 0;
+  int rc = validate_dcn(a, false, &ho, &wo);
+  if (rc) return fail(rc, "kad_conv3x3_fwd: %s", kad_last_error());
+  hipStream_t st = (hipStream_t)stream;
+  switch (a->dtype) {
+    case KAD_F32: return dispatch_conv3x3<float>(*a, st, ho, wo);
+    case KAD_F16: return dispatch_conv3x3<half_t>(*a, st, ho, wo);
+    case KAD_BF16: return dispatch_conv3x3<bf16_t>(*a, st, ho, wo);
+    default: return fail(KAD_EINVAL, "kad_conv3x3_fwd: unknown dtype %d", a->dtype);
+  }
+}
+
+extern "C" int kad_dcn_fwd(const kad_dcn_args* a, void* stream) {
+  int ho = 0, wo = 0;
+  int rc = validate_dcn(a, true, &ho, &wo);
+  if (rc) return fail(rc, "kad_dcn_fwd: %s", kad_last_error());
   hipStream_t st = (hipStream_t)stream;
   switch (a->dtype) {
     case KAD_F32: return dispatch_dcn<float>(*a, st, ho, wo);

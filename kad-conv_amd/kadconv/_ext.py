@@ -42,6 +42,30 @@ class DcnArgs(ctypes.Structure):
     ]
 
 
+class GemmArgs(ctypes.Structure):
+    _fields_ = [
+        ('x', c_vp), ('wpack', c_vp), ('bias', c_vp), ('out', c_vp),
+        ('n', c_int), ('cin', c_int), ('cout', c_int), ('h', c_int), ('w', c_int), ('pool', c_int),
+        ('in_layout', c_int), ('x_cs', c_int), ('out_layout', c_int), ('out_cs', c_int), ('act', c_int),
+        ('dtype', c_int),
+    ]
+
+
+MAX_BRANCHES = 4
+
+
+class MergeArgs(ctypes.Structure):
+    _fields_ = [
+        ('out', c_vp), ('residual', c_vp), ('gate', c_vp),
+        ('n', c_int), ('c', c_int), ('h', c_int), ('w', c_int), ('layout', c_int), ('dtype', c_int),
+        ('nbranch', c_int),
+        ('br_z', c_vp * MAX_BRANCHES), ('br_att', c_vp * MAX_BRANCHES),
+        ('br_c', c_int * MAX_BRANCHES), ('br_c_off', c_int * MAX_BRANCHES),
+        ('br_h', c_int * MAX_BRANCHES), ('br_w', c_int * MAX_BRANCHES), ('br_cs', c_int * MAX_BRANCHES),
+        ('br_coeff', ctypes.c_float * MAX_BRANCHES),
+    ]
+
+
 # name -> (restype, argtypes); must list every symbol declared in include/kadconv_hip.h
 SIGNATURES = {
     'kad_abi_version': (c_int, []),
@@ -50,6 +74,19 @@ SIGNATURES = {
     'kad_dcn_pack_weights': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     'kad_dcn_tiles': (c_int, [c_int, c_int]),
     'kad_dcn_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
+    'kad_conv3x3_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
+    'kad_gemm_wpack_elems': (c_i64, [c_int, c_int]),
+    'kad_gemm_pack_weights': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    'kad_gemm1x1_fwd': (c_int, [ctypes.POINTER(GemmArgs), c_vp]),
+    'kad_lcsa_params_elems': (c_i64, [c_int]),
+    'kad_axial_means': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_lcsa_mask': (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_se_pool_tiles': (c_int, [c_int, c_int, c_int]),
+    'kad_se_pool': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_se_mlp': (c_int, [c_vp, c_int, ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    'kad_channel_scale': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_to_nhwc': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_branch_merge': (c_int, [ctypes.POINTER(MergeArgs), c_vp]),
 }
 
 _lib = None
@@ -155,4 +192,146 @@ def dcn_fwd(x_nhwc, cin, offset, offset_strides, mask, mask_strides, wpack, cout
     if wpack.dtype != x_nhwc.dtype or out.dtype != x_nhwc.dtype:
         raise TypeError('x, packed weights and out must share a dtype')
     _check(load().kad_dcn_fwd(ctypes.byref(a), _stream()), 'kad_dcn_fwd')
+    return out
+
+
+def conv3x3_fwd(x_nhwc, cin, wpack, cout, out, *, stride=1, pad=1, bias=None, out_layout=KAD_NHWC):
+    """Plain 3x3 conv (offset branch) on NHWC input; `out` must be float32."""
+    _need_gpu(x_nhwc, wpack, out)
+    if out.dtype != torch.float32:
+        raise TypeError('conv3x3_fwd writes float32')
+    N, H, W, cs = x_nhwc.shape
+    a = DcnArgs()
+    a.x, a.wpack, a.bias, a.out = _ptr(x_nhwc), _ptr(wpack), _ptr(bias), _ptr(out)
+    a.n, a.cin, a.cout, a.h, a.w, a.stride, a.pad = N, cin, cout, H, W, stride, pad
+    a.x_cs = cs
+    a.out_layout = out_layout
+    a.out_cs = out.shape[-1] if out_layout == KAD_NHWC else cout
+    a.dtype = kad_dtype(x_nhwc.dtype)
+    _check(load().kad_conv3x3_fwd(ctypes.byref(a), _stream()), 'kad_conv3x3_fwd')
+    return out
+
+
+# ---------------------------------------------------------------------------- 1x1 GEMM
+def gemm_pack_weights(weight, dtype):
+    """weight [Cout, Cin] or [Cout, Cin, 1, 1] -> packed buffer of `dtype`."""
+    _need_gpu(weight)
+    cout = weight.shape[0]
+    w32 = weight.detach().reshape(cout, -1).to(torch.float32).contiguous()
+    cin = w32.shape[1]
+    out = torch.empty(load().kad_gemm_wpack_elems(cin, cout), dtype=dtype, device=weight.device)
+    _check(load().kad_gemm_pack_weights(_ptr(w32), _ptr(out), cin, cout, kad_dtype(dtype), _stream()),
+           'kad_gemm_pack_weights')
+    return out
+
+
+def gemm1x1_fwd(x, in_layout, cin, wpack, cout, out, out_layout, *, bias=None, pool=1, act=0, h=None, w=None):
+    """x: NCHW [N,Cin,H,W] or NHWC [N,H,W,x_cs]; out: NCHW [N,Cout,H/s,W/s] or NHWC [N,H/s,W/s,out_cs]."""
+    _need_gpu(x, wpack, out, bias)
+    a = GemmArgs()
+    if in_layout == KAD_NCHW:
+        N, C, H, W = x.shape
+        cs = C
+    else:
+        N, H, W, cs = x.shape
+    a.x, a.wpack, a.bias, a.out = _ptr(x), _ptr(wpack), _ptr(bias), _ptr(out)
+    a.n, a.cin, a.cout, a.h, a.w, a.pool = N, cin, cout, H, W, pool
+    a.in_layout, a.x_cs = in_layout, cs
+    a.out_layout = out_layout
+    a.out_cs = out.shape[-1] if out_layout == KAD_NHWC else cout
+    a.act = act
+    a.dtype = kad_dtype(x.dtype)
+    if wpack.dtype != x.dtype or out.dtype != x.dtype:
+        raise TypeError('x, packed weights and out must share a dtype')
+    if bias is not None and bias.dtype != torch.float32:
+        raise TypeError('bias must be float32')
+    _check(load().kad_gemm1x1_fwd(ctypes.byref(a), _stream()), 'kad_gemm1x1_fwd')
+    return out
+
+
+# ---------------------------------------------------------------------------- LCSA
+def lcsa_params_elems(c):
+    return load().kad_lcsa_params_elems(c)
+
+
+def axial_means(x_nhwc, c, rowm, colm):
+    _need_gpu(x_nhwc, rowm, colm)
+    N, H, W, cs = x_nhwc.shape
+    _check(load().kad_axial_means(_ptr(x_nhwc), _ptr(rowm), _ptr(colm), N, c, H, W, cs, kad_dtype(x_nhwc.dtype),
+                                  _stream()), 'kad_axial_means')
+
+
+def lcsa_mask(rowm, colm, params, mask, n, c, h, w):
+    _need_gpu(rowm, colm, params, mask)
+    _check(load().kad_lcsa_mask(_ptr(rowm), _ptr(colm), _ptr(params), _ptr(mask), n, c, h, w, _stream()),
+           'kad_lcsa_mask')
+
+
+# ---------------------------------------------------------------------------- SE
+def se_pool_tiles(h, w, layout):
+    return load().kad_se_pool_tiles(h, w, layout)
+
+
+def se_pool(x, c, layout, partial):
+    _need_gpu(x, partial)
+    if layout == KAD_NCHW:
+        N, _, H, W = x.shape
+        cs = c
+    else:
+        N, H, W, cs = x.shape
+    _check(load().kad_se_pool(_ptr(x), _ptr(partial), N, c, H, W, layout, cs, kad_dtype(x.dtype), _stream()),
+           'kad_se_pool')
+
+
+def se_mlp(partial, tiles, inv_count, w1, b1, w2, b2, att, n, c, hid):
+    _need_gpu(partial, w1, b1, w2, b2, att)
+    _check(load().kad_se_mlp(_ptr(partial), tiles, inv_count, _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(att),
+                             n, c, hid, _stream()), 'kad_se_mlp')
+
+
+def channel_scale(x, att, out, c, layout):
+    _need_gpu(x, att, out)
+    if layout == KAD_NCHW:
+        N, _, H, W = x.shape
+        cs = c
+    else:
+        N, H, W, cs = x.shape
+    _check(load().kad_channel_scale(_ptr(x), _ptr(att), _ptr(out), N, c, H, W, layout, cs, kad_dtype(x.dtype),
+                                    _stream()), 'kad_channel_scale')
+
+
+# ---------------------------------------------------------------------------- layout / merge
+def to_nhwc(x, out):
+    """x NCHW contiguous -> out NHWC [N,H,W,cs] (pad channels zeroed)."""
+    _need_gpu(x, out)
+    N, C, H, W = x.shape
+    _check(load().kad_to_nhwc(_ptr(x), _ptr(out), N, C, H, W, out.shape[-1], kad_dtype(x.dtype), _stream()),
+           'kad_to_nhwc')
+    return out
+
+
+def branch_merge(out, layout, branches, residual=None, gate=None):
+    """branches: list of dicts {z (NHWC [N,h,w,cs]), c, c_off, att (fp32 [N,c] or None), coeff}."""
+    _need_gpu(out, residual, gate)
+    if len(branches) > MAX_BRANCHES:
+        raise ValueError(f'at most {MAX_BRANCHES} branches')
+    a = MergeArgs()
+    if layout == KAD_NCHW:
+        N, C, H, W = out.shape
+    else:
+        N, H, W, C = out.shape
+    a.out, a.residual, a.gate = _ptr(out), _ptr(residual), _ptr(gate)
+    a.n, a.c, a.h, a.w, a.layout, a.dtype, a.nbranch = N, C, H, W, layout, kad_dtype(out.dtype), len(branches)
+    for i, b in enumerate(branches):
+        z = b['z']
+        _need_gpu(z, b.get('att'))
+        if z.dtype != out.dtype:
+            raise TypeError('branch maps and output must share a dtype')
+        a.br_z[i] = z.data_ptr()
+        att = b.get('att')
+        a.br_att[i] = att.data_ptr() if att is not None else None
+        a.br_c[i], a.br_c_off[i] = b['c'], b['c_off']
+        a.br_h[i], a.br_w[i], a.br_cs[i] = z.shape[1], z.shape[2], z.shape[3]
+        a.br_coeff[i] = float(b.get('coeff', 1.0))
+    _check(load().kad_branch_merge(ctypes.byref(a), _stream()), 'kad_branch_merge')
     return out

@@ -1,0 +1,130 @@
+"""The other fused blocks on the north-star path.
+
+* ``Conv1x1SiLU`` -- KAD-CNet's ``Conv`` (1x1 conv + BN + SiLU) after Conv-BN
+  fusion (KAD-CNet/models/common.py:43-57, utils/torch_utils.py:244-265):
+  SiLU(W x + b) as one MFMA GEMM with a fused epilogue.
+* ``SqueezeExcitation`` -- the channel attention KADConv applies per branch
+  (KAD-Conv/kadconv/kad_conv.py:105-109,117), as a standalone block with a
+  reduction ratio: GAP -> Linear -> ReLU -> Linear -> sigmoid -> channel scale.
+* ``KADDown`` -- stride-2 multi-branch downsampling with a learnable softmax
+  over branches and a per-channel sigmoid selection gate.  The reference has
+  no such operator; it is defined here from KADConv's branch structure
+  (kad_conv.py:112-121) as
+      y = sigmoid(gate) * sum_i softmax(alpha)_i * up(conv1x1_i(avgpool(x, 2^(i+1))))
+  with up = bilinear (align_corners=False) to (H // 2, W // 2).
+
+Eval-mode GPU inputs run the HIP kernels (no fallback: a missing library
+raises); training mode or CPU inputs run the plain torch composition.
+"""
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _ext, ops
+
+
+def _use_hip(module, x):
+    return (not module.training and x.is_cuda and x.dim() == 4
+            and x.dtype in (torch.float32, torch.float16, torch.bfloat16))
+
+
+class Conv1x1SiLU(nn.Module):
+    def __init__(self, c1, c2):
+        super().__init__()
+        self.conv = nn.Conv2d(c1, c2, 1, bias=True)
+        self._packed = {}
+
+    @classmethod
+    def from_conv_bn(cls, conv, bn):
+        """Fold a bias-free 1x1 Conv2d followed by BatchNorm2d (eval statistics)."""
+        m = cls(conv.in_channels, conv.out_channels)
+        with torch.no_grad():
+            a = bn.weight / torch.sqrt(bn.running_var + bn.eps)
+            m.conv.weight.copy_(conv.weight * a.view(-1, 1, 1, 1))
+            b = conv.bias if conv.bias is not None else torch.zeros_like(bn.bias)
+            m.conv.bias.copy_((b - bn.running_mean) * a + bn.bias)
+        return m.to(conv.weight.device)
+
+    def forward(self, x):
+        if _use_hip(self, x):
+            key = (x.dtype, self.conv.weight._version, self.conv.weight.data_ptr())
+            if key not in self._packed:
+                self._packed = {key: _ext.gemm_pack_weights(self.conv.weight, x.dtype)}
+            with torch.no_grad():
+                return ops.conv1x1(x, self.conv.weight, self.conv.bias, act='silu', wpack=self._packed[key])
+        return F.silu(self.conv(x))
+
+
+class SqueezeExcitation(nn.Module):
+    def __init__(self, c, reduction=16, min_hidden=1):
+        super().__init__()
+        hid = max(min_hidden, c // reduction)
+        self.fc = nn.Sequential(nn.Linear(c, hid), nn.ReLU(), nn.Linear(hid, c), nn.Sigmoid())
+
+    def forward(self, x):
+        if _use_hip(self, x):
+            with torch.no_grad():
+                return ops.squeeze_excitation(x, self.fc[0].weight, self.fc[0].bias, self.fc[2].weight,
+                                              self.fc[2].bias)
+        return x * self.fc(x.mean(dim=(2, 3))).view(x.shape[0], -1, 1, 1)
+
+
+class KADDown(nn.Module):
+    def __init__(self, c1, c2, n=3):
+        super().__init__()
+        self.n = n
+        self.proj = nn.ModuleList(nn.Conv2d(c1, c2, 1) for _ in range(n))
+        self.alpha = nn.Parameter(torch.zeros(n))
+        self.gate = nn.Parameter(torch.zeros(c2))
+        self._packed = {}
+
+    def _plain(self, x):
+        ho, wo = x.shape[2] // 2, x.shape[3] // 2
+        a = torch.softmax(self.alpha, dim=0)
+        z = 0
+        for i in range(self.n):
+            b = self.proj[i](F.avg_pool2d(x, kernel_size=2 ** (i + 1)))
+            if b.shape[2:] != (ho, wo):
+                b = F.interpolate(b, size=(ho, wo), mode='bilinear', align_corners=False)
+            z = z + a[i] * b
+        return z * torch.sigmoid(self.gate).view(1, -1, 1, 1)
+
+    def forward(self, x):
+        s = 2 ** self.n
+        if not _use_hip(self, x) or x.shape[2] < s or x.shape[3] < s or self.n > _ext.MAX_BRANCHES:
+            return self._plain(x)
+        with torch.no_grad():
+            return self._fast(x)
+
+    def _fast(self, x):
+        N, C, H, W = x.shape
+        c2 = self.proj[0].weight.shape[0]
+        cs = (c2 + 7) // 8 * 8
+        dtype, dev = x.dtype, x.device
+        # packed weights, softmax coefficients and gate are cached per parameter version
+        # (computing the softmax here per call would force a device->host sync)
+        params = [p.weight for p in self.proj] + [p.bias for p in self.proj] + [self.alpha, self.gate]
+        key = (dtype,) + tuple((p._version, p.data_ptr()) for p in params)
+        if key not in self._packed:
+            self._packed = {key: (
+                [_ext.gemm_pack_weights(p.weight, dtype) for p in self.proj],
+                [p.bias.detach().float().contiguous() for p in self.proj],
+                torch.softmax(self.alpha.detach().double(), dim=0).tolist(),
+                torch.sigmoid(self.gate.detach().float()).contiguous())}
+        packs, biases, coeff, gate = self._packed[key]
+        nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
+        xin, lay = (x.permute(0, 2, 3, 1), _ext.KAD_NHWC) if nhwc else (x.contiguous(), _ext.KAD_NCHW)
+        branches = []
+        for i in range(self.n):
+            s = 2 ** (i + 1)
+            b = torch.empty(N, H // s, W // s, cs, dtype=dtype, device=dev)
+            _ext.gemm1x1_fwd(xin, lay, C, packs[i], c2, b, _ext.KAD_NHWC,
+                             bias=biases[i], pool=s)
+            branches.append({'z': b, 'c': c2, 'c_off': 0, 'att': None, 'coeff': coeff[i]})
+        if nhwc:
+            out = torch.empty(N, c2, H // 2, W // 2, dtype=dtype, device=dev, memory_format=torch.channels_last)
+            _ext.branch_merge(out.permute(0, 2, 3, 1), _ext.KAD_NHWC, branches, gate=gate)
+        else:
+            out = torch.empty(N, c2, H // 2, W // 2, dtype=dtype, device=dev)
+            _ext.branch_merge(out, _ext.KAD_NCHW, branches, gate=gate)
+        return out

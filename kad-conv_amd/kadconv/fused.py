@@ -1,0 +1,192 @@
+"""Fused HIP forwards for KADConv and DSC (the fast inference path).
+
+``KADConvPlan`` snapshots one KADConv-like layer (KADConv, or KAD-CNet's
+KADC4 / KADC4_m -- same attribute names, KAD-CNet/models/module/KADC/module.py:14-68)
+into the form the kernels want: packed MFMA weights per dtype, eval-mode
+BatchNorm folded into the DCN epilogue, LCSA parameters in one block.  Its
+``forward`` runs, per branch i (kad_conv.py:112-121):
+
+  kad_gemm1x1_fwd   avg_pool 2^i + 1x1 projection        x (NCHW/NHWC) -> y_i (NHWC)
+  kad_axial_means   LCSA row/column means of y_i
+  kad_lcsa_mask     sigmoid(LCSA) mask                    -> [N, H_i, W_i, 9] fp32
+  kad_conv3x3_fwd   conv_offset                           -> [N, H_i, W_i, 18] fp32
+  kad_dcn_fwd       DCN + bias, BN, ReLU, branch scale, GAP partials -> z_i (NHWC)
+  kad_se_mlp        channel attention from the GAP partials -> att_i
+
+then one ``kad_branch_merge``: bilinear upsample, x att, concat and + x.
+
+The reference does the same stage split on A100 at batch 1 with Triton, cuDNN
+and one CUDA kernel (acceleration/kadc_fused_parallel.py:74-103,268-286;
+kadc_fused_sm75.py:1400-1488,1544-1557).  Weights are captured when the plan
+is built (as the reference folds BN at patch time, kadc_fused_parallel.py:647-655):
+rebuild it (call enable_fast_inference again) after loading new weights.
+"""
+import torch
+
+from . import _ext
+
+
+def _f32(t):
+    return None if t is None else t.detach().to(torch.float32).contiguous()
+
+
+def _fold_bn(bn):
+    a = bn.weight.detach().double() / torch.sqrt(bn.running_var.detach().double() + bn.eps)
+    b = bn.bias.detach().double() - bn.running_mean.detach().double() * a
+    return a.float().contiguous(), b.float().contiguous()
+
+
+def _lcsa_block(lcsa):
+    """LCSA parameters as the fp32 block kad_lcsa_mask reads:
+    w1[C][11] | b1[C] | bn_a[C] | bn_b[C] | w3[C][11] | b3[C] | w4[9][C] | b4[9]."""
+    ex = lcsa.excite
+    c = ex[0].weight.shape[0]
+    if tuple(ex[0].weight.shape[1:]) != (1, 1, 11) or tuple(ex[3].weight.shape[1:]) != (1, 11, 1):
+        raise NotImplementedError('LCSA kernels are written for band_kernel_size=11')
+    bna, bnb = _fold_bn(ex[1])
+    parts = [ex[0].weight.reshape(c, 11), ex[0].bias, bna, bnb, ex[3].weight.reshape(c, 11), ex[3].bias,
+             ex[4].weight.reshape(9, c), ex[4].bias]
+    blk = torch.cat([p.detach().to(torch.float32).reshape(-1) for p in parts]).contiguous()
+    assert blk.numel() == _ext.lcsa_params_elems(c)
+    return blk
+
+
+class DSCPlan:
+    """Snapshot of one DSC / DCN_RCA (kad_conv.py:42-67; KAD-CNet ops.py:40-72)."""
+
+    def __init__(self, dsc):
+        self.cin, self.cout = dsc.in_channels, dsc.out_channels
+        ks = dsc.kernel_size if isinstance(dsc.kernel_size, int) else dsc.kernel_size[0]
+        if ks != 3:
+            raise NotImplementedError('DSC kernels are 3x3')
+        st = dsc.stride if isinstance(dsc.stride, int) else dsc.stride[0]
+        pad = dsc.padding if isinstance(dsc.padding, int) else dsc.padding[0]
+        self.stride, self.pad = st, pad
+        self.weight = _f32(dsc.weight)
+        self.bias = _f32(dsc.bias)
+        self.off_w = _f32(dsc.conv_offset.weight)
+        self.off_b = _f32(dsc.conv_offset.bias)
+        self.use_mask = bool(getattr(dsc, 'mask', True)) and hasattr(dsc, 'RCA_mask')
+        self.lcsa = _lcsa_block(dsc.RCA_mask) if self.use_mask else None
+        self._packed = {}
+
+    def packed(self, dtype):
+        if dtype not in self._packed:
+            self._packed[dtype] = (_ext.dcn_pack_weights(self.weight, dtype),
+                                   _ext.dcn_pack_weights(self.off_w, dtype))
+        return self._packed[dtype]
+
+    def eligible(self, x):
+        return (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float16, torch.bfloat16)
+                and x.shape[1] == self.cin and self.stride == 1 and self.pad == 1 and x.numel() > 0)
+
+    def run(self, y, n, h, w, out, out_layout, bias=None, post_mul=None, post_add=None, post_scale=None,
+            relu=False, gap=None):
+        """DSC on an NHWC map y [N, h, w, cs] with cin channels; writes `out`."""
+        dev = y.device
+        wp, owp = self.packed(y.dtype)
+        P = h * w
+        mask = None
+        if self.use_mask:
+            rowm = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
+            colm = torch.empty(n, w, self.cin, dtype=torch.float32, device=dev)
+            _ext.axial_means(y, self.cin, rowm, colm)
+            mask = torch.empty(n, h, w, 9, dtype=torch.float32, device=dev)
+            _ext.lcsa_mask(rowm, colm, self.lcsa, mask, n, self.cin, h, w)
+        off = torch.empty(n, h, w, 18, dtype=torch.float32, device=dev)
+        _ext.conv3x3_fwd(y, self.cin, owp, 18, off, bias=self.off_b)
+        _ext.dcn_fwd(y, self.cin, off, (P * 18, 18, 1), mask, (P * 9, 9, 1), wp, self.cout, out,
+                     bias=self.bias if bias is None else bias, post_mul=post_mul, post_add=post_add,
+                     post_scale=post_scale, relu=relu, out_layout=out_layout, gap_partial=gap)
+        return out
+
+    def forward(self, x):
+        """Standalone DSC forward: NCHW (or channels-last) in, same format out."""
+        from .ops import _nhwc_view
+        n, _, h, w = x.shape
+        y, _ = _nhwc_view(x)
+        if x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous():
+            out = torch.empty(n, self.cout, h, w, dtype=x.dtype, device=x.device, memory_format=torch.channels_last)
+            self.run(y, n, h, w, out.permute(0, 2, 3, 1), _ext.KAD_NHWC)
+            return out
+        out = torch.empty(n, self.cout, h, w, dtype=x.dtype, device=x.device)
+        return self.run(y, n, h, w, out, _ext.KAD_NCHW)
+
+
+class _Branch:
+    def __init__(self, conv, fc, scale, c_off):
+        proj, dsc, bn = conv[0], conv[1], conv[2]
+        self.c = proj.weight.shape[0]
+        self.cs = (self.c + 7) // 8 * 8
+        self.c_off = c_off
+        self.proj_w = _f32(proj.weight.reshape(self.c, -1))
+        self.proj_b = _f32(proj.bias)
+        self.dsc = DSCPlan(dsc)
+        self.bn_a, self.bn_b = _fold_bn(bn)
+        self.scale = _f32(scale.weight.reshape(-1))
+        self.w1, self.b1 = _f32(fc[0].weight), _f32(fc[0].bias)
+        self.w2, self.b2 = _f32(fc[2].weight), _f32(fc[2].bias)
+        self.hid = self.w1.shape[0]
+        self._packed = {}
+
+    def proj_packed(self, dtype):
+        if dtype not in self._packed:
+            self._packed[dtype] = _ext.gemm_pack_weights(self.proj_w, dtype)
+        return self._packed[dtype]
+
+
+class KADConvPlan:
+    def __init__(self, layer):
+        self.n = layer.n
+        self.dim = layer.convs[0][0].weight.shape[1]
+        self.branches = []
+        c_off = 0
+        for i in range(self.n):
+            scale = layer.weight[i][0]
+            br = _Branch(layer.convs[i], layer.fc[i], scale, c_off)
+            c_off += br.c
+            self.branches.append(br)
+        if c_off != self.dim:
+            raise ValueError('branch widths do not add up to the layer width')
+        if self.n > _ext.MAX_BRANCHES:
+            raise NotImplementedError(f'at most {_ext.MAX_BRANCHES} branches')
+
+    def eligible(self, x):
+        if not (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+            return False
+        if x.shape[1] != self.dim:
+            return False
+        s = 2 ** (self.n - 1)
+        return x.shape[2] >= s and x.shape[3] >= s
+
+    def forward(self, x):
+        N, C, H, W = x.shape
+        dev, dtype = x.device, x.dtype
+        nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
+        if nhwc:
+            xin, in_layout = x.permute(0, 2, 3, 1), _ext.KAD_NHWC
+            out = torch.empty_like(x, memory_format=torch.channels_last)
+            out_v, out_layout = out.permute(0, 2, 3, 1), _ext.KAD_NHWC
+        else:
+            x = x.contiguous()
+            xin, in_layout = x, _ext.KAD_NCHW
+            out = torch.empty_like(x)
+            out_v, out_layout = out, _ext.KAD_NCHW
+        merged = []
+        for i, br in enumerate(self.branches):
+            s = 2 ** i
+            h, w = H // s, W // s
+            P = h * w
+            y = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
+            _ext.gemm1x1_fwd(xin, in_layout, C, br.proj_packed(dtype), br.c, y, _ext.KAD_NHWC, bias=br.proj_b,
+                             pool=s)
+            z = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
+            tiles = _ext.dcn_tiles(h, w)
+            gap = torch.empty(N, tiles, br.c, dtype=torch.float32, device=dev)
+            br.dsc.run(y, N, h, w, z, _ext.KAD_NHWC, post_mul=br.bn_a, post_add=br.bn_b, post_scale=br.scale,
+                       relu=True, gap=gap)
+            att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
+            _ext.se_mlp(gap, tiles, 1.0 / P, br.w1, br.b1, br.w2, br.b2, att, N, br.c, br.hid)
+            merged.append({'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att})
+        _ext.branch_merge(out_v, out_layout, merged, residual=xin)
+        return out

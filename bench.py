@@ -1,0 +1,244 @@
+"""Benchmark of the KAD-Conv inference hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--no-cpu]
+
+Step = one fused KADConv(256) forward on x [8, 256, 100, 100] fp16 (BASELINE
+config 2's metric shape), inputs resident in HBM, weights random from a seed
+(synthetic; no checkpoint exists offline).  The forward is captured once in a
+HIP graph and replayed (the reference protocol, KAD-CNet/inference/benchmark_s.py:9-25);
+K replays are timed between events after W warm-up replays.
+
+Printed: one JSON line with
+  value / ms_per_step      microseconds per forward (lower is better);
+  roofline                 the dominant kernel (branch-0 DCN) timed alone with
+                           events on its launch stream: algorithmic FLOPs / duration
+                           against the fp16 dense MFMA peak;
+  forward_roofline         BASELINE's derived floor for the whole forward (10.33 us)
+                           over the measured time;
+  cpu_baseline             the oracle's fp32 CPU restatement of the reference forward
+                           (plain PyTorch ops), same shape, on this host's cores;
+  stages                   per-stage event timings of one forward;
+  per_op                   the other BASELINE configs (DSC, KADDown, 1x1+SiLU, SE).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, 'kad-conv_amd'))
+sys.path.insert(0, ROOT)
+
+PEAK_MFMA_F16 = 2516.6e12   # dense fp16/bf16 MFMA, 256 CU x 2.4 GHz x 4096 flop/clk
+PEAK_HBM = 8.0e12
+FORWARD_FLOOR_US = 10.33    # max(MFMA, HBM) floor for KADConv(256) at [8,256,100,100] fp16
+
+
+def _events():
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_graph(fn, steps, warmup):
+    """Capture fn in a graph, replay warmup + steps times, return us per replay."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    a, b = _events()
+    a.record()
+    for _ in range(steps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / steps, g
+
+
+def time_eager(fn, steps, warmup=3):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = _events()
+    a.record()
+    for _ in range(steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / steps
+
+
+def build_kadconv(dim, dtype, seed=0):
+    import kadconv
+    from oracle import kadconv_oracle as O
+    m = kadconv.KADConv(dim)
+    m.load_state_dict(O.make_kadconv_state(dim, seed=seed), strict=False)
+    return m.to('cuda', dtype).eval()
+
+
+def dcn_flops(n, h, w, c):
+    return 2.0 * n * h * w * 9 * c * c
+
+
+def cpu_baseline(shape, runs=5, warmup=2):
+    """The oracle's fp32 restatement of the reference plain-PyTorch forward
+    (oracle/kadconv_oracle.py:kadconv_forward), timed on this host."""
+    from oracle import kadconv_oracle as O
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    sd = O.make_kadconv_state(shape[1])
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(0))
+    ts = []
+    with torch.no_grad():
+        for i in range(warmup + runs):
+            t0 = time.perf_counter()
+            O.kadconv_forward(sd, x)
+            if i >= warmup:
+                ts.append(time.perf_counter() - t0)
+    ts.sort()
+    cpu_model = ''
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                cpu_model = line.split(':', 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {'value': ts[len(ts) // 2] * 1e6, 'unit': 'us', 'cores': torch.get_num_threads(), 'kind': 'port',
+            'sample': f'full workload x{list(shape)} fp32, median of {runs} after {warmup} warm-up runs '
+                      f'(os.cpu_count={os.cpu_count()}, affinity={threads}, cpu="{cpu_model}")'}
+
+
+def per_op(steps, warmup):
+    """The other BASELINE configs, graph-timed (us per call) with their floors."""
+    import kadconv
+    from oracle import kadconv_oracle as O
+    res = {}
+    g = torch.Generator().manual_seed(0)
+    dt = torch.float16
+    # config 2: DSC(C, C) at the neck scales
+    for C, H in [(128, 100), (256, 50), (512, 25)]:
+        d = kadconv.DSC(C, C)
+        d.load_state_dict(O.make_dsc_state(C, C, seed=C, offset_std_px=2.0), strict=False)
+        d = d.to('cuda', dt).eval()
+        kadconv.enable_fast_inference(d)
+        x = torch.randn(8, C, H, H, generator=g).to('cuda', dt)
+        us, _ = time_graph(lambda: d(x), steps, warmup)
+        fl = 8 * H * H * (2 * 9 * C * C + 2 * 9 * 18 * C + 2 * 9 * C + 44 * C)
+        by = 2 * 8 * C * H * H * 2 + 2 * (9 * C * C + 162 * C + 9 * C)
+        floor = max(fl / PEAK_MFMA_F16, by / PEAK_HBM) * 1e6
+        res[f'dsc_{C}x{H}'] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+    # config 3: KADDown [8,256,100,100] -> [8,512,50,50]
+    m = kadconv.KADDown(256, 512)
+    m.load_state_dict(O.make_kaddown_state(256, 512))
+    m = m.to('cuda', dt).eval()
+    x = torch.randn(8, 256, 100, 100, generator=g).to('cuda', dt)
+    us, _ = time_graph(lambda: m(x), steps, warmup)
+    floor = max(6.86e9 / PEAK_MFMA_F16, 61.44e6 / PEAK_HBM) * 1e6
+    res['kaddown_256to512_100'] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+    # config 4a: 1x1 conv + SiLU [16,512,50,50]
+    m = kadconv.Conv1x1SiLU(512, 512)
+    with torch.no_grad():
+        m.conv.weight.normal_(0, 0.02)
+        m.conv.bias.normal_(0, 0.02)
+    m = m.to('cuda', dt).eval()
+    x = torch.randn(16, 512, 50, 50, generator=g).to('cuda', dt)
+    us, _ = time_graph(lambda: m(x), steps, warmup)
+    floor = max(20.97e9 / PEAK_MFMA_F16, 82.44e6 / PEAK_HBM) * 1e6
+    res['conv1x1_silu_512_50'] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+    # config 4b: SE [16,1024,25,25], r=16
+    m = kadconv.SqueezeExcitation(1024, reduction=16).to('cuda', dt).eval()
+    x = torch.randn(16, 1024, 25, 25, generator=g).to('cuda', dt)
+    us, _ = time_graph(lambda: m(x), steps, warmup)
+    floor = 40.96e6 / PEAK_HBM * 1e6
+    res['se_1024_25'] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=200)
+    ap.add_argument('--warmup', type=int, default=20)
+    ap.add_argument('--no-ops', action='store_true', help='skip the per-op table of the other configs')
+    ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one GPU: every GPU box of this build has one MI355X and the KAD-Conv forward '
+              'shards by batch with no exchange; run with --gpus 1', file=sys.stderr)
+        sys.exit(2)
+    import kadconv
+    from kadconv import _ext
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    dtype = torch.float16
+    shape = (8, 256, 100, 100)
+    m = build_kadconv(256, dtype)
+    kadconv.enable_fast_inference(m)
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(0)).to('cuda', dtype)
+    with torch.no_grad():
+        # whole forward, graph-replayed; bracket with synchronize (one rank: no barrier needed)
+        torch.cuda.synchronize()
+        us, _ = time_graph(lambda: m(x), args.steps, args.warmup)
+
+        # dominant kernel alone: branch-0 DCN, events on the stream it is launched on
+        plan = m._kad_plan
+        stages, _ = plan.stages(x)
+        for _, fn in stages:
+            fn()
+        stage_us = {name: round(time_eager(fn, 20), 2) for name, fn in stages}
+        dcn0 = dict(stages)['dcn0']
+        c0 = plan.branches[0].c
+        dcn_us = time_eager(dcn0, args.steps, args.warmup)
+        flops = dcn_flops(shape[0], shape[2], shape[3], c0)
+        achieved = flops / (dcn_us * 1e-6)
+
+    traffic = None
+    tfile = os.path.join(ROOT, 'profiles', 'dcn0_traffic.json')
+    if os.path.exists(tfile):
+        traffic = json.load(open(tfile)).get('bytes_per_launch')
+
+    out = {
+        'metric': 'KAD-Conv fwd us & % roofline at [8,256,100,100] fp16; KAD-CNet-S img/s bs16',
+        'value': round(us, 3),
+        'unit': 'us',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(us / 1e3, 6),
+        'higher_is_better': False,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'f16',
+        'data': 'synthetic: x ~ N(0,1) seed 0; random-init weights by state-dict name (seed 0)',
+        'config': {'workload': 'KADConv(256) forward, x [8,256,100,100] fp16, NCHW, HIP-graph replay',
+                   'batch': 8, 'channels': 256, 'hw': [100, 100], 'branches': 3},
+        'roofline': {'bound': 'mfma', 'achieved': round(achieved / 1e12, 3), 'peak': PEAK_MFMA_F16 / 1e12,
+                     'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_MFMA_F16, 4), 'traffic': traffic,
+                     'kernel': 'dcn_fwd_kernel (branch 0: c=86, 8x100x100)', 'kernel_us': round(dcn_us, 3),
+                     'flops_per_launch': flops},
+        'forward_roofline': {'floor_us': FORWARD_FLOOR_US, 'frac': round(FORWARD_FLOOR_US / us, 4)},
+        'stages_us': stage_us,
+        'kadcnet_s_img_per_s': None,
+    }
+    if not args.no_ops:
+        out['per_op'] = per_op(max(args.steps // 4, 20), 5)
+    if not args.no_cpu:
+        out['cpu_baseline'] = cpu_baseline(shape)
+    else:
+        out['cpu_baseline'] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

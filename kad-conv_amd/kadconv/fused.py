@@ -80,25 +80,33 @@ class DSCPlan:
         return (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float16, torch.bfloat16)
                 and x.shape[1] == self.cin and self.stride == 1 and self.pad == 1 and x.numel() > 0)
 
-    def run(self, y, n, h, w, out, out_layout, bias=None, post_mul=None, post_add=None, post_scale=None,
-            relu=False, gap=None):
-        """DSC on an NHWC map y [N, h, w, cs] with cin channels; writes `out`."""
+    def stages(self, y, n, h, w, out, out_layout, bias=None, post_mul=None, post_add=None, post_scale=None,
+               relu=False, gap=None, tag=''):
+        """DSC on an NHWC map y [N, h, w, cs] (cin channels) as a list of
+        (name, launch) pairs with every buffer allocated up front."""
         dev = y.device
         wp, owp = self.packed(y.dtype)
         P = h * w
+        st = []
         mask = None
         if self.use_mask:
             rowm = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
             colm = torch.empty(n, w, self.cin, dtype=torch.float32, device=dev)
-            _ext.axial_means(y, self.cin, rowm, colm)
             mask = torch.empty(n, h, w, 9, dtype=torch.float32, device=dev)
-            _ext.lcsa_mask(rowm, colm, self.lcsa, mask, n, self.cin, h, w)
+            st.append(('axial_means' + tag, lambda: _ext.axial_means(y, self.cin, rowm, colm)))
+            st.append(('lcsa_mask' + tag, lambda: _ext.lcsa_mask(rowm, colm, self.lcsa, mask, n, self.cin, h, w)))
         off = torch.empty(n, h, w, 18, dtype=torch.float32, device=dev)
-        _ext.conv3x3_fwd(y, self.cin, owp, 18, off, bias=self.off_b)
-        _ext.dcn_fwd(y, self.cin, off, (P * 18, 18, 1), mask, (P * 9, 9, 1), wp, self.cout, out,
-                     bias=self.bias if bias is None else bias, post_mul=post_mul, post_add=post_add,
-                     post_scale=post_scale, relu=relu, out_layout=out_layout, gap_partial=gap)
-        return out
+        st.append(('offset_conv' + tag, lambda: _ext.conv3x3_fwd(y, self.cin, owp, 18, off, bias=self.off_b)))
+        b = self.bias if bias is None else bias
+        st.append(('dcn' + tag, lambda: _ext.dcn_fwd(
+            y, self.cin, off, (P * 18, 18, 1), mask, (P * 9, 9, 1), wp, self.cout, out, bias=b, post_mul=post_mul,
+            post_add=post_add, post_scale=post_scale, relu=relu, out_layout=out_layout, gap_partial=gap)))
+        return st
+
+    def run(self, *args, **kw):
+        for _, fn in self.stages(*args, **kw):
+            fn()
+        return args[4]
 
     def forward(self, x):
         """Standalone DSC forward: NCHW (or channels-last) in, same format out."""
@@ -159,7 +167,8 @@ class KADConvPlan:
         s = 2 ** (self.n - 1)
         return x.shape[2] >= s and x.shape[3] >= s
 
-    def forward(self, x):
+    def stages(self, x):
+        """The fused forward as (name, launch) pairs; returns (stages, out)."""
         N, C, H, W = x.shape
         dev, dtype = x.device, x.dtype
         nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
@@ -172,21 +181,30 @@ class KADConvPlan:
             xin, in_layout = x, _ext.KAD_NCHW
             out = torch.empty_like(x)
             out_v, out_layout = out, _ext.KAD_NCHW
+        st = []
         merged = []
         for i, br in enumerate(self.branches):
             s = 2 ** i
             h, w = H // s, W // s
             P = h * w
             y = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
-            _ext.gemm1x1_fwd(xin, in_layout, C, br.proj_packed(dtype), br.c, y, _ext.KAD_NHWC, bias=br.proj_b,
-                             pool=s)
+            wp = br.proj_packed(dtype)
+            st.append((f'proj{i}', lambda y=y, wp=wp, br=br, s=s: _ext.gemm1x1_fwd(
+                xin, in_layout, C, wp, br.c, y, _ext.KAD_NHWC, bias=br.proj_b, pool=s)))
             z = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
             tiles = _ext.dcn_tiles(h, w)
             gap = torch.empty(N, tiles, br.c, dtype=torch.float32, device=dev)
-            br.dsc.run(y, N, h, w, z, _ext.KAD_NHWC, post_mul=br.bn_a, post_add=br.bn_b, post_scale=br.scale,
-                       relu=True, gap=gap)
+            st += br.dsc.stages(y, N, h, w, z, _ext.KAD_NHWC, post_mul=br.bn_a, post_add=br.bn_b,
+                                post_scale=br.scale, relu=True, gap=gap, tag=str(i))
             att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
-            _ext.se_mlp(gap, tiles, 1.0 / P, br.w1, br.b1, br.w2, br.b2, att, N, br.c, br.hid)
+            st.append((f'se{i}', lambda gap=gap, tiles=tiles, P=P, br=br, att=att: _ext.se_mlp(
+                gap, tiles, 1.0 / P, br.w1, br.b1, br.w2, br.b2, att, N, br.c, br.hid)))
             merged.append({'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att})
-        _ext.branch_merge(out_v, out_layout, merged, residual=xin)
+        st.append(('merge', lambda: _ext.branch_merge(out_v, out_layout, merged, residual=xin)))
+        return st, out
+
+    def forward(self, x):
+        st, out = self.stages(x)
+        for _, fn in st:
+            fn()
         return out

@@ -136,23 +136,74 @@ typedef struct kad_gemm_args {
 int kad_gemm1x1_fwd(const kad_gemm_args *a, void *stream);
 
 /* ------------------------------------------------------------------------ */
+/* One-pass branch pyramid: avg-pool 2^b + 1x1 projection for b = 0..nb-1    */
+/* ------------------------------------------------------------------------ */
+
+/* Tile grid of kad_pyramid_proj (4 x 32 input pixels per tile): the number of
+ * row / column partial-sum slices it writes. */
+int kad_pyramid_tiles(int h, int w, int *ntx, int *nty);
+
+typedef struct kad_pyramid_args {
+  const void *x;            /* NCHW [N][Cin][H][W] or NHWC [N][H][W][x_cs], dtype */
+  int n, cin, h, w, in_layout, x_cs, dtype;
+  int nb;                   /* branches, 1..3; branch b pools by 2^b */
+  int ntx, nty;             /* from kad_pyramid_tiles */
+  const void *wpack[3];     /* kad_gemm_pack_weights(W_b [cout_b][Cin]) */
+  const float *bias[3];     /* [cout_b] or NULL */
+  void *out[3];             /* y_b NHWC [N][H>>b][W>>b][out_cs_b], pad channels written 0 */
+  int cout[3], out_cs[3], out_h[3], out_w[3];
+  float *rowpart[3];        /* [N][ntx][H>>b][cout_b]: sums over each tile's columns (fp32), or NULL */
+  float *colpart[3];        /* [N][nty][W>>b][cout_b]: sums over each tile's rows, or NULL */
+} kad_pyramid_args;
+
+/* y_b = conv1x1_b(avg_pool2d(x, 2^b)) + bias_b for every branch from one read
+ * of x, plus the LCSA axial partial sums of each y_b.  Stands in for
+ * KADConv's per-branch `F.avg_pool2d` + `nn.Conv2d(dim, c, 1)`
+ * (kad_conv.py:101,115; reference kadc_fused_parallel.py:74-103 with
+ * k_avg_pool_pow2, kadc_fused_sm75.py:707-726) and LCSA's pool_h/pool_w
+ * (kad_conv.py:26-27; k_reduce_hconv_bn_relu, kadc_fused_sm75.py:830-888). */
+int kad_pyramid_proj(const kad_pyramid_args *a, void *stream);
+
+/* ------------------------------------------------------------------------ */
 /* LCSA mask                                                                 */
 /* ------------------------------------------------------------------------ */
 
 /* Elements of the fp32 LCSA parameter block for C channels:
- * w1[C][11] | b1[C] | bn_a[C] | bn_b[C] | w3[C][11] | b3[C] | w4[9][C] | b4[9]. */
+ * w1[C][11] | b1[C] | bn_a[C] | bn_b[C] | w3[C][11] | b3[C] | w4[9][C] | b4[9]
+ * (bn_a = gamma / sqrt(var + eps), bn_b = beta - mean * bn_a: eval-mode BN). */
 int64_t kad_lcsa_params_elems(int c);
 
-/* Row means rowm[N][H][C] (over w) and column means colm[N][W][C] (over h) of
- * an NHWC map: LCSA's pool_h / pool_w (kad_conv.py:26-27,39); reference
- * Triton k_reduce_hw / k_reduce_hconv_bn_relu (acceleration/kadc_fused_sm75.py:800-888). */
-int kad_axial_means(const void *x, float *rowm, float *colm, int n, int c, int h, int w, int x_cs, int dtype,
-                    void *stream);
+/* Elements of the packed projection matrix E[16][11][roundup(C, 32)]. */
+int64_t kad_lcsa_emat_elems(int c);
 
-/* mask[N][H][W][9] = sigmoid(LCSA(x)) from the axial means (kad_conv.py:28-39,65);
- * reference k_hconv_bn_relu + k_vconv_pointwise9 (acceleration/kadc_fused_sm75.py:812-1080). */
-int kad_lcsa_mask(const float *rowm, const float *colm, const float *params, float *mask, int n, int c, int h,
-                  int w, void *stream);
+/* Row sums rows[N][H][C] (over w) and column sums cols[N][W][C] (over h) of an
+ * NHWC map, one partial slice each: LCSA's pool_h / pool_w numerators
+ * (kad_conv.py:26-27,39); reference Triton k_reduce_hw / k_reduce_hconv_bn_relu
+ * (acceleration/kadc_fused_sm75.py:800-888).  kad_pyramid_proj produces the
+ * same sums as partial slices for KADConv branches. */
+int kad_axial_sums(const void *x, float *rows, float *cols, int n, int c, int h, int w, int x_cs, int dtype,
+                   void *stream);
+
+/* E[j][k][c] = w4[j][c] * w3[c][k] (j < 9, else 0) and ebias[16] = b4 + w4 . b3:
+ * the 11x1 depthwise conv and the 1x1 projection of LCSA (kad_conv.py:33-35)
+ * fused into one matrix.  emat_dtype KAD_F16 (fp16/bf16 runs) or KAD_F32. */
+int kad_lcsa_pack(const float *params, void *emat, float *ebias, int c, int emat_dtype, void *stream);
+
+/* Axial means from sums given as partial slices rows[N][nrp][H][C],
+ * cols[N][ncp][W][C]: arow[N][H][C] = sum / W, colm[N][W][C] = sum / H
+ * (LCSA's pool_h / pool_w, kad_conv.py:26-27). */
+int kad_lcsa_prep(const float *rows, int nrp, const float *cols, int ncp, float *arow, float *colm, int n, int c,
+                  int h, int w, void *stream);
+
+/* mask[N][H][W][9] = sigmoid(E * u + ebias) with the strip activation
+ * u = relu(bn(a[h] * S(w) + B(w) + b1)) formed from the means and the fp32
+ * parameter block (the separable 1x11 conv, BN and ReLU of kad_conv.py:29-32;
+ * identity of kadc_fused_sm75.py:861-878), then LCSA's 11x1 conv + 1x1
+ * projection + DSC's sigmoid (kad_conv.py:33-35,65) as an MFMA GEMM.  Reference
+ * k_vconv_pointwise9* (acceleration/kadc_fused_sm75.py:905-1080) and the RCA tail
+ * inside the CUDA DCN kernel (kadc_dcn16_kernel.cu:132-157,219-229). */
+int kad_lcsa_mask(const float *arow, const float *colm, const float *params, const void *emat, const float *ebias,
+                  float *mask, int n, int c, int h, int w, int emat_dtype, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Squeeze-excitation                                                        */

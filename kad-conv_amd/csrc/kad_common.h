@@ -47,6 +47,14 @@ __device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + __ex
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ inline int round_up(int a, int b) { return ceil_div(a, b) * b; }
 
+// Raise a kernel's dynamic-LDS limit above the 64 KB default when it needs
+// more (gfx950 has 160 KB per CU).  Host-side attribute, not a stream op.
+template <typename F>
+inline void allow_lds(F* kernel, size_t bytes) {
+  if (bytes > 64 * 1024)
+    (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
 inline int dtype_size(int dtype) {
   return dtype == KAD_F32 ? 4 : 2;
 }

@@ -2,128 +2,246 @@
 //   mask = sigmoid( conv1x1_{C->9}( dwconv_{11x1}( relu(bn( dwconv_{1x11}( mean_w(x)[h] + mean_h(x)[w] ))))))
 // (KAD-Conv/kadconv/kad_conv.py:18-39, 65; twin RCA in KAD-CNet/models/module/ops.py:12-37).
 //
-// The broadcast sum s[h, w] = a[h] + b[w] never exists here.  The 1x11
-// depthwise conv of it is separable (the reference's fast path uses the same
-// identity, acceleration/kadc_fused_sm75.py:861-878):
-//   t[c, h, w] = a[c, h] * S_c(w) + B_c(w) + b1[c],
-//   S_c(w) = sum of the taps that land inside the row, B_c(w) = (w1 * b)(w).
-// So the only full-resolution work is u = relu(bn(t)) (3 ops), the 11-tap
-// vertical conv and the 9 x C projection, done per image column in LDS.
+// Algebra used here (all exact rewrites of the module):
+//  * The 1x11 depthwise conv of the broadcast sum a[h] + b[w] is separable
+//    (the reference's Triton path uses the same identity,
+//    acceleration/kadc_fused_sm75.py:861-878):
+//      t[c,h,w] = a[c,h] * S_c(w) + B_c(w) + b1[c],  S_c(w) = sum of in-row taps,
+//      B_c(w) = sum_k w1[c,k] b[c, w+k-5].
+//    With eval BN folded (bn_a, bn_b):  u[c,h,w] = relu(alpha[c,w] * a[c,h] + beta[c,w]),
+//      alpha = bn_a * S,  beta = bn_a * (B + b1) + bn_b.
+//  * The 11x1 depthwise conv followed by the 1x1 projection is one matrix product
+//      m[j, (h,w)] = b4'[j] + sum_{k,c} E[j,k,c] * u[c, h+k-5, w],
+//      E[j,k,c] = w4[j,c] * w3[c,k],  b4' = b4 + w4 . b3,
+//    i.e. a GEMM with M = 9 (padded to 16), K = 11 * C, N = pixels, run on MFMA
+//    with u staged in LDS per 16 x 16 pixel tile (+5 rows above and below).
 //
-// Two kernels: kad_axial_means reads the NHWC feature map once and writes the
-// row means a[n, h, c] and column means b[n, w, c]; kad_lcsa_mask turns them
-// into the fp32 mask [N, H, W, 9] (pixel-major, sigmoid applied).
+// Kernels: kad_axial_sums (row/column sums of an NHWC map, used when the sums
+// do not come from kad_pyramid_proj), kad_lcsa_pack (E, b4' from the module
+// weights), kad_lcsa_prep (row and column means from partial sums),
+// kad_lcsa_mask (alpha/beta for its columns, u in LDS, the GEMM + sigmoid ->
+// mask [N, H, W, 9] fp32, pixel-major).
 #include "kad_common.h"
 
 namespace kad {
 
-constexpr int AX_THREADS = 256;
+constexpr int BAND = 11;
+constexpr int HALF_BAND = 5;
 
-// grid.x = H + W lines, grid.y = N.  Line l < H is row l (mean over w);
-// otherwise column l - H (mean over h).  Threads stride over channels, so each
-// step reads consecutive channels of one pixel (coalesced in NHWC).
+// ---- axial sums of an NHWC map ---------------------------------------------------------------
+// grid.x = H + W lines, grid.y = N.  Line l < H is row l (sum over w);
+// otherwise column l - H (sum over h).  Threads stride over channels.
 template <typename T>
-__global__ __launch_bounds__(AX_THREADS) void axial_means_kernel(const T* x, float* rowm, float* colm, int c, int h,
-                                                                int w, int cs) {
+__global__ __launch_bounds__(256) void axial_sums_kernel(const T* x, float* rows, float* cols, int c, int h, int w,
+                                                        int cs) {
   const int n = blockIdx.y;
   const int l = blockIdx.x;
   const T* base = x + (int64_t)n * h * w * cs;
   if (l < h) {
-    const float inv = 1.f / (float)w;
-    for (int ch = threadIdx.x; ch < c; ch += AX_THREADS) {
+    for (int ch = threadIdx.x; ch < c; ch += 256) {
       float acc = 0.f;
       const T* p = base + (int64_t)l * w * cs + ch;
       for (int j = 0; j < w; ++j) acc += to_f32(p[(int64_t)j * cs]);
-      rowm[((int64_t)n * h + l) * c + ch] = acc * inv;
+      rows[((int64_t)n * h + l) * c + ch] = acc;
     }
   } else {
     const int col = l - h;
-    const float inv = 1.f / (float)h;
-    for (int ch = threadIdx.x; ch < c; ch += AX_THREADS) {
+    for (int ch = threadIdx.x; ch < c; ch += 256) {
       float acc = 0.f;
       const T* p = base + (int64_t)col * cs + ch;
       for (int i = 0; i < h; ++i) acc += to_f32(p[(int64_t)i * w * cs]);
-      colm[((int64_t)n * w + col) * c + ch] = acc * inv;
+      cols[((int64_t)n * w + col) * c + ch] = acc;
     }
   }
 }
 
-// Parameter block layout (fp32), built once by the host from the LCSA weights:
-//   w1[C][11] | b1[C] | bn_a[C] | bn_b[C] | w3[C][11] | b3[C] | w4[9][C] | b4[9]
-// with bn_a = gamma / sqrt(var + eps), bn_b = beta - mean * bn_a (eval-mode BN).
-struct LcsaParams {
-  const float *w1, *b1, *bna, *bnb, *w3, *b3, *w4, *b4;
-  __device__ LcsaParams(const float* p, int c)
-      : w1(p), b1(p + 11 * c), bna(p + 12 * c), bnb(p + 13 * c), w3(p + 14 * c), b3(p + 25 * c),
-        w4(p + 26 * c), b4(p + 35 * c) {}
-};
+// ---- E and b4' from the module weights -----------------------------------------------------------
+// params (fp32): w1[C][11] | b1[C] | bn_a[C] | bn_b[C] | w3[C][11] | b3[C] | w4[9][C] | b4[9]
+template <typename ET>
+__global__ void lcsa_pack_kernel(const float* params, ET* emat, float* ebias, int c, int cp) {
+  const float* w3 = params + 14 * c;
+  const float* b3 = params + 25 * c;
+  const float* w4 = params + 26 * c;
+  const float* b4 = params + 35 * c;
+  const int total = 16 * BAND * cp;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+    const int ch = i % cp, k = (i / cp) % BAND, j = i / (cp * BAND);
+    const float v = (j < 9 && ch < c) ? w4[j * c + ch] * w3[ch * BAND + k] : 0.f;
+    emat[i] = from_f32<ET>(v);
+  }
+  if (blockIdx.x == 0 && threadIdx.x < 16) {
+    const int j = threadIdx.x;
+    float acc = 0.f;
+    if (j < 9) {
+      acc = b4[j];
+      for (int ch = 0; ch < c; ++ch) acc += w4[j * c + ch] * b3[ch];
+    }
+    ebias[j] = acc;
+  }
+}
 
+// ---- axial means from partial slices -----------------------------------------------------------
+// grid (H + W, N): block l < H reduces row l's slices, else column l - H's.
+__global__ __launch_bounds__(256) void lcsa_prep_kernel(const float* rows, int nrp, const float* cols, int ncp,
+                                                       float* arow, float* colm, int c, int h, int w) {
+  const int n = blockIdx.y, l = blockIdx.x;
+  if (l < h) {
+    const float inv = 1.f / (float)w;
+    for (int ch = threadIdx.x; ch < c; ch += 256) {
+      float s = 0.f;
+      for (int p = 0; p < nrp; ++p) s += rows[(((int64_t)n * nrp + p) * h + l) * c + ch];
+      arow[((int64_t)n * h + l) * c + ch] = s * inv;
+    }
+  } else {
+    const int x = l - h;
+    const float inv = 1.f / (float)h;
+    for (int ch = threadIdx.x; ch < c; ch += 256) {
+      float s = 0.f;
+      for (int p = 0; p < ncp; ++p) s += cols[(((int64_t)n * ncp + p) * w + x) * c + ch];
+      colm[((int64_t)n * w + x) * c + ch] = s * inv;
+    }
+  }
+}
+
+// ---- mask GEMM ------------------------------------------------------------------------------------
+constexpr int LM_TH = 16, LM_TW = 16;                   // output tile
+constexpr int LM_UR = LM_TH + 2 * HALF_BAND;            // u rows staged
 constexpr int LM_THREADS = 256;
-constexpr int BAND = 11;
-constexpr int HALF_BAND = 5;
 
-// grid = (W, N).  One block per image column; rows processed in chunks of hc
-// so that u [(hc + 10) x C] and v [hc x C] fit the dynamic LDS budget.
-__global__ __launch_bounds__(LM_THREADS) void lcsa_mask_kernel(const float* rowm, const float* colm,
-                                                              const float* params, float* mask, int c, int h,
-                                                              int w, int hc) {
-  extern __shared__ float lds[];
-  const int col = blockIdx.x;
-  const int n = blockIdx.y;
-  const LcsaParams prm(params, c);
-  float* sS = lds;             // [C]
-  float* sB = sS + c;          // [C]
-  float* u = sB + c;           // [(hc + 10)][C]
-  float* v = u + (hc + 2 * HALF_BAND) * c;  // [hc][C]
-  const float* bcol = colm + (int64_t)n * w * c;
-  for (int ch = threadIdx.x; ch < c; ch += LM_THREADS) {
-    float S = 0.f, B = 0.f;
+template <typename ET> struct LmCfg { static constexpr int ldu = 40; };  // 32 + 8 halves per (row, col)
+template <> struct LmCfg<float> { static constexpr int ldu = 36; };
+
+// grid (ceil(W/16), ceil(H/16), N).  Wave v computes tile rows 4v..4v+3 (4 MFMA
+// column fragments of 16 pixels each) for all 16 (9 used) mask logits.
+template <typename ET>
+__global__ __launch_bounds__(LM_THREADS) void lcsa_mask_kernel(const float* arow, const float* colm,
+                                                              const float* params, const ET* emat,
+                                                              const float* ebias, float* mask, int c, int h, int w,
+                                                              int cp) {
+  constexpr int LDU = LmCfg<ET>::ldu;
+  __shared__ __align__(16) ET us[LM_UR * LM_TW * LDU];
+  __shared__ __align__(16) ET es[16 * BAND * LDU];                 // E slice [j][k][32 c]
+  __shared__ __align__(16) float s_alpha[LM_TW][32], s_beta[LM_TW][32], s_a[LM_UR][32];
+  const float* w1 = params;
+  const float* b1 = params + 11 * c;
+  const float* bna = params + 12 * c;
+  const float* bnb = params + 13 * c;
+  const int n = blockIdx.z;
+  const int h0 = blockIdx.y * LM_TH, w0 = blockIdx.x * LM_TW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, grp = lane >> 4;
+  const float* colm_n = colm + (int64_t)n * w * c;
+  const float* arow_n = arow + (int64_t)n * h * c;
+  floatx4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = 0; c0 < cp; c0 += 32) {
+    __syncthreads();
+    // E slice for these 32 channels (16 x 11 rows of 32), 8 elements per task
+    for (int e = tid; e < 16 * BAND * 4; e += LM_THREADS) {
+      const int g = e & 3, row = e >> 2;  // row = j * 11 + k
+      const ET* src = emat + (int64_t)row * cp + c0 + g * 8;
+      ET* dst = es + row * LDU + g * 8;
+      if constexpr (sizeof(ET) == 2) {
+        *(uint4*)dst = *(const uint4*)src;
+      } else {
+        ((floatx4*)dst)[0] = ((const floatx4*)src)[0];
+        ((floatx4*)dst)[1] = ((const floatx4*)src)[1];
+      }
+    }
+    // strip-conv coefficients of this block's 16 columns (separable 1x11 conv + folded BN)
+    for (int e = tid; e < LM_TW * 32; e += LM_THREADS) {
+      const int ch = e & 31, col = e >> 5;
+      const int gx = w0 + col, gc = c0 + ch;
+      float al = 0.f, be = 0.f;
+      if (gx < w && gc < c) {
+        float S = 0.f, B = 0.f;
+#pragma unroll
+        for (int k = 0; k < BAND; ++k) {
+          const int xx = gx + k - HALF_BAND;
+          if (xx >= 0 && xx < w) {
+            const float wk = w1[gc * BAND + k];
+            S += wk;
+            B += wk * colm_n[xx * c + gc];
+          }
+        }
+        al = bna[gc] * S;
+        be = bna[gc] * (B + b1[gc]) + bnb[gc];
+      }
+      s_alpha[col][ch] = al;
+      s_beta[col][ch] = be;
+    }
+    for (int e = tid; e < LM_UR * 32; e += LM_THREADS) {
+      const int ch = e & 31, r = e >> 5;
+      const int gy = h0 - HALF_BAND + r, gc = c0 + ch;
+      s_a[r][ch] = (gy >= 0 && gy < h && gc < c) ? arow_n[gy * c + gc] : 0.f;
+    }
+    __syncthreads();
+    // u = relu(alpha * a + beta), 8 channels per task, one 16-byte LDS store
+    for (int e = tid; e < LM_UR * LM_TW * 4; e += LM_THREADS) {
+      const int g = e & 3, q = e >> 2, col = q & (LM_TW - 1), r = q >> 4;
+      const int gy = h0 - HALF_BAND + r;
+      const bool rv = gy >= 0 && gy < h;
+      const floatx4 al0 = *(const floatx4*)&s_alpha[col][g * 8], al1 = *(const floatx4*)&s_alpha[col][g * 8 + 4];
+      const floatx4 be0 = *(const floatx4*)&s_beta[col][g * 8], be1 = *(const floatx4*)&s_beta[col][g * 8 + 4];
+      const floatx4 a0 = *(const floatx4*)&s_a[r][g * 8], a1 = *(const floatx4*)&s_a[r][g * 8 + 4];
+      ET* dst = us + (r * LM_TW + col) * LDU + g * 8;
+      if constexpr (sizeof(ET) == 2) {
+        half8_t v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = (half_t)(rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f);
+          v[j + 4] = (half_t)(rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f);
+        }
+        *(half8_t*)dst = v;
+      } else {
+        floatx4 v0, v1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v0[j] = rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f;
+          v1[j] = rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f;
+        }
+        ((floatx4*)dst)[0] = v0;
+        ((floatx4*)dst)[1] = v1;
+      }
+    }
+    __syncthreads();
 #pragma unroll
     for (int k = 0; k < BAND; ++k) {
-      const int ww = col + k - HALF_BAND;
-      if (ww >= 0 && ww < w) {
-        const float wk = prm.w1[ch * BAND + k];
-        S += wk;
-        B += wk * bcol[(int64_t)ww * c + ch];
-      }
-    }
-    sS[ch] = S;
-    sB[ch] = B + prm.b1[ch];
-  }
-  __syncthreads();
-  const float* arow = rowm + (int64_t)n * h * c;
-  for (int h0 = 0; h0 < h; h0 += hc) {
-    const int rows = (h - h0) < hc ? (h - h0) : hc;
-    const int urows = rows + 2 * HALF_BAND;
-    // u for rows [h0 - 5, h0 + rows + 5); rows outside the image are the vertical conv's zero padding
-    for (int e = threadIdx.x; e < urows * c; e += LM_THREADS) {
-      const int r = e / c, ch = e - (e / c) * c;
-      const int hh = h0 - HALF_BAND + r;
-      float val = 0.f;
-      if (hh >= 0 && hh < h) {
-        const float t = arow[(int64_t)hh * c + ch] * sS[ch] + sB[ch];
-        val = fmaxf(t * prm.bna[ch] + prm.bnb[ch], 0.f);
-      }
-      u[r * c + ch] = val;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < rows * c; e += LM_THREADS) {
-      const int r = e / c, ch = e - (e / c) * c;
-      float acc = prm.b3[ch];
+      const ET* ap = es + (l16 * BAND + k) * LDU + grp * 8;
+      if constexpr (sizeof(ET) == 2) {
+        const half8_t af = *(const half8_t*)ap;
 #pragma unroll
-      for (int k = 0; k < BAND; ++k) acc += prm.w3[ch * BAND + k] * u[(r + k) * c + ch];
-      v[r * c + ch] = acc;
+        for (int f = 0; f < 4; ++f) {
+          const int r = wave * 4 + f;  // tile row of this fragment
+          const half8_t bfr = *(const half8_t*)&us[((r + k) * LM_TW + l16) * LDU + grp * 8];
+          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bfr, acc[f], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float av = ap[j];
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            const int r = wave * 4 + f;
+            acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, us[((r + k) * LM_TW + l16) * LDU + grp * 8 + j],
+                                                          acc[f], 0, 0, 0);
+          }
+        }
+      }
     }
-    __syncthreads();
-    for (int e = threadIdx.x; e < rows * 9; e += LM_THREADS) {
-      const int r = e / 9, j = e - (e / 9) * 9;
-      float acc = prm.b4[j];
-      const float* wj = prm.w4 + j * c;
-      const float* vr = v + r * c;
-      for (int ch = 0; ch < c; ++ch) acc += wj[ch] * vr[ch];
-      mask[(((int64_t)n * h + h0 + r) * w + col) * 9 + j] = sigmoidf_(acc);
+  }
+  // acc[f][i]: logit j = 4 * grp + i of pixel (row 4 * wave + f, col l16)
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    const int gy = h0 + wave * 4 + f, gx = w0 + l16;
+    if (gy >= h || gx >= w) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = grp * 4 + i;
+      if (j < 9) mask[(((int64_t)n * h + gy) * w + gx) * 9 + j] = sigmoidf_(acc[f][i] + ebias[j]);
     }
-    __syncthreads();
   }
 }
 
@@ -133,32 +251,61 @@ using namespace kad;
 
 extern "C" int64_t kad_lcsa_params_elems(int c) { return c > 0 ? 35 * (int64_t)c + 9 : 0; }
 
-extern "C" int kad_axial_means(const void* x, float* rowm, float* colm, int n, int c, int h, int w, int x_cs,
-                               int dtype, void* stream) {
-  KAD_CHECK_ARG(x && rowm && colm, "kad_axial_means: null pointer");
-  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0 && x_cs >= c, "kad_axial_means: bad shape");
+extern "C" int64_t kad_lcsa_emat_elems(int c) { return c > 0 ? (int64_t)16 * BAND * round_up(c, 32) : 0; }
+
+extern "C" int kad_axial_sums(const void* x, float* rows, float* cols, int n, int c, int h, int w, int x_cs,
+                              int dtype, void* stream) {
+  KAD_CHECK_ARG(x && rows && cols, "kad_axial_sums: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0 && x_cs >= c, "kad_axial_sums: bad shape");
   dim3 grid(h + w, n);
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
-    case KAD_F32: hipLaunchKernelGGL(axial_means_kernel<float>, grid, dim3(AX_THREADS), 0, st, (const float*)x, rowm, colm, c, h, w, x_cs); break;
-    case KAD_F16: hipLaunchKernelGGL(axial_means_kernel<half_t>, grid, dim3(AX_THREADS), 0, st, (const half_t*)x, rowm, colm, c, h, w, x_cs); break;
-    case KAD_BF16: hipLaunchKernelGGL(axial_means_kernel<bf16_t>, grid, dim3(AX_THREADS), 0, st, (const bf16_t*)x, rowm, colm, c, h, w, x_cs); break;
-    default: return fail(KAD_EINVAL, "kad_axial_means: unknown dtype %d", dtype);
+    case KAD_F32: hipLaunchKernelGGL(axial_sums_kernel<float>, grid, dim3(256), 0, st, (const float*)x, rows, cols, c, h, w, x_cs); break;
+    case KAD_F16: hipLaunchKernelGGL(axial_sums_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, rows, cols, c, h, w, x_cs); break;
+    case KAD_BF16: hipLaunchKernelGGL(axial_sums_kernel<bf16_t>, grid, dim3(256), 0, st, (const bf16_t*)x, rows, cols, c, h, w, x_cs); break;
+    default: return fail(KAD_EINVAL, "kad_axial_sums: unknown dtype %d", dtype);
   }
-  return check_launch("kad_axial_means");
+  return check_launch("kad_axial_sums");
 }
 
-extern "C" int kad_lcsa_mask(const float* rowm, const float* colm, const float* params, float* mask, int n, int c,
-                             int h, int w, void* stream) {
-  KAD_CHECK_ARG(rowm && colm && params && mask, "kad_lcsa_mask: null pointer");
+extern "C" int kad_lcsa_pack(const float* params, void* emat, float* ebias, int c, int emat_dtype, void* stream) {
+  KAD_CHECK_ARG(params && emat && ebias && c > 0, "kad_lcsa_pack: bad arguments");
+  const int cp = round_up(c, 32);
+  hipStream_t st = (hipStream_t)stream;
+  if (emat_dtype == KAD_F32)
+    hipLaunchKernelGGL(lcsa_pack_kernel<float>, dim3(64), dim3(256), 0, st, params, (float*)emat, ebias, c, cp);
+  else if (emat_dtype == KAD_F16)
+    hipLaunchKernelGGL(lcsa_pack_kernel<half_t>, dim3(64), dim3(256), 0, st, params, (half_t*)emat, ebias, c, cp);
+  else
+    return fail(KAD_EINVAL, "kad_lcsa_pack: emat dtype must be KAD_F32 or KAD_F16");
+  return check_launch("kad_lcsa_pack");
+}
+
+extern "C" int kad_lcsa_prep(const float* rows, int nrp, const float* cols, int ncp, float* arow, float* colm,
+                             int n, int c, int h, int w, void* stream) {
+  KAD_CHECK_ARG(rows && cols && arow && colm, "kad_lcsa_prep: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0 && nrp > 0 && ncp > 0, "kad_lcsa_prep: bad shape");
+  hipLaunchKernelGGL(lcsa_prep_kernel, dim3(h + w, n), dim3(256), 0, (hipStream_t)stream, rows, nrp, cols, ncp,
+                     arow, colm, c, h, w);
+  return check_launch("kad_lcsa_prep");
+}
+
+extern "C" int kad_lcsa_mask(const float* arow, const float* colm, const float* params, const void* emat,
+                             const float* ebias, float* mask, int n, int c, int h, int w, int emat_dtype,
+                             void* stream) {
+  KAD_CHECK_ARG(arow && colm && params && emat && ebias && mask, "kad_lcsa_mask: null pointer");
   KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0, "kad_lcsa_mask: bad shape");
-  // LDS budget 48 KB: (2C + (2 hc + 10) C) floats
-  const int budget = 48 * 1024 / 4;
-  int hc = (budget / c - 2 - 2 * HALF_BAND) / 2;
-  KAD_CHECK_ARG(hc >= 1, "kad_lcsa_mask: C=%d too large for one LDS column", c);
-  if (hc > h) hc = h;
-  const size_t lds = (size_t)(2 * c + (2 * hc + 2 * HALF_BAND) * c) * sizeof(float);
-  hipLaunchKernelGGL(lcsa_mask_kernel, dim3(w, n), dim3(LM_THREADS), lds, (hipStream_t)stream, rowm, colm, params,
-                     mask, c, h, w, hc);
+  KAD_CHECK_ARG(((uintptr_t)emat) % 16 == 0, "kad_lcsa_mask: emat must be 16-byte aligned");
+  const int cp = round_up(c, 32);
+  dim3 grid(ceil_div(w, LM_TW), ceil_div(h, LM_TH), n);
+  hipStream_t st = (hipStream_t)stream;
+  if (emat_dtype == KAD_F32)
+    hipLaunchKernelGGL(lcsa_mask_kernel<float>, grid, dim3(LM_THREADS), 0, st, arow, colm, params,
+                       (const float*)emat, ebias, mask, c, h, w, cp);
+  else if (emat_dtype == KAD_F16)
+    hipLaunchKernelGGL(lcsa_mask_kernel<half_t>, grid, dim3(LM_THREADS), 0, st, arow, colm, params,
+                       (const half_t*)emat, ebias, mask, c, h, w, cp);
+  else
+    return fail(KAD_EINVAL, "kad_lcsa_mask: emat dtype must be KAD_F32 or KAD_F16");
   return check_launch("kad_lcsa_mask");
 }

@@ -1,0 +1,422 @@
+// One-pass branch pyramid for KADConv: the input is read once and every
+// branch's avg-pool + 1x1 projection is computed from the same tile
+// (KAD-Conv/kadconv/kad_conv.py:101,115: y_i = conv1x1_i(avg_pool2d(x, 2^i))),
+// together with the LCSA axial partial sums of every y_i (kad_conv.py:26-27,39).
+//
+// Tile: 4 rows x 32 columns of x (128 px).  Branch b sees (4 >> b) x (32 >> b)
+// pooled pixels of it (floor-mode windows never straddle tiles because tiles are
+// aligned to the largest window, 4).  Per K step of 32 input channels the block
+// stages in LDS: the x slice [128 px][32 ch] (transposed on the way in from
+// NCHW), its 2x2 and 4x4 averages, and the three branches' weight slices; the
+// four waves then run v_mfma_f32_16x16x32 in a 2 x 2 split (pixel halves x
+// column halves).  The epilogue goes through LDS: bias, 16-byte NHWC stores of
+// y_b (pad channels zeroed) and deterministic per-tile row / column sums of the
+// fp32 results, from which kad_lcsa_mask forms the axial means.
+//
+// The reference runs these as separate cuDNN 1x1 convs after separate pooling
+// kernels, one branch per stream (acceleration/kadc_fused_parallel.py:74-103,
+// kadc_fused_sm75.py:707-726) and reduces rows/columns again inside LCSA
+// (kadc_fused_sm75.py:830-888).
+#include "kad_common.h"
+
+namespace kad {
+
+constexpr int PY_TR = 4, PY_TC = 32, PY_TILE = PY_TR * PY_TC;
+constexpr int PY_THREADS = 256;
+
+__device__ __forceinline__ int nbf_sel(const int* nbf, int b) { return b == 0 ? nbf[0] : (b == 1 ? nbf[1] : nbf[2]); }
+__device__ __forceinline__ const void* sel3(const void* const* p, int b) { return b == 0 ? p[0] : (b == 1 ? p[1] : p[2]); }
+
+template <typename T> struct PyLds { static constexpr int lda = 40; };   // 32 + 8 halves (80 B rows)
+template <> struct PyLds<float> { static constexpr int lda = 36; };      // 32 + 4 floats
+
+template <typename T>
+__device__ __forceinline__ floatx4 py_mma(const T* a, const T* b, floatx4 c) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+    return c;
+  } else if constexpr (__is_same(T, half_t)) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8_t*)a, *(const half8_t*)b, c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8_t*)a, *(const bf16x8_t*)b, c, 0, 0, 0);
+  }
+}
+
+// Eight elements of T held in registers as raw bits: one uint4 for 16-bit
+// types, two for fp32 (only .lo used by 16-bit types).
+struct Raw8 { uint4 lo, hi; };
+
+template <typename T>
+__device__ __forceinline__ T raw_get(const Raw8& r, int j) {
+  if constexpr (sizeof(T) == 2) {
+    const unsigned w = j < 2 ? r.lo.x : j < 4 ? r.lo.y : j < 6 ? r.lo.z : r.lo.w;
+    const unsigned short hbits = (unsigned short)((j & 1) ? (w >> 16) : (w & 0xffffu));
+    return __builtin_bit_cast(T, hbits);
+  } else {
+    const uint4& q = j < 4 ? r.lo : r.hi;
+    const int k = j & 3;
+    const unsigned w = k == 0 ? q.x : k == 1 ? q.y : k == 2 ? q.z : q.w;
+    return __builtin_bit_cast(T, w);
+  }
+}
+
+// 8 consecutive elements at p, the first `valid` real, the rest 0.
+template <typename T>
+__device__ __forceinline__ Raw8 load8_raw(const T* p, int valid) {
+  Raw8 r;
+  r.lo = uint4{0u, 0u, 0u, 0u};
+  r.hi = r.lo;
+  const uintptr_t addr = (uintptr_t)p;
+  if constexpr (sizeof(T) == 2) {
+    if (valid == 8 && (addr & 15) == 0) {
+      r.lo = *(const uint4*)p;
+    } else if (valid == 8 && (addr & 7) == 0) {
+      const uint2 a0 = ((const uint2*)p)[0], a1 = ((const uint2*)p)[1];
+      r.lo = uint4{a0.x, a0.y, a1.x, a1.y};
+    } else {
+      unsigned w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const unsigned v = j < valid ? (unsigned)__builtin_bit_cast(unsigned short, p[j]) : 0u;
+        w[j >> 1] |= (j & 1) ? (v << 16) : v;
+      }
+      r.lo = uint4{w[0], w[1], w[2], w[3]};
+    }
+  } else {
+    if (valid == 8 && (addr & 15) == 0) {
+      r.lo = ((const uint4*)p)[0];
+      r.hi = ((const uint4*)p)[1];
+    } else {
+      unsigned w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = j < valid ? __builtin_bit_cast(unsigned, p[j]) : 0u;
+      r.lo = uint4{w[0], w[1], w[2], w[3]};
+      r.hi = uint4{w[4], w[5], w[6], w[7]};
+    }
+  }
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void store8_raw(T* d, const Raw8& r) {
+  *(uint4*)d = r.lo;
+  if constexpr (sizeof(T) == 4) *(uint4*)(d + 4) = r.hi;
+}
+
+template <typename T>
+__device__ __forceinline__ Raw8 load8_full(const T* p) {
+  Raw8 r;
+  r.lo = *(const uint4*)p;
+  if constexpr (sizeof(T) == 4) r.hi = *(const uint4*)(p + 4);
+  else r.hi = uint4{0u, 0u, 0u, 0u};
+  return r;
+}
+
+// HB = MFMA column fragments per wave and branch (columns per block = 32 * HB).
+template <typename T, int HB>
+__global__ __launch_bounds__(PY_THREADS) void pyramid_kernel(kad_pyramid_args a, int cin_pad) {
+  constexpr int LDA = PyLds<T>::lda;
+  constexpr int NB = 32 * HB;              // output columns per branch per block
+  constexpr int BTASKS = 3 * NB * 4;       // 16-byte weight pieces per K step (3 branches)
+  constexpr int BPT = (BTASKS + PY_THREADS - 1) / PY_THREADS;
+  constexpr int OBS = NB + 1;
+  extern __shared__ __align__(16) char smem[];
+  T* xs = (T*)smem;                   // [128][LDA]
+  T* p1 = xs + PY_TILE * LDA;         // [32][LDA]
+  T* p2 = p1 + 32 * LDA;              // [16][LDA] (8 used)
+  T* bs = p2 + 16 * LDA;              // [3][NB][LDA]
+  float* ob = (float*)smem;           // epilogue: [128][OBS]
+
+  const int tx = blockIdx.x, ty = blockIdx.y % a.nty, cy = blockIdx.y / a.nty, n = blockIdx.z;
+  const int r0 = ty * PY_TR, c0 = tx * PY_TC;
+  const int col0 = cy * NB;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wa = wave & 1, wb = wave >> 1;
+  const int row16 = lane & 15, grp = lane >> 4;
+  const int nb = a.nb;
+
+  int ncols[3], nbf[3];
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    int c = (b < nb ? a.out_cs[b] : 0) - col0;   // columns incl. zero pad channels
+    c = c < 0 ? 0 : (c > NB ? NB : c);
+    ncols[b] = c;
+    nbf[b] = ceil_div(c, 16);
+  }
+
+  floatx4 acc0[4][HB], acc1[HB], acc2[HB];
+#pragma unroll
+  for (int j = 0; j < HB; ++j) {
+    acc1[j] = acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc0[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- register-staged prefetch of one K step (x slice + weight slices) ---------------------
+  const T* x = (const T*)a.x;
+  Raw8 xr[2];
+  Raw8 br[BPT];
+  auto load_step = [&](int k0) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int e = tid + t * PY_THREADS;
+      if (a.in_layout == KAD_NCHW) {
+        // lanes run along channels so the transposed LDS writes hit distinct banks
+        const int ch = e & 31, rs = e >> 5, row = rs >> 2, seg = rs & 3;
+        const int gy = r0 + row, gx = c0 + seg * 8, ci = k0 + ch;
+        int valid = (gy < a.h && ci < a.cin) ? a.w - gx : 0;
+        valid = valid < 0 ? 0 : (valid > 8 ? 8 : valid);
+        xr[t] = load8_raw(x + (((int64_t)n * a.cin + ci) * a.h + gy) * a.w + gx, valid);
+      } else {
+        const int px = e >> 2, g = e & 3;
+        const int gy = r0 + (px >> 5), gx = c0 + (px & 31), ci = k0 + g * 8;
+        int valid = (gy < a.h && gx < a.w) ? a.cin - ci : 0;
+        valid = valid < 0 ? 0 : (valid > 8 ? 8 : valid);
+        xr[t] = load8_raw(x + (((int64_t)n * a.h + gy) * a.w + gx) * a.x_cs + ci, valid);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < BPT; ++t) {
+      const int e = tid + t * PY_THREADS;
+      const int b = e / (NB * 4), r = e - b * (NB * 4), cl = r >> 2, g = r & 3;
+      if (e < BTASKS && cl < nbf_sel(nbf, b) * 16) {
+        br[t] = load8_full((const T*)sel3(a.wpack, b) + (int64_t)(col0 + cl) * cin_pad + k0 + g * 8);
+      }
+    }
+  };
+  auto store_step = [&]() {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int e = tid + t * PY_THREADS;
+      if (a.in_layout == KAD_NCHW) {
+        const int ch = e & 31, rs = e >> 5, row = rs >> 2, seg = rs & 3;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xs[(row * PY_TC + seg * 8 + j) * LDA + ch] = raw_get<T>(xr[t], j);
+      } else {
+        const int px = e >> 2, g = e & 3;
+        store8_raw(xs + px * LDA + g * 8, xr[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < BPT; ++t) {
+      const int e = tid + t * PY_THREADS;
+      const int b = e / (NB * 4), r = e - b * (NB * 4), cl = r >> 2, g = r & 3;
+      if (e < BTASKS && cl < nbf_sel(nbf, b) * 16) {
+        store8_raw(bs + (b * NB + cl) * LDA + g * 8, br[t]);
+      }
+    }
+  };
+
+  load_step(0);
+  for (int k0 = 0; k0 < cin_pad; k0 += 32) {
+    __syncthreads();  // the previous step's MFMAs are done with xs / bs
+    store_step();
+    if (k0 + 32 < cin_pad) load_step(k0 + 32);  // in flight while this step computes
+    __syncthreads();
+    // ---- 2x2 and 4x4 averages of the slice ---------------------------------------------------
+    if (nb > 1) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int e = tid + t * PY_THREADS;
+        const int ch = e & 31, q = e >> 5, pr = q >> 4, pc = q & 15;
+        const int b0 = (2 * pr) * PY_TC + 2 * pc;
+        const float sum = to_f32(xs[b0 * LDA + ch]) + to_f32(xs[(b0 + 1) * LDA + ch]) +
+                          to_f32(xs[(b0 + PY_TC) * LDA + ch]) + to_f32(xs[(b0 + PY_TC + 1) * LDA + ch]);
+        p1[q * LDA + ch] = from_f32<T>(0.25f * sum);
+      }
+    }
+    if (nb > 2) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int e = tid + t * PY_THREADS;
+        const int ch = e & 31, pc = e >> 5;
+        float sum = 0.f;
+        if (pc < 8) {
+#pragma unroll
+          for (int dy = 0; dy < 4; ++dy)
+#pragma unroll
+            for (int dx = 0; dx < 4; ++dx) sum += to_f32(xs[(dy * PY_TC + 4 * pc + dx) * LDA + ch]);
+        }
+        p2[pc * LDA + ch] = from_f32<T>(sum * (1.f / 16.f));
+      }
+    }
+    __syncthreads();
+    // ---- MFMA: wave (wa, wb) = pixel half x column half ----------------------------------------
+#pragma unroll
+    for (int bb = 0; bb < HB; ++bb) {
+      const int bf = wb * HB + bb;
+      if (bf < nbf[0]) {
+        const T* bp = bs + (0 * NB + bf * 16 + row16) * LDA + grp * 8;
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm)
+          acc0[mm][bb] = py_mma<T>(xs + ((wa * 4 + mm) * 16 + row16) * LDA + grp * 8, bp, acc0[mm][bb]);
+      }
+      if (bf < nbf[1])
+        acc1[bb] = py_mma<T>(p1 + (wa * 16 + row16) * LDA + grp * 8, bs + (1 * NB + bf * 16 + row16) * LDA + grp * 8,
+                             acc1[bb]);
+      if (wa == 0 && bf < nbf[2])
+        acc2[bb] = py_mma<T>(p2 + row16 * LDA + grp * 8, bs + (2 * NB + bf * 16 + row16) * LDA + grp * 8, acc2[bb]);
+    }
+  }
+
+  // ---- epilogue, one branch at a time through LDS -------------------------------------------------
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    if (ncols[b] == 0) continue;   // uniform across the block
+    const int tr = PY_TR >> b, tc = PY_TC >> b;
+    const int hbch = a.out_h[b], wbch = a.out_w[b];
+    __syncthreads();
+#pragma unroll
+    for (int bb = 0; bb < HB; ++bb) {
+      const int bf = wb * HB + bb;
+      if (bf >= nbf[b]) continue;
+      const int col = bf * 16 + row16;
+      if (b == 0) {
+#pragma unroll
+        for (int mm = 0; mm < 4; ++mm)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ob[((wa * 4 + mm) * 16 + grp * 4 + i) * OBS + col] = acc0[mm][bb][i];
+      } else if (b == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ob[(wa * 16 + grp * 4 + i) * OBS + col] = acc1[bb][i];
+      } else if (wa == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ob[(grp * 4 + i) * OBS + col] = acc2[bb][i];
+      }
+    }
+    __syncthreads();
+    const int cout = a.cout[b];
+    const float* bias = a.bias[b];
+    // y_b: NHWC, 8 channels per 16-byte store, bias added (pad channels stay 0)
+    T* y = (T*)a.out[b];
+    const int g8 = ncols[b] >> 3;
+    {
+      const int g = tid & 15;
+      float bv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int co = col0 + g * 8 + j;
+        bv[j] = (bias && co < cout) ? bias[co] : 0.f;
+      }
+      if (g < g8) {
+        for (int px = tid >> 4; px < tr * tc; px += PY_THREADS / 16) {
+          const int py_ = px / tc;  // tc is a power of two
+          const int gy = ty * tr + py_, gx = tx * tc + (px - py_ * tc);
+          if (gy >= hbch || gx >= wbch) continue;
+          T* d = y + (((int64_t)n * hbch + gy) * wbch + gx) * a.out_cs[b] + col0 + g * 8;
+          if constexpr (sizeof(T) == 2) {
+            typedef T v8 __attribute__((ext_vector_type(8)));
+            v8 vals;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vals[j] = from_f32<T>(ob[px * OBS + g * 8 + j] + bv[j]);
+            *(v8*)d = vals;
+          } else {
+            floatx4 v0, v1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              v0[j] = ob[px * OBS + g * 8 + j] + bv[j];
+              v1[j] = ob[px * OBS + g * 8 + 4 + j] + bv[4 + j];
+            }
+            ((floatx4*)d)[0] = v0;
+            ((floatx4*)d)[1] = v1;
+          }
+        }
+      }
+    }
+    // axial partial sums of (acc + bias) in fp32: rows over this tile's valid columns,
+    // columns over its valid rows
+    const int ncr = cout - col0 < ncols[b] ? cout - col0 : ncols[b];
+    if (a.rowpart[b] && ncr > 0) {
+      const int vc = (wbch - tx * tc) < tc ? (wbch - tx * tc) : tc;  // valid columns in this tile
+      const int vr = (hbch - ty * tr) < tr ? (hbch - ty * tr) : tr;  // valid rows
+      for (int e = tid; e < tr * NB; e += PY_THREADS) {
+        const int cl = e % NB, r = e / NB;
+        if (cl >= ncr || r >= vr) continue;
+        const float bvl = bias ? bias[col0 + cl] : 0.f;
+        float acc = 0.f;
+        for (int cc = 0; cc < vc; ++cc) acc += ob[(r * tc + cc) * OBS + cl];
+        a.rowpart[b][(((int64_t)n * a.ntx + tx) * hbch + ty * tr + r) * cout + col0 + cl] = acc + vc * bvl;
+      }
+      for (int e = tid; e < tc * NB; e += PY_THREADS) {
+        const int cl = e % NB, cc = e / NB;
+        if (cl >= ncr || cc >= vc) continue;
+        const float bvl = bias ? bias[col0 + cl] : 0.f;
+        float acc = 0.f;
+        for (int r = 0; r < vr; ++r) acc += ob[(r * tc + cc) * OBS + cl];
+        a.colpart[b][(((int64_t)n * a.nty + ty) * wbch + tx * tc + cc) * cout + col0 + cl] = acc + vr * bvl;
+      }
+    }
+  }
+}
+
+template <typename T, int HB>
+static size_t pyramid_lds() {
+  const size_t stage = (size_t)(PY_TILE + 32 + 16 + 3 * 32 * HB) * PyLds<T>::lda * sizeof(T);
+  const size_t epi = (size_t)PY_TILE * (32 * HB + 1) * sizeof(float);
+  return stage > epi ? stage : epi;
+}
+
+template <typename T, int HB>
+static void launch_pyramid(const kad_pyramid_args& a, int cin_pad, int maxcols, hipStream_t st) {
+  dim3 grid(a.ntx, a.nty * ceil_div(maxcols, 32 * HB), a.n);
+  const size_t lds = pyramid_lds<T, HB>();
+  allow_lds(pyramid_kernel<T, HB>, lds);
+  hipLaunchKernelGGL((pyramid_kernel<T, HB>), grid, dim3(PY_THREADS), lds, st, a, cin_pad);
+}
+
+template <typename T>
+static int dispatch_pyramid(const kad_pyramid_args& a, int cin_pad, int maxcols, hipStream_t st) {
+  const int hb = ceil_div(ceil_div(maxcols, 16), 2);
+  switch (hb) {
+    case 1: launch_pyramid<T, 1>(a, cin_pad, maxcols, st); break;
+    case 2: launch_pyramid<T, 2>(a, cin_pad, maxcols, st); break;
+    case 3: launch_pyramid<T, 3>(a, cin_pad, maxcols, st); break;
+    default: launch_pyramid<T, 4>(a, cin_pad, maxcols, st); break;
+  }
+  return check_launch("kad_pyramid_proj");
+}
+
+}  // namespace kad
+
+using namespace kad;
+
+extern "C" int kad_pyramid_tiles(int h, int w, int* ntx, int* nty) {
+  KAD_CHECK_ARG(ntx && nty && h > 0 && w > 0, "kad_pyramid_tiles: bad arguments");
+  *ntx = ceil_div(w, PY_TC);
+  *nty = ceil_div(h, PY_TR);
+  return KAD_OK;
+}
+
+extern "C" int kad_pyramid_proj(const kad_pyramid_args* a, void* stream) {
+  KAD_CHECK_ARG(a && a->x, "kad_pyramid_proj: null pointer");
+  KAD_CHECK_ARG(a->nb >= 1 && a->nb <= 3, "kad_pyramid_proj: nb=%d must be 1..3", a->nb);
+  KAD_CHECK_ARG(a->n > 0 && a->cin > 0 && a->h >= (1 << (a->nb - 1)) && a->w >= (1 << (a->nb - 1)),
+                "kad_pyramid_proj: bad shape");
+  KAD_CHECK_ARG(a->in_layout == KAD_NCHW || (a->in_layout == KAD_NHWC && a->x_cs >= a->cin),
+                "kad_pyramid_proj: bad input layout");
+  KAD_CHECK_ARG(a->ntx == ceil_div(a->w, PY_TC) && a->nty == ceil_div(a->h, PY_TR),
+                "kad_pyramid_proj: ntx/nty must come from kad_pyramid_tiles");
+  int maxcols = 0;
+  for (int b = 0; b < a->nb; ++b) {
+    KAD_CHECK_ARG(a->wpack[b] && a->out[b], "kad_pyramid_proj: branch %d has a null pointer", b);
+    KAD_CHECK_ARG(a->cout[b] > 0 && a->out_cs[b] % 8 == 0 && a->out_cs[b] >= a->cout[b] &&
+                      a->out_cs[b] <= round_up(round_up(a->cout[b], 8), 128),
+                  "kad_pyramid_proj: branch %d: out_cs %d must be a multiple of 8 in [cout, roundup128]", b,
+                  a->out_cs[b]);
+    KAD_CHECK_ARG(a->out_h[b] == a->h >> b && a->out_w[b] == a->w >> b, "kad_pyramid_proj: branch %d size", b);
+    KAD_CHECK_ARG((a->rowpart[b] == nullptr) == (a->colpart[b] == nullptr),
+                  "kad_pyramid_proj: rowpart and colpart go together");
+    KAD_CHECK_ARG(((uintptr_t)a->wpack[b] | (uintptr_t)a->out[b]) % 16 == 0,
+                  "kad_pyramid_proj: wpack/out must be 16-byte aligned");
+    maxcols = a->out_cs[b] > maxcols ? a->out_cs[b] : maxcols;
+  }
+  const int cin_pad = round_up(a->cin, 32);
+  hipStream_t st = (hipStream_t)stream;
+  switch (a->dtype) {
+    case KAD_F32: return dispatch_pyramid<float>(*a, cin_pad, maxcols, st);
+    case KAD_F16: return dispatch_pyramid<half_t>(*a, cin_pad, maxcols, st);
+    case KAD_BF16: return dispatch_pyramid<bf16_t>(*a, cin_pad, maxcols, st);
+    default: return fail(KAD_EINVAL, "kad_pyramid_proj: unknown dtype %d", a->dtype);
+  }
+}

@@ -107,43 +107,223 @@ __device__ __forceinline__ void src_index(int dst, int in, int out, float scale,
   l1 = s - (float)i0;
 }
 
+// Per-branch source rows for output row y (same for every column and channel).
+struct RowSrc { int y0, y1; float ly; };
+
+__device__ __forceinline__ RowSrc row_src(const kad_merge_args& a, int b, int y) {
+  RowSrc r;
+  src_index(y, a.br_h[b], a.h, (float)a.br_h[b] / (float)a.h, r.y0, r.y1, r.ly);
+  return r;
+}
+
+constexpr int MG_XS = 64;   // output columns per block (NCHW path)
+constexpr int MG_CH = 16;   // output channels per block (NCHW path)
+constexpr int MG_SX = MG_XS + 2;  // staged source columns per branch row (upsampling only shrinks spans)
+
+// NCHW output.  Block = (64 columns, one row, 16 channels, image).  The source
+// rows of every branch that owns one of the 16 channels are staged in LDS
+// (reads run along channels, the NHWC contiguous axis); outputs are then
+// written along x (the NCHW contiguous axis).  Thread t takes column t & 63 and
+// channels (t >> 6) + 4k, so the column interpolation is computed once per
+// thread and reused for its four channels.
 template <typename T>
-__global__ __launch_bounds__(256) void merge_kernel(kad_merge_args a) {
-  const int64_t total = (int64_t)a.n * a.c * a.h * a.w;
-  for (int64_t i = blockIdx.x * (int64_t)256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    int n, c, y, x;
-    if (a.layout == KAD_NCHW) {
-      x = (int)(i % a.w);
-      y = (int)((i / a.w) % a.h);
-      c = (int)((i / ((int64_t)a.w * a.h)) % a.c);
-      n = (int)(i / ((int64_t)a.w * a.h * a.c));
-    } else {
-      c = (int)(i % a.c);
-      x = (int)((i / a.c) % a.w);
-      y = (int)((i / ((int64_t)a.c * a.w)) % a.h);
-      n = (int)(i / ((int64_t)a.c * a.w * a.h));
+__global__ __launch_bounds__(256) void merge_nchw_kernel(kad_merge_args a) {
+  __shared__ float lds[KAD_MAX_BRANCHES][2][MG_SX][MG_CH + 1];
+  __shared__ float s_scale[KAD_MAX_BRANCHES][MG_CH], s_gate[MG_CH];
+  __shared__ int s_owner[MG_CH];  // bit b set: branch b covers this channel
+  const int tid = threadIdx.x;
+  const int xb = blockIdx.x * MG_XS;
+  const int y = blockIdx.y;
+  const int nch = ceil_div(a.c, MG_CH);
+  const int c0 = (blockIdx.z % nch) * MG_CH;
+  const int n = blockIdx.z / nch;
+  const int xe = (xb + MG_XS < a.w) ? xb + MG_XS : a.w;
+  int sx_lo[KAD_MAX_BRANCHES];
+  float ly[KAD_MAX_BRANCHES];
+  if (tid < MG_CH) {
+    const int c = c0 + tid;
+    int owner = 0;
+#pragma unroll
+    for (int b = 0; b < KAD_MAX_BRANCHES; ++b) {
+      float sc = 0.f;
+      if (b < a.nbranch && c < a.c) {
+        const int cb = c - a.br_c_off[b];
+        if (cb >= 0 && cb < a.br_c[b]) {
+          owner |= 1 << b;
+          sc = a.br_coeff[b] * (a.br_att[b] ? a.br_att[b][(int64_t)n * a.br_c[b] + cb] : 1.f);
+        }
+      }
+      s_scale[b][tid] = sc;
     }
-    float v = 0.f;
-    if (a.residual) v = to_f32(((const T*)a.residual)[i]);
+    s_owner[tid] = owner;
+    s_gate[tid] = (a.gate && c < a.c) ? a.gate[c] : 1.f;
+  }
+#pragma unroll
+  for (int b = 0; b < KAD_MAX_BRANCHES; ++b) {
+    sx_lo[b] = 0;
+    ly[b] = 0.f;
+    if (b >= a.nbranch) continue;
+    const int lo = a.br_c_off[b], hi = a.br_c_off[b] + a.br_c[b];
+    if (hi <= c0 || lo >= c0 + MG_CH) continue;  // branch owns none of these channels
+    const RowSrc r = row_src(a, b, y);
+    ly[b] = r.ly;
+    int x0a, x1a, x0b, x1b;
+    float l;
+    const float sc = (float)a.br_w[b] / (float)a.w;
+    src_index(xb, a.br_w[b], a.w, sc, x0a, x1a, l);
+    src_index(xe - 1, a.br_w[b], a.w, sc, x0b, x1b, l);
+    sx_lo[b] = x0a;
+    const int nsx = x1b - x0a + 1;  // <= MG_SX
+    const T* z = (const T*)a.br_z[b];
+    const int cl = tid & (MG_CH - 1);
+    const int cb = c0 + cl - lo;
+    const bool ok = cb >= 0 && cb < a.br_c[b];
+    const T* zr0 = z + (((int64_t)n * a.br_h[b] + r.y0) * a.br_w[b] + x0a) * a.br_cs[b] + cb;
+    const T* zr1 = z + (((int64_t)n * a.br_h[b] + r.y1) * a.br_w[b] + x0a) * a.br_cs[b] + cb;
+    for (int q = tid >> 4; q < 2 * nsx; q += 256 / MG_CH) {
+      const int rr = q >= nsx ? 1 : 0;
+      const int sx = q - rr * nsx;
+      lds[b][rr][sx][cl] = ok ? to_f32((rr ? zr1 : zr0)[(int64_t)sx * a.br_cs[b]]) : 0.f;
+    }
+  }
+  __syncthreads();
+  const int x = xb + (tid & 63);
+  if (x >= a.w) return;
+  int x0[KAD_MAX_BRANCHES], x1[KAD_MAX_BRANCHES];
+  float lx[KAD_MAX_BRANCHES];
+#pragma unroll
+  for (int b = 0; b < KAD_MAX_BRANCHES; ++b) {
+    x0[b] = x1[b] = 0;
+    lx[b] = 0.f;
+    if (b < a.nbranch) {
+      src_index(x, a.br_w[b], a.w, (float)a.br_w[b] / (float)a.w, x0[b], x1[b], lx[b]);
+      x0[b] -= sx_lo[b];
+      x1[b] -= sx_lo[b];
+    }
+  }
+  const T* res = (const T*)a.residual;
+#pragma unroll
+  for (int k = 0; k < MG_CH / 4; ++k) {
+    const int cl = (tid >> 6) + 4 * k;
+    const int c = c0 + cl;
+    if (c >= a.c) continue;
+    const int64_t oi = (((int64_t)n * a.c + c) * a.h + y) * a.w + x;
+    float v = res ? to_f32(res[oi]) : 0.f;
+    const int owner = s_owner[cl];
+#pragma unroll
+    for (int bb = 0; bb < KAD_MAX_BRANCHES; ++bb) {
+      if (!(owner & (1 << bb))) continue;
+      const float top = lds[bb][0][x0[bb]][cl] + lx[bb] * (lds[bb][0][x1[bb]][cl] - lds[bb][0][x0[bb]][cl]);
+      const float bot = lds[bb][1][x0[bb]][cl] + lx[bb] * (lds[bb][1][x1[bb]][cl] - lds[bb][1][x0[bb]][cl]);
+      v += s_scale[bb][cl] * (top + ly[bb] * (bot - top));
+    }
+    ((T*)a.out)[oi] = from_f32<T>(v * s_gate[cl]);
+  }
+}
+
+// NCHW output, branches with disjoint channel ranges (KADConv's concat).
+// Block = (output row, 32-channel chunk of one branch, image).  The one or two
+// source rows of the chunk are staged in LDS (64-byte channel runs per source
+// pixel), the column interpolation table once per block; outputs and the
+// residual then stream along x.
+template <typename T>
+__global__ __launch_bounds__(256) void merge_rows_kernel(kad_merge_args a) {
+  extern __shared__ __align__(16) float dsm[];
+  const int y = blockIdx.x, chunk = blockIdx.y, n = blockIdx.z;
+  const int tid = threadIdx.x;
+  int b = 0, k = chunk;
+#pragma unroll
+  for (int i = 0; i < KAD_MAX_BRANCHES; ++i) {
+    if (i == b && i < a.nbranch - 1) {
+      const int nc = ceil_div(a.br_c[i], 32);
+      if (k >= nc) {
+        k -= nc;
+        b = i + 1;
+      }
+    }
+  }
+  const int cb0 = k * 32;
+  const int nch = a.br_c[b] - cb0 < 32 ? a.br_c[b] - cb0 : 32;
+  const int cbase = a.br_c_off[b] + cb0;
+  const int bh = a.br_h[b], bw = a.br_w[b], cs = a.br_cs[b];
+  float* zs = dsm;                           // [2][bw][33]
+  float* lxs = zs + 2 * bw * 33;             // [W]
+  int* x0s = (int*)(lxs + a.w);              // [W]
+  int* x1s = x0s + a.w;                      // [W]
+  __shared__ float s_att[32], s_gate[32];
+  RowSrc r = row_src(a, b, y);
+  const T* z = (const T*)a.br_z[b] + (int64_t)n * bh * bw * cs + cb0;
+  {
+    const int cl = tid & 31;
+    for (int q = tid >> 5; q < 2 * bw; q += 8) {
+      const int rr = q >= bw ? 1 : 0;
+      const int sx = q - rr * bw;
+      const int sy = rr ? r.y1 : r.y0;
+      zs[(rr * bw + sx) * 33 + cl] = cl < nch ? to_f32(z[((int64_t)sy * bw + sx) * cs + cl]) : 0.f;
+    }
+  }
+  const float scale = (float)bw / (float)a.w;
+  for (int x = tid; x < a.w; x += 256) {
+    int x0, x1;
+    float lx;
+    src_index(x, bw, a.w, scale, x0, x1, lx);
+    x0s[x] = x0;
+    x1s[x] = x1;
+    lxs[x] = lx;
+  }
+  if (tid < 32) {
+    s_att[tid] = tid < nch ? a.br_coeff[b] * (a.br_att[b] ? a.br_att[b][(int64_t)n * a.br_c[b] + cb0 + tid] : 1.f)
+                           : 0.f;
+    s_gate[tid] = (a.gate && tid < nch) ? a.gate[cbase + tid] : 1.f;
+  }
+  __syncthreads();
+  const T* res = (const T*)a.residual;
+  T* out = (T*)a.out;
+  for (int cl = tid >> 6; cl < nch; cl += 4) {
+    const int64_t rowbase = (((int64_t)n * a.c + cbase + cl) * a.h + y) * a.w;
+    const float at = s_att[cl], gt = s_gate[cl];
+    for (int x = tid & 63; x < a.w; x += 64) {
+      const int x0 = x0s[x], x1 = x1s[x];
+      const float lx = lxs[x];
+      const float t0 = zs[x0 * 33 + cl], t1 = zs[x1 * 33 + cl];
+      const float u0 = zs[(bw + x0) * 33 + cl], u1 = zs[(bw + x1) * 33 + cl];
+      const float top = t0 + lx * (t1 - t0), bot = u0 + lx * (u1 - u0);
+      float v = at * (top + r.ly * (bot - top));
+      if (res) v += to_f32(res[rowbase + x]);
+      out[rowbase + x] = from_f32<T>(v * gt);
+    }
+  }
+}
+
+// NHWC output: block = (one row, image); threads run along channels, so every
+// read (branch maps, residual) and the write are contiguous.
+template <typename T>
+__global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
+  const int y = blockIdx.x, n = blockIdx.y;
+  RowSrc rs[KAD_MAX_BRANCHES];
+  for (int b = 0; b < a.nbranch; ++b) rs[b] = row_src(a, b, y);
+  for (int e = threadIdx.x; e < a.w * a.c; e += 256) {
+    const int c = e % a.c, x = e / a.c;
+    const int64_t oi = (((int64_t)n * a.h + y) * a.w + x) * a.c + c;
+    float v = a.residual ? to_f32(((const T*)a.residual)[oi]) : 0.f;
     for (int b = 0; b < a.nbranch; ++b) {
       const int cb = c - a.br_c_off[b];
       if (cb < 0 || cb >= a.br_c[b]) continue;
-      const int bh = a.br_h[b], bw = a.br_w[b], bcs = a.br_cs[b];
-      const T* z = (const T*)a.br_z[b] + (int64_t)n * bh * bw * bcs + cb;
-      int y0, y1, x0, x1;
-      float ly, lx;
-      src_index(y, bh, a.h, (float)bh / (float)a.h, y0, y1, ly);
-      src_index(x, bw, a.w, (float)bw / (float)a.w, x0, x1, lx);
-      const float v00 = to_f32(z[((int64_t)y0 * bw + x0) * bcs]);
-      const float v01 = to_f32(z[((int64_t)y0 * bw + x1) * bcs]);
-      const float v10 = to_f32(z[((int64_t)y1 * bw + x0) * bcs]);
-      const float v11 = to_f32(z[((int64_t)y1 * bw + x1) * bcs]);
-      float s = (1.f - ly) * ((1.f - lx) * v00 + lx * v01) + ly * ((1.f - lx) * v10 + lx * v11);
+      int x0, x1;
+      float lx;
+      src_index(x, a.br_w[b], a.w, (float)a.br_w[b] / (float)a.w, x0, x1, lx);
+      const T* z = (const T*)a.br_z[b] + (int64_t)n * a.br_h[b] * a.br_w[b] * a.br_cs[b] + cb;
+      const int bw = a.br_w[b], cs = a.br_cs[b];
+      const float v00 = to_f32(z[((int64_t)rs[b].y0 * bw + x0) * cs]);
+      const float v01 = to_f32(z[((int64_t)rs[b].y0 * bw + x1) * cs]);
+      const float v10 = to_f32(z[((int64_t)rs[b].y1 * bw + x0) * cs]);
+      const float v11 = to_f32(z[((int64_t)rs[b].y1 * bw + x1) * cs]);
+      float s = (1.f - rs[b].ly) * ((1.f - lx) * v00 + lx * v01) + rs[b].ly * ((1.f - lx) * v10 + lx * v11);
       if (a.br_att[b]) s *= a.br_att[b][(int64_t)n * a.br_c[b] + cb];
       v += a.br_coeff[b] * s;
     }
     if (a.gate) v *= a.gate[c];
-    ((T*)a.out)[i] = from_f32<T>(v);
+    ((T*)a.out)[oi] = from_f32<T>(v);
   }
 }
 
@@ -254,13 +434,44 @@ extern "C" int kad_branch_merge(const kad_merge_args* a, void* stream) {
                       a->br_h[b] > 0 && a->br_w[b] > 0 && a->br_cs[b] >= a->br_c[b],
                   "kad_branch_merge: branch %d has a bad shape", b);
   }
-  const int64_t total = (int64_t)a->n * a->c * a->h * a->w;
+  for (int b = 0; b < a->nbranch; ++b)
+    KAD_CHECK_ARG(a->br_h[b] <= a->h && a->br_w[b] <= a->w, "kad_branch_merge: branch %d larger than the output", b);
   hipStream_t st = (hipStream_t)stream;
-  switch (a->dtype) {
-    case KAD_F32: hipLaunchKernelGGL(merge_kernel<float>, dim3(grid_for(total)), dim3(256), 0, st, *a); break;
-    case KAD_F16: hipLaunchKernelGGL(merge_kernel<half_t>, dim3(grid_for(total)), dim3(256), 0, st, *a); break;
-    case KAD_BF16: hipLaunchKernelGGL(merge_kernel<bf16_t>, dim3(grid_for(total)), dim3(256), 0, st, *a); break;
-    default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
+  // disjoint, ordered channel ranges covering [0, C): the row kernel (one branch per block)
+  bool disjoint = a->nbranch > 0;
+  int cover = 0, nchunks = 0, maxbw = 0;
+  for (int b = 0; b < a->nbranch; ++b) {
+    disjoint = disjoint && a->br_c_off[b] == cover;
+    cover += a->br_c[b];
+    nchunks += ceil_div(a->br_c[b], 32);
+    maxbw = a->br_w[b] > maxbw ? a->br_w[b] : maxbw;
+  }
+  disjoint = disjoint && cover == a->c;
+  const size_t row_lds = (size_t)2 * maxbw * 33 * 4 + (size_t)3 * a->w * 4;
+  if (a->layout == KAD_NCHW && disjoint && row_lds <= 64 * 1024) {
+    dim3 grid(a->h, nchunks, a->n);
+    switch (a->dtype) {
+      case KAD_F32: hipLaunchKernelGGL(merge_rows_kernel<float>, grid, dim3(256), row_lds, st, *a); break;
+      case KAD_F16: hipLaunchKernelGGL(merge_rows_kernel<half_t>, grid, dim3(256), row_lds, st, *a); break;
+      case KAD_BF16: hipLaunchKernelGGL(merge_rows_kernel<bf16_t>, grid, dim3(256), row_lds, st, *a); break;
+      default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
+    }
+  } else if (a->layout == KAD_NCHW) {
+    dim3 grid(ceil_div(a->w, MG_XS), a->h, a->n * ceil_div(a->c, MG_CH));
+    switch (a->dtype) {
+      case KAD_F32: hipLaunchKernelGGL(merge_nchw_kernel<float>, grid, dim3(256), 0, st, *a); break;
+      case KAD_F16: hipLaunchKernelGGL(merge_nchw_kernel<half_t>, grid, dim3(256), 0, st, *a); break;
+      case KAD_BF16: hipLaunchKernelGGL(merge_nchw_kernel<bf16_t>, grid, dim3(256), 0, st, *a); break;
+      default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
+    }
+  } else {
+    dim3 grid(a->h, a->n);
+    switch (a->dtype) {
+      case KAD_F32: hipLaunchKernelGGL(merge_nhwc_kernel<float>, grid, dim3(256), 0, st, *a); break;
+      case KAD_F16: hipLaunchKernelGGL(merge_nhwc_kernel<half_t>, grid, dim3(256), 0, st, *a); break;
+      case KAD_BF16: hipLaunchKernelGGL(merge_nhwc_kernel<bf16_t>, grid, dim3(256), 0, st, *a); break;
+      default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
+    }
   }
   return check_launch("kad_branch_merge");
 }

@@ -54,6 +54,16 @@ class GemmArgs(ctypes.Structure):
 MAX_BRANCHES = 4
 
 
+class PyramidArgs(ctypes.Structure):
+    _fields_ = [
+        ('x', c_vp), ('n', c_int), ('cin', c_int), ('h', c_int), ('w', c_int), ('in_layout', c_int),
+        ('x_cs', c_int), ('dtype', c_int), ('nb', c_int), ('ntx', c_int), ('nty', c_int),
+        ('wpack', c_vp * 3), ('bias', c_vp * 3), ('out', c_vp * 3),
+        ('cout', c_int * 3), ('out_cs', c_int * 3), ('out_h', c_int * 3), ('out_w', c_int * 3),
+        ('rowpart', c_vp * 3), ('colpart', c_vp * 3),
+    ]
+
+
 class MergeArgs(ctypes.Structure):
     _fields_ = [
         ('out', c_vp), ('residual', c_vp), ('gate', c_vp),
@@ -78,9 +88,14 @@ SIGNATURES = {
     'kad_gemm_wpack_elems': (c_i64, [c_int, c_int]),
     'kad_gemm_pack_weights': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     'kad_gemm1x1_fwd': (c_int, [ctypes.POINTER(GemmArgs), c_vp]),
+    'kad_pyramid_tiles': (c_int, [c_int, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
+    'kad_pyramid_proj': (c_int, [ctypes.POINTER(PyramidArgs), c_vp]),
     'kad_lcsa_params_elems': (c_i64, [c_int]),
-    'kad_axial_means': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
-    'kad_lcsa_mask': (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_lcsa_emat_elems': (c_i64, [c_int]),
+    'kad_axial_sums': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_lcsa_pack': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_vp]),
+    'kad_lcsa_prep': (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_lcsa_mask': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_se_pool_tiles': (c_int, [c_int, c_int, c_int]),
     'kad_se_pool': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_se_mlp': (c_int, [c_vp, c_int, ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
@@ -249,22 +264,75 @@ def gemm1x1_fwd(x, in_layout, cin, wpack, cout, out, out_layout, *, bias=None, p
     return out
 
 
+# ---------------------------------------------------------------------------- pyramid
+def pyramid_tiles(h, w):
+    tx, ty = c_int(), c_int()
+    _check(load().kad_pyramid_tiles(h, w, ctypes.byref(tx), ctypes.byref(ty)), 'kad_pyramid_tiles')
+    return tx.value, ty.value
+
+
+def pyramid_proj(x, in_layout, cin, branches):
+    """branches: list of dicts {wpack, bias (fp32 or None), cout, out (NHWC [N,h_b,w_b,cs]),
+    rowpart (fp32 [N,ntx,h_b,cout] or None), colpart (fp32 [N,nty,w_b,cout] or None)}."""
+    _need_gpu(x)
+    if in_layout == KAD_NCHW:
+        N, C, H, W = x.shape
+        cs = C
+    else:
+        N, H, W, cs = x.shape
+    if not 1 <= len(branches) <= 3:
+        raise ValueError('kad_pyramid_proj takes 1..3 branches')
+    a = PyramidArgs()
+    a.x, a.n, a.cin, a.h, a.w, a.in_layout, a.x_cs = _ptr(x), N, cin, H, W, in_layout, cs
+    a.dtype = kad_dtype(x.dtype)
+    a.nb = len(branches)
+    a.ntx, a.nty = pyramid_tiles(H, W)
+    for i, b in enumerate(branches):
+        out = b['out']
+        _need_gpu(out, b['wpack'], b.get('bias'), b.get('rowpart'), b.get('colpart'))
+        if out.dtype != x.dtype or b['wpack'].dtype != x.dtype:
+            raise TypeError('x, packed weights and outputs must share a dtype')
+        a.wpack[i] = b['wpack'].data_ptr()
+        a.bias[i] = b['bias'].data_ptr() if b.get('bias') is not None else None
+        a.out[i] = out.data_ptr()
+        a.cout[i], a.out_cs[i], a.out_h[i], a.out_w[i] = b['cout'], out.shape[3], out.shape[1], out.shape[2]
+        a.rowpart[i] = b['rowpart'].data_ptr() if b.get('rowpart') is not None else None
+        a.colpart[i] = b['colpart'].data_ptr() if b.get('colpart') is not None else None
+    _check(load().kad_pyramid_proj(ctypes.byref(a), _stream()), 'kad_pyramid_proj')
+
+
 # ---------------------------------------------------------------------------- LCSA
 def lcsa_params_elems(c):
     return load().kad_lcsa_params_elems(c)
 
 
-def axial_means(x_nhwc, c, rowm, colm):
-    _need_gpu(x_nhwc, rowm, colm)
+def lcsa_pack(params, c, emat_dtype):
+    """-> (E [16*11*roundup(c,32)] of emat_dtype (float16 or float32), ebias [16] fp32)."""
+    _need_gpu(params)
+    emat = torch.empty(load().kad_lcsa_emat_elems(c), dtype=emat_dtype, device=params.device)
+    ebias = torch.empty(16, dtype=torch.float32, device=params.device)
+    _check(load().kad_lcsa_pack(_ptr(params), _ptr(emat), _ptr(ebias), c, kad_dtype(emat_dtype), _stream()),
+           'kad_lcsa_pack')
+    return emat, ebias
+
+
+def axial_sums(x_nhwc, c, rows, cols):
+    _need_gpu(x_nhwc, rows, cols)
     N, H, W, cs = x_nhwc.shape
-    _check(load().kad_axial_means(_ptr(x_nhwc), _ptr(rowm), _ptr(colm), N, c, H, W, cs, kad_dtype(x_nhwc.dtype),
-                                  _stream()), 'kad_axial_means')
+    _check(load().kad_axial_sums(_ptr(x_nhwc), _ptr(rows), _ptr(cols), N, c, H, W, cs, kad_dtype(x_nhwc.dtype),
+                                 _stream()), 'kad_axial_sums')
 
 
-def lcsa_mask(rowm, colm, params, mask, n, c, h, w):
-    _need_gpu(rowm, colm, params, mask)
-    _check(load().kad_lcsa_mask(_ptr(rowm), _ptr(colm), _ptr(params), _ptr(mask), n, c, h, w, _stream()),
-           'kad_lcsa_mask')
+def lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, c, h, w):
+    _need_gpu(rows, cols, arow, colm)
+    _check(load().kad_lcsa_prep(_ptr(rows), nrp, _ptr(cols), ncp, _ptr(arow), _ptr(colm), n, c, h, w, _stream()),
+           'kad_lcsa_prep')
+
+
+def lcsa_mask(arow, colm, params, emat, ebias, mask, n, c, h, w):
+    _need_gpu(arow, colm, params, emat, ebias, mask)
+    _check(load().kad_lcsa_mask(_ptr(arow), _ptr(colm), _ptr(params), _ptr(emat), _ptr(ebias), _ptr(mask), n, c,
+                                h, w, kad_dtype(emat.dtype), _stream()), 'kad_lcsa_mask')
 
 
 # ---------------------------------------------------------------------------- SE

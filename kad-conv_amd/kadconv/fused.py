@@ -6,9 +6,10 @@ into the form the kernels want: packed MFMA weights per dtype, eval-mode
 BatchNorm folded into the DCN epilogue, LCSA parameters in one block.  Its
 ``forward`` runs, per branch i (kad_conv.py:112-121):
 
-  kad_gemm1x1_fwd   avg_pool 2^i + 1x1 projection        x (NCHW/NHWC) -> y_i (NHWC)
-  kad_axial_means   LCSA row/column means of y_i
-  kad_lcsa_mask     sigmoid(LCSA) mask                    -> [N, H_i, W_i, 9] fp32
+  kad_pyramid_proj  (once, all branches) avg_pool 2^i + 1x1 projection
+                    x (NCHW/NHWC) -> y_i (NHWC), plus LCSA row/column partial sums
+  kad_lcsa_prep     row means, strip-conv coefficients alpha/beta
+  kad_lcsa_mask     sigmoid(LCSA) mask (MFMA GEMM)        -> [N, H_i, W_i, 9] fp32
   kad_conv3x3_fwd   conv_offset                           -> [N, H_i, W_i, 18] fp32
   kad_dcn_fwd       DCN + bias, BN, ReLU, branch scale, GAP partials -> z_i (NHWC)
   kad_se_mlp        channel attention from the GAP partials -> att_i
@@ -71,9 +72,15 @@ class DSCPlan:
         self._packed = {}
 
     def packed(self, dtype):
+        """(DCN weights, offset-conv weights, LCSA E matrix, LCSA bias) for `dtype`;
+        the LCSA matrix is fp16 for fp16/bf16 runs and fp32 for fp32 runs."""
         if dtype not in self._packed:
+            emat = ebias = None
+            if self.use_mask:
+                emat, ebias = _ext.lcsa_pack(self.lcsa, self.cin,
+                                             torch.float32 if dtype == torch.float32 else torch.float16)
             self._packed[dtype] = (_ext.dcn_pack_weights(self.weight, dtype),
-                                   _ext.dcn_pack_weights(self.off_w, dtype))
+                                   _ext.dcn_pack_weights(self.off_w, dtype), emat, ebias)
         return self._packed[dtype]
 
     def eligible(self, x):
@@ -81,20 +88,29 @@ class DSCPlan:
                 and x.shape[1] == self.cin and self.stride == 1 and self.pad == 1 and x.numel() > 0)
 
     def stages(self, y, n, h, w, out, out_layout, bias=None, post_mul=None, post_add=None, post_scale=None,
-               relu=False, gap=None, tag=''):
+               relu=False, gap=None, tag='', sums=None):
         """DSC on an NHWC map y [N, h, w, cs] (cin channels) as a list of
-        (name, launch) pairs with every buffer allocated up front."""
+        (name, launch) pairs with every buffer allocated up front.  `sums` =
+        (rows, nrp, cols, ncp) axial partial sums of y if already computed."""
         dev = y.device
-        wp, owp = self.packed(y.dtype)
+        wp, owp, emat, ebias = self.packed(y.dtype)
         P = h * w
         st = []
         mask = None
         if self.use_mask:
-            rowm = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
+            if sums is None:
+                rows = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
+                cols = torch.empty(n, w, self.cin, dtype=torch.float32, device=dev)
+                nrp = ncp = 1
+                st.append(('axial_sums' + tag, lambda: _ext.axial_sums(y, self.cin, rows, cols)))
+            else:
+                rows, nrp, cols, ncp = sums
+            arow = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
             colm = torch.empty(n, w, self.cin, dtype=torch.float32, device=dev)
             mask = torch.empty(n, h, w, 9, dtype=torch.float32, device=dev)
-            st.append(('axial_means' + tag, lambda: _ext.axial_means(y, self.cin, rowm, colm)))
-            st.append(('lcsa_mask' + tag, lambda: _ext.lcsa_mask(rowm, colm, self.lcsa, mask, n, self.cin, h, w)))
+            st.append(('lcsa_prep' + tag, lambda: _ext.lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, self.cin, h, w)))
+            st.append(('lcsa_mask' + tag, lambda: _ext.lcsa_mask(arow, colm, self.lcsa, emat, ebias, mask, n,
+                                                                 self.cin, h, w)))
         off = torch.empty(n, h, w, 18, dtype=torch.float32, device=dev)
         st.append(('offset_conv' + tag, lambda: _ext.conv3x3_fwd(y, self.cin, owp, 18, off, bias=self.off_b)))
         b = self.bias if bias is None else bias
@@ -156,8 +172,8 @@ class KADConvPlan:
             self.branches.append(br)
         if c_off != self.dim:
             raise ValueError('branch widths do not add up to the layer width')
-        if self.n > _ext.MAX_BRANCHES:
-            raise NotImplementedError(f'at most {_ext.MAX_BRANCHES} branches')
+        if self.n > 3:
+            raise NotImplementedError('the fused forward covers n <= 3 branches (the paper uses 3)')
 
     def eligible(self, x):
         if not (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float16, torch.bfloat16)):
@@ -183,19 +199,27 @@ class KADConvPlan:
             out_v, out_layout = out, _ext.KAD_NCHW
         st = []
         merged = []
+        ys, sums = [], []
+        pyr = []
+        ntx, nty = _ext.pyramid_tiles(H, W)
         for i, br in enumerate(self.branches):
-            s = 2 ** i
-            h, w = H // s, W // s
-            P = h * w
+            h, w = H >> i, W >> i
             y = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
-            wp = br.proj_packed(dtype)
-            st.append((f'proj{i}', lambda y=y, wp=wp, br=br, s=s: _ext.gemm1x1_fwd(
-                xin, in_layout, C, wp, br.c, y, _ext.KAD_NHWC, bias=br.proj_b, pool=s)))
+            rows = torch.empty(N, ntx, h, br.c, dtype=torch.float32, device=dev)
+            cols = torch.empty(N, nty, w, br.c, dtype=torch.float32, device=dev)
+            ys.append(y)
+            sums.append((rows, ntx, cols, nty))
+            pyr.append({'wpack': br.proj_packed(dtype), 'bias': br.proj_b, 'cout': br.c, 'out': y,
+                        'rowpart': rows, 'colpart': cols})
+        st.append(('pyramid', lambda: _ext.pyramid_proj(xin, in_layout, C, pyr)))
+        for i, br in enumerate(self.branches):
+            h, w = H >> i, W >> i
+            P = h * w
             z = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
             tiles = _ext.dcn_tiles(h, w)
             gap = torch.empty(N, tiles, br.c, dtype=torch.float32, device=dev)
-            st += br.dsc.stages(y, N, h, w, z, _ext.KAD_NHWC, post_mul=br.bn_a, post_add=br.bn_b,
-                                post_scale=br.scale, relu=True, gap=gap, tag=str(i))
+            st += br.dsc.stages(ys[i], N, h, w, z, _ext.KAD_NHWC, post_mul=br.bn_a, post_add=br.bn_b,
+                                post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i])
             att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
             st.append((f'se{i}', lambda gap=gap, tiles=tiles, P=P, br=br, att=att: _ext.se_mlp(
                 gap, tiles, 1.0 / P, br.w1, br.b1, br.w2, br.b2, att, N, br.c, br.hid)))

@@ -80,11 +80,12 @@ static void pick_tile(int ho, int wo, int* th_out, int* tw_out) {
 }
 
 // ---- sample info ----------------------------------------------------------------------------
-// code: bit 31 = slow (corners read from global memory), bit 17 = dy step, bit 16 = dx step,
-// bits 15..0 = region pixel of the top-left corner; slow: bit 30 = dy step, bit 29 = dx step,
-// bits 28..14 = cy0, bits 13..0 = cx0.
-struct Info16 { unsigned code; unsigned w01, w23; };   // weights as 2 x half2 (fp16 / bf16 paths)
-struct Info32 { unsigned code; float w[4]; };            // fp32 path
+// Fast-path record per (tap, pixel): byte offsets of the four corners inside the
+// staged region (16 bits each) and the corner weights.  Samples that are dead
+// (all weights 0) or outside a capped region get zero weights here; the latter
+// are accumulated by a separate pass from global memory (s_slow).
+struct __align__(16) Info16 { unsigned o01, o23; unsigned w01, w23; };  // weights as 2 x half2
+struct __align__(16) Info32 { unsigned o01, o23, pad0, pad1; float w[4]; };
 
 __device__ __forceinline__ unsigned pack_h2(float a, float b) {
   const half2_t h{(half_t)a, (half_t)b};
@@ -95,10 +96,12 @@ template <typename T> struct InfoOf { typedef Info16 type; };
 template <> struct InfoOf<float> { typedef Info32 type; };
 
 template <typename T>
-__device__ __forceinline__ typename InfoOf<T>::type make_info(unsigned code, const float* w) {
+__device__ __forceinline__ typename InfoOf<T>::type make_info(unsigned o01, unsigned o23, const float* w) {
   typename InfoOf<T>::type r;
-  r.code = code;
+  r.o01 = o01;
+  r.o23 = o23;
   if constexpr (sizeof(T) == 4) {
+    r.pad0 = r.pad1 = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.w[i] = w[i];
   } else {
@@ -192,6 +195,31 @@ __device__ __forceinline__ typename DcnFrag<T>::frag zero8() {
   }
 }
 
+// Bilinear geometry of one sample at (py, px) (torchvision's rule): clamped
+// top-left corner, corner steps (0 or 1 per axis) and the four weights times m;
+// all weights 0 for a dead sample.
+__device__ __forceinline__ void sample_geom(float py, float px, float m, int h, int w, int& cy0, int& cx0, int& sy,
+                                            int& sx, float* wt) {
+  cy0 = cx0 = sy = sx = 0;
+  wt[0] = wt[1] = wt[2] = wt[3] = 0.f;
+  if (py > -1.f && py < (float)h && px > -1.f && px < (float)w) {
+    const float fy = floorf(py), fx = floorf(px);
+    const int y0 = (int)fy, x0 = (int)fx, y1 = y0 + 1, x1 = x0 + 1;
+    const float ly = py - fy, lx = px - fx, hy = 1.f - ly, hx = 1.f - lx;
+    const bool vy0 = y0 >= 0, vy1 = y1 <= h - 1, vx0 = x0 >= 0, vx1 = x1 <= w - 1;
+    cy0 = vy0 ? y0 : 0;
+    const int cy1 = vy1 ? y1 : h - 1;
+    cx0 = vx0 ? x0 : 0;
+    const int cx1 = vx1 ? x1 : w - 1;
+    sy = cy1 - cy0;
+    sx = cx1 - cx0;
+    wt[0] = (vy0 && vx0) ? hy * hx * m : 0.f;
+    wt[1] = (vy0 && vx1) ? hy * lx * m : 0.f;
+    wt[2] = (vy1 && vx0) ? ly * hx * m : 0.f;
+    wt[3] = (vy1 && vx1) ? ly * lx * m : 0.f;
+  }
+}
+
 // ---- kernel ------------------------------------------------------------------------------------
 // PLAIN = true computes an ordinary 3x3 convolution (integer taps, no offsets or
 // mask): DSC's offset branch, conv_offset (kad_conv.py:55-56).
@@ -205,7 +233,8 @@ __global__ __launch_bounds__(DCN_THREADS, 2) void dcn_fwd_kernel(kad_dcn_args a,
   static_assert(RCAP * PXS * sizeof(T) >= DCN_NPAIR * 24, "prologue scratch must fit in the region buffer");
   // region [RCAP][PXS] T; during the prologue it holds the raw samples instead
   __shared__ __align__(16) T region[RCAP * PXS];
-  __shared__ Info s_info[DCN_NPAIR];                 // [9][128] per-sample corner address + weights
+  __shared__ Info s_info[DCN_NPAIR];                 // [9][128] per-sample corner offsets + weights
+  __shared__ unsigned char s_slow[DCN_NPAIR];        // [9][128] 1 = sample outside the capped region
   __shared__ int s_box[4];       // ymin, ymax, xmin, xmax (clamped corners of live samples)
   __shared__ int s_reg[5];       // region y0, x0, rows, cols, capped flag
   __shared__ float gap_red[4][NBF * 16];
@@ -234,7 +263,29 @@ __global__ __launch_bounds__(DCN_THREADS, 2) void dcn_fwd_kernel(kad_dcn_args a,
   __syncthreads();
   // ---- 1. samples: clamped corners, weights, bounding box ------------------------------------------
   int bymin = 0x7fffffff, bymax = -1, bxmin = 0x7fffffff, bxmax = -1;
-  for (int q = tid; q < DCN_NPAIR; q += DCN_THREADS) {
+  // offsets and mask of this thread's samples, all loads issued before any use
+  constexpr int PPT = (DCN_NPAIR + DCN_THREADS - 1) / DCN_THREADS;
+  float pre_dy[PPT], pre_dx[PPT], pre_m[PPT];
+#pragma unroll
+  for (int u = 0; u < PPT; ++u) {
+    const int q = tid + u * DCN_THREADS;
+    pre_dy[u] = pre_dx[u] = 0.f;
+    pre_m[u] = 1.f;
+    if (!PLAIN && q < DCN_NPAIR) {
+      const int k = q / DCN_TILE, pl = q - k * DCN_TILE;
+      const int oy = ty0 + pl / g.tw, ox = tx0 + pl - (pl / g.tw) * g.tw;
+      if (pl < g.th * g.tw && oy < g.ho && ox < g.wo) {
+        const int64_t p = oy * g.wo + ox;
+        pre_dy[u] = a.offset[n * a.off_sn + p * a.off_sp + (2 * k) * a.off_sc];
+        pre_dx[u] = a.offset[n * a.off_sn + p * a.off_sp + (2 * k + 1) * a.off_sc];
+        if (a.mask) pre_m[u] = a.mask[n * a.mask_sn + p * a.mask_sp + k * a.mask_sc];
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < PPT; ++u) {
+    const int q = tid + u * DCN_THREADS;
+    if (q >= DCN_NPAIR) break;
     const int k = q / DCN_TILE, pl = q - k * DCN_TILE;
     const int oy = ty0 + pl / g.tw, ox = tx0 + pl - (pl / g.tw) * g.tw;
     float w[4] = {0.f, 0.f, 0.f, 0.f};
@@ -249,28 +300,9 @@ __global__ __launch_bounds__(DCN_THREADS, 2) void dcn_fwd_kernel(kad_dcn_args a,
         w[0] = 1.f;
       }
     } else if (live_px) {
-      const int p = oy * g.wo + ox;
-      const float dy = a.offset[n * a.off_sn + (int64_t)p * a.off_sp + (2 * k) * a.off_sc];
-      const float dx = a.offset[n * a.off_sn + (int64_t)p * a.off_sp + (2 * k + 1) * a.off_sc];
-      const float m = a.mask ? a.mask[n * a.mask_sn + (int64_t)p * a.mask_sp + k * a.mask_sc] : 1.f;
-      const float py = (float)(oy * a.stride - a.pad + ky) + dy;
-      const float px = (float)(ox * a.stride - a.pad + kx) + dx;
-      if (py > -1.f && py < (float)a.h && px > -1.f && px < (float)a.w) {
-        const float fy = floorf(py), fx = floorf(px);
-        const int y0 = (int)fy, x0 = (int)fx, y1 = y0 + 1, x1 = x0 + 1;
-        const float ly = py - fy, lx = px - fx, hy = 1.f - ly, hx = 1.f - lx;
-        const bool vy0 = y0 >= 0, vy1 = y1 <= a.h - 1, vx0 = x0 >= 0, vx1 = x1 <= a.w - 1;
-        cy0 = vy0 ? y0 : 0;
-        const int cy1 = vy1 ? y1 : a.h - 1;
-        cx0 = vx0 ? x0 : 0;
-        const int cx1 = vx1 ? x1 : a.w - 1;
-        sy = cy1 - cy0;  // 0 or 1
-        sx = cx1 - cx0;
-        w[0] = (vy0 && vx0) ? hy * hx * m : 0.f;
-        w[1] = (vy0 && vx1) ? hy * lx * m : 0.f;
-        w[2] = (vy1 && vx0) ? ly * hx * m : 0.f;
-        w[3] = (vy1 && vx1) ? ly * lx * m : 0.f;
-      }
+      const float py = (float)(oy * a.stride - a.pad + ky) + pre_dy[u];
+      const float px = (float)(ox * a.stride - a.pad + kx) + pre_dx[u];
+      sample_geom(py, px, pre_m[u], a.h, a.w, cy0, cx0, sy, sx, w);
     }
     const bool live = w[0] != 0.f || w[1] != 0.f || w[2] != 0.f || w[3] != 0.f;
     if (live) {
@@ -336,23 +368,31 @@ __global__ __launch_bounds__(DCN_THREADS, 2) void dcn_fwd_kernel(kad_dcn_args a,
   __syncthreads();
   const int ry0 = s_reg[0], rx0 = s_reg[1], rh = s_reg[2], rw = s_reg[3];
   const bool block_may_slow = s_reg[4] != 0;
-  // ---- 2. sample info: region-relative corner address (or global coordinates) + weights ------------
+  // ---- 2. sample info: corner byte offsets in the region + weights; slow samples listed apart -------
+  constexpr int PXB = PXS * (int)sizeof(T);          // bytes per region pixel
   for (int q = tid; q < DCN_NPAIR; q += DCN_THREADS) {
     const int yx = raw_yx[q], st = raw_st[q];
     const float4 wv = raw_w[q];
-    const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+    float w[4] = {wv.x, wv.y, wv.z, wv.w};
     const int cy0 = yx >> 15, cx0 = yx & 0x7fff;
     const int sy = st >> 1, sx = st & 1;
-    unsigned code;
     const int ly = cy0 - ry0, lx = cx0 - rx0;
-    if (ly >= 0 && ly + sy < rh && lx >= 0 && lx + sx < rw) {
-      code = (unsigned)(ly * rw + lx) | ((unsigned)sx << 16) | ((unsigned)sy << 17);
-    } else if (w[0] == 0.f && w[1] == 0.f && w[2] == 0.f && w[3] == 0.f) {
-      code = 0;  // dead sample: any in-region address, zero weights
+    const bool dead = w[0] == 0.f && w[1] == 0.f && w[2] == 0.f && w[3] == 0.f;
+    unsigned o01 = 0, o23 = 0;
+    unsigned char slow = 0;
+    if (!dead && ly >= 0 && ly + sy < rh && lx >= 0 && lx + sx < rw) {
+      const unsigned b0 = (unsigned)((ly * rw + lx) * PXB);
+      const unsigned bx = (unsigned)(sx * PXB), by = (unsigned)(sy * rw * PXB);
+      o01 = b0 | ((b0 + bx) << 16);
+      o23 = (b0 + by) | ((b0 + by + bx) << 16);
+    } else if (!dead) {
+      slow = 1;                         // the fast path skips it; the slow pass adds it
+      w[0] = w[1] = w[2] = w[3] = 0.f;
     } else {
-      code = 0x80000000u | ((unsigned)sy << 30) | ((unsigned)sx << 29) | ((unsigned)cy0 << 14) | (unsigned)cx0;
+      w[0] = w[1] = w[2] = w[3] = 0.f;
     }
-    s_info[q] = make_info<T>(code, w);
+    s_info[q] = make_info<T>(o01, o23, w);
+    s_slow[q] = slow;
   }
 
   const T* xb = (const T*)a.x + (int64_t)n * a.h * a.w * a.x_cs;
@@ -367,89 +407,131 @@ __global__ __launch_bounds__(DCN_THREADS, 2) void dcn_fwd_kernel(kad_dcn_args a,
 
   const int rpix = rh * rw;
   const int step = DCN_THREADS / 4;
-  const int st_y = step / rw, st_x = step - (step / rw) * rw;
+  const int ibase = wave * (16 * DCN_WM) + row;      // this lane's pixel slot within a tap row of s_info
+  const T* wrow[NBF];                                // this lane's weight row (output channel) per fragment
+#pragma unroll
+  for (int b = 0; b < NBF; ++b) {
+    const int co = co0 + b * 16 + row;
+    wrow[b] = wp + (int64_t)(co < g.cout_pad ? co : 0) * g.nchunk * 9 * 32 + grp * 8;
+  }
   for (int c = 0; c < g.nchunk; ++c) {
     __syncthreads();  // previous chunk (or the prologue's raw samples) fully consumed
-    // ---- 3a. stage the region slice [rpix][32 ch] ------------------------------------------------
+    // ---- 3a. stage the region slice [rpix][32 ch], four 16-byte loads in flight per thread -------------
     {
       const int gq = tid & 3;
-      const int ch = c * 32 + gq * 8;
-      const bool ch_ok = ch < cin8;
-      int q = tid >> 2;
-      int qy = q / rw, qx = q - (q / rw) * rw;
-      for (; q < rpix; q += step) {
-        frag v = zero8<T>();
-        if (ch_ok) v = ld8<T>(xb + ((int64_t)(ry0 + qy) * a.w + rx0 + qx) * a.x_cs + ch);
-        T* d = region + q * PXS + gq * 8;
-        if constexpr (sizeof(T) == 4) {
-          *(floatx4*)d = v.lo;
-          *(floatx4*)(d + 4) = v.hi;
-        } else {
-          *(frag*)d = v;
+      const int chs = c * 32 + gq * 8;
+      const bool chs_ok = chs < cin8;
+      const float inv_rw = 1.f / (float)rw;
+      for (int base = tid >> 2; base < rpix; base += 4 * step) {
+        frag v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int q = base + u * step;
+          v[u] = zero8<T>();
+          if (q < rpix && chs_ok) {
+            const int qy = (int)(((float)q + 0.5f) * inv_rw);
+            const int qx = q - qy * rw;
+            v[u] = ld8<T>(xb + ((int64_t)(ry0 + qy) * a.w + rx0 + qx) * a.x_cs + chs);
+          }
         }
-        qx += st_x;
-        qy += st_y;
-        if (qx >= rw) {
-          qx -= rw;
-          ++qy;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int q = base + u * step;
+          if (q < rpix) {
+            T* d = region + q * PXS + gq * 8;
+            if constexpr (sizeof(T) == 4) {
+              *(floatx4*)d = v[u].lo;
+              *(floatx4*)(d + 4) = v[u].hi;
+            } else {
+              *(frag*)d = v[u];
+            }
+          }
         }
       }
     }
     __syncthreads();
-    // ---- 3b. nine taps of this chunk (B fragments prefetched one tap ahead) ---------------------------
-    const int ch = c * 32 + grp * 8;
-    const bool ch_ok = ch < cin8;
+    // ---- 3b. nine taps of this chunk: weights and sample records prefetched one tap ahead -----------
+    const bool ch_ok = c * 32 + grp * 8 < cin8;
     frag bf[NBF], bn[NBF];
+    Info ic[DCN_WM], inx[DCN_WM];
 #pragma unroll
-    for (int b = 0; b < NBF; ++b) {
-      const int co = co0 + b * 16 + row;
-      bn[b] = co < g.cout_pad ? ld8<T>(wp + ((int64_t)(co * g.nchunk + c) * 9 + 0) * 32 + grp * 8) : zero8<T>();
-    }
+    for (int b = 0; b < NBF; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9) * 32);
+#pragma unroll
+    for (int m = 0; m < DCN_WM; ++m) inx[m] = s_info[m * 16 + ibase];
 #pragma unroll 1
     for (int k = 0; k < 9; ++k) {
 #pragma unroll
       for (int b = 0; b < NBF; ++b) bf[b] = bn[b];
+#pragma unroll
+      for (int m = 0; m < DCN_WM; ++m) ic[m] = inx[m];
       if (k < 8) {
 #pragma unroll
-        for (int b = 0; b < NBF; ++b) {
-          const int co = co0 + b * 16 + row;
-          bn[b] = co < g.cout_pad ? ld8<T>(wp + ((int64_t)(co * g.nchunk + c) * 9 + k + 1) * 32 + grp * 8)
-                                  : zero8<T>();
-        }
+        for (int b = 0; b < NBF; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9 + k + 1) * 32);
+#pragma unroll
+        for (int m = 0; m < DCN_WM; ++m) inx[m] = s_info[(k + 1) * DCN_TILE + m * 16 + ibase];
       }
+      frag af[DCN_WM];
 #pragma unroll
       for (int m = 0; m < DCN_WM; ++m) {
-        const Info in = s_info[k * DCN_TILE + wave * (16 * DCN_WM) + m * 16 + row];
-        const unsigned code = in.code;
-        // slow samples carry global coordinates in the low bits: read region pixel 0 instead
-        const unsigned fcode = (code & 0x80000000u) ? 0u : code;
-        const int q0 = (int)(fcode & 0xffffu);
-        const int dxs = (fcode >> 16) & 1, dys = (fcode >> 17) & 1;
-        const T* r0 = region + q0 * PXS + grp * 8;
-        frag af;
+        const char* rb = (const char*)region + grp * 8 * (int)sizeof(T);
         if (PLAIN) {
-          af = Ops::blend(ld8<T>(r0), zero8<T>(), zero8<T>(), zero8<T>(), in);
+          af[m] = Ops::blend(ld8<T>((const T*)(rb + (ic[m].o01 & 0xffffu))), zero8<T>(), zero8<T>(), zero8<T>(),
+                             ic[m]);
         } else {
-          const frag v0 = ld8<T>(r0);
-          const frag v1 = ld8<T>(r0 + dxs * PXS);
-          const frag v2 = ld8<T>(r0 + dys * rw * PXS);
-          const frag v3 = ld8<T>(r0 + (dys * rw + dxs) * PXS);
-          af = Ops::blend(v0, v1, v2, v3, in);
+          const frag v0 = ld8<T>((const T*)(rb + (ic[m].o01 & 0xffffu)));
+          const frag v1 = ld8<T>((const T*)(rb + (ic[m].o01 >> 16)));
+          const frag v2 = ld8<T>((const T*)(rb + (ic[m].o23 & 0xffffu)));
+          const frag v3 = ld8<T>((const T*)(rb + (ic[m].o23 >> 16)));
+          af[m] = Ops::blend(v0, v1, v2, v3, ic[m]);
         }
-        if (block_may_slow) {
-          // capped region: a few samples live outside it; read their corners from global memory
-          const bool slow = (code & 0x80000000u) != 0;
-          if (__builtin_amdgcn_ballot_w64(slow) != 0 && slow) {
-            const int cy0 = (int)((code >> 14) & 0x7fffu), cx0 = (int)(code & 0x3fffu);
-            const int sy = (code >> 30) & 1, sx = (code >> 29) & 1;
-            const T* g0 = xb + ((int64_t)cy0 * a.w + cx0) * a.x_cs + (ch_ok ? ch : 0);
-            af = Ops::blend(ld8<T>(g0), ld8<T>(g0 + sx * a.x_cs), ld8<T>(g0 + (int64_t)sy * a.w * a.x_cs),
-                            ld8<T>(g0 + ((int64_t)sy * a.w + sx) * a.x_cs), in);
+        if (!ch_ok) af[m] = zero8<T>();
+      }
+#pragma unroll
+      for (int m = 0; m < DCN_WM; ++m)
+#pragma unroll
+        for (int b = 0; b < NBF; ++b) acc[m][b] = Ops::mma(af[m], bf[b], acc[m][b]);
+    }
+  }
+
+  // ---- 3c. samples outside a capped region: straight from global memory (rare) -----------------------
+  if (block_may_slow) {
+    for (int c = 0; c < g.nchunk; ++c) {
+      const int ch = c * 32 + grp * 8;
+      if (ch >= cin8) continue;  // uniform per lane group; no barrier inside
+#pragma unroll 1
+      for (int k = 0; k < 9; ++k) {
+        frag af[DCN_WM];
+        bool any = false;
+#pragma unroll
+        for (int m = 0; m < DCN_WM; ++m) {
+          const int q = k * DCN_TILE + m * 16 + ibase;
+          af[m] = zero8<T>();
+          if (s_slow[q]) {
+            // recompute the sample's geometry from the offsets (rare path)
+            const int pl = m * 16 + ibase;
+            const int oy = ty0 + pl / g.tw, ox = tx0 + pl - (pl / g.tw) * g.tw;
+            const int64_t p = oy * g.wo + ox;
+            const float dy = a.offset[n * a.off_sn + p * a.off_sp + (2 * k) * a.off_sc];
+            const float dx = a.offset[n * a.off_sn + p * a.off_sp + (2 * k + 1) * a.off_sc];
+            const float mk = a.mask ? a.mask[n * a.mask_sn + p * a.mask_sp + k * a.mask_sc] : 1.f;
+            int cy0, cx0, sy, sx;
+            float w[4];
+            sample_geom((float)(oy * a.stride - a.pad + k / 3) + dy, (float)(ox * a.stride - a.pad + k % 3) + dx, mk,
+                        a.h, a.w, cy0, cx0, sy, sx, w);
+            const typename InfoOf<T>::type in = make_info<T>(0u, 0u, w);
+            const T* g0 = xb + ((int64_t)cy0 * a.w + cx0) * a.x_cs + ch;
+            af[m] = Ops::blend(ld8<T>(g0), ld8<T>(g0 + sx * a.x_cs), ld8<T>(g0 + (int64_t)sy * a.w * a.x_cs),
+                               ld8<T>(g0 + ((int64_t)sy * a.w + sx) * a.x_cs), in);
+            any = true;
           }
         }
-        if (!ch_ok) af = zero8<T>();
+        if (__builtin_amdgcn_ballot_w64(any) == 0) continue;
 #pragma unroll
-        for (int b = 0; b < NBF; ++b) acc[m][b] = Ops::mma(af, bf[b], acc[m][b]);
+        for (int b = 0; b < NBF; ++b) {
+          const frag bw = ld8<T>(wrow[b] + (c * 9 + k) * 32);
+#pragma unroll
+          for (int m = 0; m < DCN_WM; ++m) acc[m][b] = Ops::mma(af[m], bw, acc[m][b]);
+        }
       }
     }
   }

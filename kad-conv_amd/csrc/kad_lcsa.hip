@@ -89,6 +89,7 @@ __global__ __launch_bounds__(256) void lcsa_prep_kernel(const float* rows, int n
     const float inv = 1.f / (float)w;
     for (int ch = threadIdx.x; ch < c; ch += 256) {
       float s = 0.f;
+#pragma unroll 8
       for (int p = 0; p < nrp; ++p) s += rows[(((int64_t)n * nrp + p) * h + l) * c + ch];
       arow[((int64_t)n * h + l) * c + ch] = s * inv;
     }
@@ -97,6 +98,7 @@ __global__ __launch_bounds__(256) void lcsa_prep_kernel(const float* rows, int n
     const float inv = 1.f / (float)h;
     for (int ch = threadIdx.x; ch < c; ch += 256) {
       float s = 0.f;
+#pragma unroll 8
       for (int p = 0; p < ncp; ++p) s += cols[(((int64_t)n * ncp + p) * w + x) * c + ch];
       colm[((int64_t)n * w + x) * c + ch] = s * inv;
     }
@@ -139,6 +141,7 @@ __global__ __launch_bounds__(LM_THREADS) void lcsa_mask_kernel(const float* arow
   for (int c0 = 0; c0 < cp; c0 += 32) {
     __syncthreads();
     // E slice for these 32 channels (16 x 11 rows of 32), 8 elements per task
+#pragma unroll
     for (int e = tid; e < 16 * BAND * 4; e += LM_THREADS) {
       const int g = e & 3, row = e >> 2;  // row = j * 11 + k
       const ET* src = emat + (int64_t)row * cp + c0 + g * 8;
@@ -151,6 +154,7 @@ __global__ __launch_bounds__(LM_THREADS) void lcsa_mask_kernel(const float* arow
       }
     }
     // strip-conv coefficients of this block's 16 columns (separable 1x11 conv + folded BN)
+#pragma unroll
     for (int e = tid; e < LM_TW * 32; e += LM_THREADS) {
       const int ch = e & 31, col = e >> 5;
       const int gx = w0 + col, gc = c0 + ch;
@@ -172,6 +176,7 @@ __global__ __launch_bounds__(LM_THREADS) void lcsa_mask_kernel(const float* arow
       s_alpha[col][ch] = al;
       s_beta[col][ch] = be;
     }
+#pragma unroll
     for (int e = tid; e < LM_UR * 32; e += LM_THREADS) {
       const int ch = e & 31, r = e >> 5;
       const int gy = h0 - HALF_BAND + r, gc = c0 + ch;

@@ -115,7 +115,7 @@ __device__ __forceinline__ Raw8 load8_full(const T* p) {
 
 // HB = MFMA column fragments per wave and branch (columns per block = 32 * HB).
 template <typename T, int HB>
-__global__ __launch_bounds__(PY_THREADS) void pyramid_kernel(kad_pyramid_args a, int cin_pad) {
+__global__ __launch_bounds__(PY_THREADS, 2) void pyramid_kernel(kad_pyramid_args a, int cin_pad) {
   constexpr int LDA = PyLds<T>::lda;
   constexpr int NB = 32 * HB;              // output columns per branch per block
   constexpr int BTASKS = 3 * NB * 4;       // 16-byte weight pieces per K step (3 branches)
@@ -154,36 +154,58 @@ __global__ __launch_bounds__(PY_THREADS) void pyramid_kernel(kad_pyramid_args a,
   }
 
   // ---- register-staged prefetch of one K step (x slice + weight slices) ---------------------
+  // Per-thread source pointers and validity are fixed across K steps; each step
+  // advances them by 32 channels.
   const T* x = (const T*)a.x;
   Raw8 xr[2];
   Raw8 br[BPT];
+  const T* xp[2];
+  int xvalid[2];      // elements of the 8-wide piece inside the image / channel range, before the K offset
+  int xch[2];         // channel (NCHW) or channel-group start (NHWC) relative to k0
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int e = tid + t * PY_THREADS;
+    if (a.in_layout == KAD_NCHW) {
+      // lanes run along channels so the transposed LDS writes hit distinct banks
+      const int ch = e & 31, rs = e >> 5, row = rs >> 2, seg = rs & 3;
+      const int gy = r0 + row, gx = c0 + seg * 8;
+      int valid = gy < a.h ? a.w - gx : 0;
+      xvalid[t] = valid < 0 ? 0 : (valid > 8 ? 8 : valid);
+      xch[t] = ch;
+      xp[t] = x + (((int64_t)n * a.cin + ch) * a.h + (gy < a.h ? gy : 0)) * a.w + gx;
+    } else {
+      const int px = e >> 2, g = e & 3;
+      const int gy = r0 + (px >> 5), gx = c0 + (px & 31);
+      xvalid[t] = (gy < a.h && gx < a.w) ? 8 : 0;
+      xch[t] = g * 8;
+      xp[t] = x + (((int64_t)n * a.h + (gy < a.h ? gy : 0)) * a.w + (gx < a.w ? gx : 0)) * a.x_cs + g * 8;
+    }
+  }
+  const int64_t xstep = a.in_layout == KAD_NCHW ? (int64_t)32 * a.h * a.w : 32;
+  const T* bp_[BPT];
+  bool bok[BPT];
+#pragma unroll
+  for (int t = 0; t < BPT; ++t) {
+    const int e = tid + t * PY_THREADS;
+    const int b = e / (NB * 4), r = e - b * (NB * 4), cl = r >> 2, g = r & 3;
+    bok[t] = e < BTASKS && cl < nbf_sel(nbf, b) * 16;
+    bp_[t] = bok[t] ? (const T*)sel3(a.wpack, b) + (int64_t)(col0 + cl) * cin_pad + g * 8 : nullptr;
+  }
   auto load_step = [&](int k0) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const int e = tid + t * PY_THREADS;
+      int valid;
       if (a.in_layout == KAD_NCHW) {
-        // lanes run along channels so the transposed LDS writes hit distinct banks
-        const int ch = e & 31, rs = e >> 5, row = rs >> 2, seg = rs & 3;
-        const int gy = r0 + row, gx = c0 + seg * 8, ci = k0 + ch;
-        int valid = (gy < a.h && ci < a.cin) ? a.w - gx : 0;
-        valid = valid < 0 ? 0 : (valid > 8 ? 8 : valid);
-        xr[t] = load8_raw(x + (((int64_t)n * a.cin + ci) * a.h + gy) * a.w + gx, valid);
+        valid = (k0 + xch[t] < a.cin) ? xvalid[t] : 0;
       } else {
-        const int px = e >> 2, g = e & 3;
-        const int gy = r0 + (px >> 5), gx = c0 + (px & 31), ci = k0 + g * 8;
-        int valid = (gy < a.h && gx < a.w) ? a.cin - ci : 0;
-        valid = valid < 0 ? 0 : (valid > 8 ? 8 : valid);
-        xr[t] = load8_raw(x + (((int64_t)n * a.h + gy) * a.w + gx) * a.x_cs + ci, valid);
+        const int rem = a.cin - (k0 + xch[t]);
+        valid = xvalid[t] ? (rem < 0 ? 0 : (rem > 8 ? 8 : rem)) : 0;
       }
+      xr[t] = load8_raw(xp[t] + (k0 / 32) * xstep, valid);
     }
 #pragma unroll
-    for (int t = 0; t < BPT; ++t) {
-      const int e = tid + t * PY_THREADS;
-      const int b = e / (NB * 4), r = e - b * (NB * 4), cl = r >> 2, g = r & 3;
-      if (e < BTASKS && cl < nbf_sel(nbf, b) * 16) {
-        br[t] = load8_full((const T*)sel3(a.wpack, b) + (int64_t)(col0 + cl) * cin_pad + k0 + g * 8);
-      }
-    }
+    for (int t = 0; t < BPT; ++t)
+      if (bok[t]) br[t] = load8_full(bp_[t] + k0);
   };
   auto store_step = [&]() {
 #pragma unroll
@@ -215,30 +237,67 @@ __global__ __launch_bounds__(PY_THREADS) void pyramid_kernel(kad_pyramid_args a,
     if (k0 + 32 < cin_pad) load_step(k0 + 32);  // in flight while this step computes
     __syncthreads();
     // ---- 2x2 and 4x4 averages of the slice ---------------------------------------------------
-    if (nb > 1) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int e = tid + t * PY_THREADS;
-        const int ch = e & 31, q = e >> 5, pr = q >> 4, pc = q & 15;
+    if constexpr (sizeof(T) == 2) {
+      // 8 channels per task with 16-byte LDS reads; fp32 sums, one rounding to T
+      if (nb > 1 && tid < 128) {
+        const int g = tid & 3, q = tid >> 2, pr = q >> 4, pc = q & 15;
         const int b0 = (2 * pr) * PY_TC + 2 * pc;
-        const float sum = to_f32(xs[b0 * LDA + ch]) + to_f32(xs[(b0 + 1) * LDA + ch]) +
-                          to_f32(xs[(b0 + PY_TC) * LDA + ch]) + to_f32(xs[(b0 + PY_TC + 1) * LDA + ch]);
-        p1[q * LDA + ch] = from_f32<T>(0.25f * sum);
-      }
-    }
-    if (nb > 2) {
+        typedef T v8 __attribute__((ext_vector_type(8)));
+        const v8 s0 = *(const v8*)&xs[b0 * LDA + g * 8], s1 = *(const v8*)&xs[(b0 + 1) * LDA + g * 8];
+        const v8 s2 = *(const v8*)&xs[(b0 + PY_TC) * LDA + g * 8], s3 = *(const v8*)&xs[(b0 + PY_TC + 1) * LDA + g * 8];
+        v8 o;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int e = tid + t * PY_THREADS;
-        const int ch = e & 31, pc = e >> 5;
-        float sum = 0.f;
+        for (int j = 0; j < 8; ++j)
+          o[j] = from_f32<T>(0.25f * ((to_f32(s0[j]) + to_f32(s1[j])) + (to_f32(s2[j]) + to_f32(s3[j]))));
+        *(v8*)&p1[q * LDA + g * 8] = o;
+      }
+      if (nb > 2 && tid >= 128 && tid < 128 + 64) {
+        const int t2 = tid - 128, g = t2 & 3, pc = t2 >> 2;  // pc 0..15 (8 used)
+        typedef T v8 __attribute__((ext_vector_type(8)));
+        float acc8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc8[j] = 0.f;
         if (pc < 8) {
 #pragma unroll
           for (int dy = 0; dy < 4; ++dy)
 #pragma unroll
-            for (int dx = 0; dx < 4; ++dx) sum += to_f32(xs[(dy * PY_TC + 4 * pc + dx) * LDA + ch]);
+            for (int dx = 0; dx < 4; ++dx) {
+              const v8 sv = *(const v8*)&xs[(dy * PY_TC + 4 * pc + dx) * LDA + g * 8];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) acc8[j] += to_f32(sv[j]);
+            }
         }
-        p2[pc * LDA + ch] = from_f32<T>(sum * (1.f / 16.f));
+        v8 o;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = from_f32<T>(acc8[j] * (1.f / 16.f));
+        *(v8*)&p2[pc * LDA + g * 8] = o;
+      }
+    } else {
+      if (nb > 1) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int e = tid + t * PY_THREADS;
+          const int ch = e & 31, q = e >> 5, pr = q >> 4, pc = q & 15;
+          const int b0 = (2 * pr) * PY_TC + 2 * pc;
+          const float sum = to_f32(xs[b0 * LDA + ch]) + to_f32(xs[(b0 + 1) * LDA + ch]) +
+                            to_f32(xs[(b0 + PY_TC) * LDA + ch]) + to_f32(xs[(b0 + PY_TC + 1) * LDA + ch]);
+          p1[q * LDA + ch] = from_f32<T>(0.25f * sum);
+        }
+      }
+      if (nb > 2) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int e = tid + t * PY_THREADS;
+          const int ch = e & 31, pc = e >> 5;
+          float sum = 0.f;
+          if (pc < 8) {
+#pragma unroll
+            for (int dy = 0; dy < 4; ++dy)
+#pragma unroll
+              for (int dx = 0; dx < 4; ++dx) sum += to_f32(xs[(dy * PY_TC + 4 * pc + dx) * LDA + ch]);
+          }
+          p2[pc * LDA + ch] = from_f32<T>(sum * (1.f / 16.f));
+        }
       }
     }
     __syncthreads();

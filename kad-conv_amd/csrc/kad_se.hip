@@ -56,6 +56,7 @@ __global__ __launch_bounds__(256) void se_mlp_kernel(const float* partial, int t
   const int n = blockIdx.x;
   for (int ch = threadIdx.x; ch < c; ch += 256) {
     float acc = 0.f;
+#pragma unroll 8
     for (int t = 0; t < tiles; ++t) acc += partial[((int64_t)n * tiles + t) * c + ch];
     g[ch] = acc * inv_count;
   }
@@ -63,6 +64,7 @@ __global__ __launch_bounds__(256) void se_mlp_kernel(const float* partial, int t
   for (int j = threadIdx.x; j < hid; j += 256) {
     float acc = b1 ? b1[j] : 0.f;
     const float* wr = w1 + (int64_t)j * c;
+#pragma unroll 8
     for (int ch = 0; ch < c; ++ch) acc += wr[ch] * g[ch];
     hbuf[j] = fmaxf(acc, 0.f);
   }
@@ -70,6 +72,7 @@ __global__ __launch_bounds__(256) void se_mlp_kernel(const float* partial, int t
   for (int ch = threadIdx.x; ch < c; ch += 256) {
     float acc = b2 ? b2[ch] : 0.f;
     const float* wr = w2 + (int64_t)ch * hid;
+#pragma unroll 8
     for (int j = 0; j < hid; ++j) acc += wr[j] * hbuf[j];
     att[(int64_t)n * c + ch] = sigmoidf_(acc);
   }
@@ -222,13 +225,15 @@ __global__ __launch_bounds__(256) void merge_nchw_kernel(kad_merge_args a) {
 }
 
 // NCHW output, branches with disjoint channel ranges (KADConv's concat).
-// Block = (output row, 32-channel chunk of one branch, image).  The one or two
-// source rows of the chunk are staged in LDS (64-byte channel runs per source
-// pixel), the column interpolation table once per block; outputs and the
-// residual then stream along x.
+// Block = (output row, 32-channel chunk of one branch, image).  Every global
+// load of the block is issued in one round: the chunk's one or two source rows
+// of the branch map (16-byte pieces of 8 channels, NHWC) and its 32 residual
+// rows (8-byte pieces) go to LDS; the outputs are then formed four columns per
+// task and written with 8-byte stores.
 template <typename T>
 __global__ __launch_bounds__(256) void merge_rows_kernel(kad_merge_args a) {
-  extern __shared__ __align__(16) float dsm[];
+  extern __shared__ __align__(16) char dsm[];
+  constexpr int ZS = 40;                     // T per staged source pixel (32 channels + 8 pad)
   const int y = blockIdx.x, chunk = blockIdx.y, n = blockIdx.z;
   const int tid = threadIdx.x;
   int b = 0, k = chunk;
@@ -246,30 +251,74 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(kad_merge_args a) {
   const int nch = a.br_c[b] - cb0 < 32 ? a.br_c[b] - cb0 : 32;
   const int cbase = a.br_c_off[b] + cb0;
   const int bh = a.br_h[b], bw = a.br_w[b], cs = a.br_cs[b];
-  float* zs = dsm;                           // [2][bw][33]
-  float* lxs = zs + 2 * bw * 33;             // [W]
-  int* x0s = (int*)(lxs + a.w);              // [W]
-  int* x1s = x0s + a.w;                      // [W]
+  const int W = a.w;
+  const int W4 = ceil_div(W, 4);
+  T* zs = (T*)dsm;                           // [2][bw][ZS]
+  T* rs = zs + 2 * bw * ZS;                  // [32][W4 * 4]
   __shared__ float s_att[32], s_gate[32];
-  RowSrc r = row_src(a, b, y);
+  const RowSrc r = row_src(a, b, y);
+  const int nrow = (bh == a.h) ? 1 : 2;
   const T* z = (const T*)a.br_z[b] + (int64_t)n * bh * bw * cs + cb0;
-  {
-    const int cl = tid & 31;
-    for (int q = tid >> 5; q < 2 * bw; q += 8) {
-      const int rr = q >= bw ? 1 : 0;
-      const int sx = q - rr * bw;
-      const int sy = rr ? r.y1 : r.y0;
-      zs[(rr * bw + sx) * 33 + cl] = cl < nch ? to_f32(z[((int64_t)sy * bw + sx) * cs + cl]) : 0.f;
+  const T* res = (const T*)a.residual;
+  const int npiece = ceil_div(nch, 8);       // 8-channel pieces that hold real channels
+  const int zt = nrow * bw * 4;              // 16-byte source pieces (4 per pixel)
+  const int rt = res ? nch * W4 : 0;         // 4-element residual pieces
+  const int64_t rbase = (((int64_t)n * a.c + cbase) * a.h + y) * W;
+  // one round of loads: up to 8 per thread in flight
+  for (int e0 = tid; e0 < zt + rt; e0 += 8 * 256) {
+    uint4 zv[8];
+    uint2 rv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * 256;
+      zv[u] = uint4{0u, 0u, 0u, 0u};
+      rv[u] = uint2{0u, 0u};
+      if (e < zt) {
+        const int g = e & 3, q = e >> 2, rr = q >= bw ? 1 : 0, sx = q - rr * bw;
+        if (g < npiece) {
+          const T* src = z + ((int64_t)(rr ? r.y1 : r.y0) * bw + sx) * cs + g * 8;
+          if constexpr (sizeof(T) == 2) zv[u] = *(const uint4*)src;
+          else zv[u] = uint4{0u, 0u, 0u, 0u};  // fp32 path loads below
+        }
+      } else if (e < zt + rt) {
+        const int f = e - zt, cl = f / W4, x4 = (f - cl * W4) * 4;
+        const T* src = res + rbase + (int64_t)cl * a.h * W + x4;
+        if constexpr (sizeof(T) == 2) {
+          if (x4 + 4 <= W && ((uintptr_t)src & 7) == 0) {
+            rv[u] = *(const uint2*)src;
+          } else {
+            unsigned short hv[4] = {0, 0, 0, 0};
+            for (int j = 0; j < 4; ++j)
+              if (x4 + j < W) hv[j] = __builtin_bit_cast(unsigned short, src[j]);
+            rv[u] = uint2{hv[0] | ((unsigned)hv[1] << 16), hv[2] | ((unsigned)hv[3] << 16)};
+          }
+        }
+      }
     }
-  }
-  const float scale = (float)bw / (float)a.w;
-  for (int x = tid; x < a.w; x += 256) {
-    int x0, x1;
-    float lx;
-    src_index(x, bw, a.w, scale, x0, x1, lx);
-    x0s[x] = x0;
-    x1s[x] = x1;
-    lxs[x] = lx;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + u * 256;
+      if (e < zt) {
+        const int g = e & 3, q = e >> 2;
+        T* d = zs + q * ZS + g * 8;
+        if constexpr (sizeof(T) == 2) {
+          *(uint4*)d = zv[u];
+        } else {
+          const int rr = q >= bw ? 1 : 0, sx = q - rr * bw;
+          const T* src = z + ((int64_t)(rr ? r.y1 : r.y0) * bw + sx) * cs + g * 8;
+          for (int j = 0; j < 8; ++j) d[j] = (g * 8 + j < nch) ? src[j] : from_f32<T>(0.f);
+        }
+      } else if (e < zt + rt) {
+        const int f = e - zt, cl = f / W4, x4 = (f - cl * W4) * 4;
+        T* d = rs + cl * W4 * 4 + x4;
+        if constexpr (sizeof(T) == 2) {
+          *(uint2*)d = rv[u];
+        } else {
+          const T* src = res + rbase + (int64_t)cl * a.h * W + x4;
+          for (int j = 0; j < 4; ++j) d[j] = (x4 + j < W) ? src[j] : 0.f;
+        }
+      }
+    }
   }
   if (tid < 32) {
     s_att[tid] = tid < nch ? a.br_coeff[b] * (a.br_att[b] ? a.br_att[b][(int64_t)n * a.br_c[b] + cb0 + tid] : 1.f)
@@ -277,20 +326,36 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(kad_merge_args a) {
     s_gate[tid] = (a.gate && tid < nch) ? a.gate[cbase + tid] : 1.f;
   }
   __syncthreads();
-  const T* res = (const T*)a.residual;
+  const float scale = (float)bw / (float)W;
+  const int zr1 = (nrow == 2) ? bw * ZS : 0;
   T* out = (T*)a.out;
-  for (int cl = tid >> 6; cl < nch; cl += 4) {
-    const int64_t rowbase = (((int64_t)n * a.c + cbase + cl) * a.h + y) * a.w;
+  for (int f = tid; f < nch * W4; f += 256) {
+    const int cl = f / W4, x4 = (f - cl * W4) * 4;
     const float at = s_att[cl], gt = s_gate[cl];
-    for (int x = tid & 63; x < a.w; x += 64) {
-      const int x0 = x0s[x], x1 = x1s[x];
-      const float lx = lxs[x];
-      const float t0 = zs[x0 * 33 + cl], t1 = zs[x1 * 33 + cl];
-      const float u0 = zs[(bw + x0) * 33 + cl], u1 = zs[(bw + x1) * 33 + cl];
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int x = x4 + j < W ? x4 + j : W - 1;
+      int x0, x1;
+      float lx;
+      src_index(x, bw, W, scale, x0, x1, lx);
+      const float t0 = to_f32(zs[x0 * ZS + cl]), t1 = to_f32(zs[x1 * ZS + cl]);
+      const float u0 = to_f32(zs[zr1 + x0 * ZS + cl]), u1 = to_f32(zs[zr1 + x1 * ZS + cl]);
       const float top = t0 + lx * (t1 - t0), bot = u0 + lx * (u1 - u0);
-      float v = at * (top + r.ly * (bot - top));
-      if (res) v += to_f32(res[rowbase + x]);
-      out[rowbase + x] = from_f32<T>(v * gt);
+      float o = at * (top + r.ly * (bot - top));
+      if (res) o += to_f32(rs[cl * W4 * 4 + x4 + j]);
+      v[j] = o * gt;
+    }
+    T* d = out + rbase + (int64_t)cl * a.h * W + x4;
+    if (sizeof(T) == 2 && x4 + 4 <= W && ((uintptr_t)d & 7) == 0) {
+      typedef T v4 __attribute__((ext_vector_type(4)));
+      v4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = from_f32<T>(v[j]);
+      *(v4*)d = o;
+    } else {
+      for (int j = 0; j < 4; ++j)
+        if (x4 + j < W) d[j] = from_f32<T>(v[j]);
     }
   }
 }
@@ -447,7 +512,8 @@ extern "C" int kad_branch_merge(const kad_merge_args* a, void* stream) {
     maxbw = a->br_w[b] > maxbw ? a->br_w[b] : maxbw;
   }
   disjoint = disjoint && cover == a->c;
-  const size_t row_lds = (size_t)2 * maxbw * 33 * 4 + (size_t)3 * a->w * 4;
+  const int tsz = a->dtype == KAD_F32 ? 4 : 2;
+  const size_t row_lds = (size_t)2 * maxbw * 40 * tsz + (size_t)32 * ceil_div(a->w, 4) * 4 * tsz;
   if (a->layout == KAD_NCHW && disjoint && row_lds <= 64 * 1024) {
     dim3 grid(a->h, nchunks, a->n);
     switch (a->dtype) {

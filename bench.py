@@ -85,8 +85,9 @@ def build_kadconv(dim, dtype, seed=0):
     return m.to('cuda', dtype).eval()
 
 
-def dcn_flops(n, h, w, c):
-    return 2.0 * n * h * w * 9 * c * c
+def dsc_flops(n, h, w, c):
+    """Algorithmic flops of one DSC launch: deformable conv c -> c plus conv_offset c -> 18 (3x3)."""
+    return 2.0 * n * h * w * 9 * c * (c + 18)
 
 
 def cpu_baseline(shape, runs=5, warmup=2):
@@ -197,10 +198,10 @@ def main():
         for _, fn in stages:
             fn()
         stage_us = {name: round(time_eager(fn, 20), 2) for name, fn in stages}
-        dcn0 = dict(stages)['dcn0']
+        dsc0 = dict(stages)['dsc0']
         c0 = plan.branches[0].c
-        dcn_us = time_eager(dcn0, args.steps, args.warmup)
-        flops = dcn_flops(shape[0], shape[2], shape[3], c0)
+        dcn_us = time_eager(dsc0, args.steps, args.warmup)
+        flops = dsc_flops(shape[0], shape[2], shape[3], c0)
         achieved = flops / (dcn_us * 1e-6)
 
     traffic = None
@@ -225,7 +226,8 @@ def main():
                    'batch': 8, 'channels': 256, 'hw': [100, 100], 'branches': 3},
         'roofline': {'bound': 'mfma', 'achieved': round(achieved / 1e12, 3), 'peak': PEAK_MFMA_F16 / 1e12,
                      'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_MFMA_F16, 4), 'traffic': traffic,
-                     'kernel': 'dcn_fwd_kernel (branch 0: c=86, 8x100x100)', 'kernel_us': round(dcn_us, 3),
+                     'kernel': 'dcn_fwd_kernel<half,half,6,FUSED> (branch-0 DSC: conv_offset + DCN, c=86, '
+                               '8x100x100)', 'kernel_us': round(dcn_us, 3),
                      'flops_per_launch': flops},
         'forward_roofline': {'floor_us': FORWARD_FLOOR_US, 'frac': round(FORWARD_FLOOR_US / us, 4)},
         'stages_us': stage_us,

@@ -82,6 +82,8 @@ typedef struct kad_dcn_args {
   const float *post_scale;/* [Cout] or NULL: applied after the optional ReLU */
   void *out;              /* NHWC [N][Ho][Wo][out_cs] or NCHW [N][Cout][Ho][Wo], dtype */
   float *gap_partial;     /* [N][kad_dcn_tiles(Ho,Wo)][Cout] per-tile sums of out, or NULL */
+  const void *off_wpack;  /* kad_dsc_fwd only: conv_offset weights packed by kad_dcn_pack_weights (Cout = 18) */
+  const float *off_bias;  /* kad_dsc_fwd only: conv_offset bias [18] or NULL */
   int64_t off_sn, off_sp, off_sc;
   int64_t mask_sn, mask_sp, mask_sc;
   int n, cin, cout, h, w, stride, pad;
@@ -104,6 +106,16 @@ int kad_dcn_fwd(const kad_dcn_args *a, void *stream);
  * `out` is always fp32 here (offsets feed the sampling coordinates); weights
  * are packed with kad_dcn_pack_weights; post_* and relu apply as in kad_dcn_fwd. */
 int kad_conv3x3_fwd(const kad_dcn_args *a, void *stream);
+
+/* Whole DSC forward given the LCSA mask: offset = conv_offset(x) (weights
+ * a->off_wpack, bias a->off_bias) is computed inside each output tile and
+ * consumed by the deformable convolution in the same kernel, so the offsets
+ * never go to memory (a->offset is ignored).  Otherwise as kad_dcn_fwd.
+ * Stands in for DSC.forward (KAD-Conv/kadconv/kad_conv.py:63-67) minus the
+ * mask branch, i.e. the reference fast path's cuDNN conv_offset
+ * (acceleration/kadc_fused_sm75.py:1414-1421) followed by its DCN kernel
+ * (kadc_dcn16.cpp:247-289).  stride <= 2 (also for kad_conv3x3_fwd). */
+int kad_dsc_fwd(const kad_dcn_args *a, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* 1x1 convolution GEMM with fused input average pool and bias/SiLU epilogue */

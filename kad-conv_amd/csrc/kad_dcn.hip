@@ -1,4 +1,5 @@
-// Modulated deformable 3x3 convolution (DCNv2) fused into an MFMA GEMM.
+// Modulated deformable 3x3 convolution (DCNv2) fused into an MFMA GEMM, and the
+// plain 3x3 convolution that produces its offsets.
 //
 // Semantics: torchvision.ops.deform_conv2d as called by DSC.forward
 // (KAD-Conv/kadconv/kad_conv.py:63-67), one offset group; sampling rule as
@@ -13,24 +14,38 @@
 // GEMM view: out[p, co] = sum_k S[p, k] * Wt[k, co] with k = (chunk, tap, c32),
 // M = output pixels, N = Cout, K = 9 * roundup(Cin, 32).
 //
+// One kernel template, three modes:
+//  EXT    offsets (and mask) come from memory             -> kad_dcn_fwd
+//  FUSED  offsets = conv_offset(x) computed in the block   -> kad_dsc_fwd
+//  PLAIN  ordinary 3x3 convolution (no sampling)          -> kad_conv3x3_fwd
+//
 // Block = 256 threads (4 waves) x one output tile of up to 128 pixels (TH x TW,
-// chosen per image size to waste few lanes) x 16 * NBF output channels.
-//  1. Prologue: every (pixel, tap) sample position is computed once; its
-//     clamped top-left corner, corner steps and weights (bilinear x mask, 0 for
-//     out-of-image corners) go to LDS, and the block reduces the bounding box
-//     of all live corners.
-//  2. The input region = that bounding box (capped at RCAP pixels around the
-//     tile; typical offsets fit).  Each sample's region-relative corner address
-//     and weights (fp16 except on the fp32 path) are stored in LDS once.
-//     Samples whose corners fall outside a capped region are flagged and read
-//     straight from global memory by a rarely taken branch.
-//  3. Per 32-channel chunk: the region slice [pixels][32 ch] is staged in LDS
-//     (16-byte loads along channels of the NHWC input); then for each of the 9
-//     taps, each lane builds its MFMA A fragment (8 channels of one (pixel, tap))
-//     from four 16-byte LDS corner reads blended with packed fp16 FMAs, and the
-//     wave issues 2 x NBF v_mfma_f32_16x16x32 against B fragments (packed
-//     weights, 16 bytes per lane from global/L2, prefetched one tap ahead).
-//  4. Epilogue: bias, BN scale/shift, ReLU, branch scale, store, GAP partials.
+// chosen per image size to waste few lanes) x 16 * NBF output channels; wave w
+// owns tile pixels [32 w, 32 w + 32) and all the block's channels.
+//  0. Loads that do not depend on anything are issued first: epilogue
+//     parameters, the mask (and offsets in EXT mode), the first input chunk.
+//  1. PLAIN / FUSED: the tile's 3x3 footprint (tile + 1-pixel ring, zero
+//     padded) is staged per 32-channel chunk in LDS and convolved on MFMA
+//     (integer taps need no sample records).  FUSED keeps the 18 offset
+//     channels in LDS; PLAIN goes straight to the epilogue.
+//  2. Every (tap, pixel) sample position is computed once (registers), and the
+//     block reduces the bounding box of all live corners.  The input region =
+//     that box, capped to the LDS budget around the tile (typical offsets fit).
+//     Each sample's four region byte offsets and weights (bilinear x mask, 0
+//     for out-of-image corners; fp16 except on the fp32 path) go to LDS once.
+//     Samples outside a capped region are flagged and added by a rare pass
+//     that reads global memory.
+//  3. Per 32-channel chunk (next chunk prefetched into registers): the region
+//     slice [pixels][32 ch] and, on 16-bit paths, the chunk's weights
+//     [9 taps][cols][32] are staged in LDS; for each tap each lane builds its
+//     MFMA A fragment (8 channels of one (pixel, tap)) from four 16-byte LDS
+//     corner reads blended with packed FMAs, and the wave issues 2 x NBF
+//     v_mfma_f32_16x16x32 against 16-byte B fragments.  Weight rows are
+//     64 bytes, so their four 16-byte pieces are stored XOR-swizzled by
+//     column (piece g of column c at slot g ^ ((c >> 1) & 3)): the 16 lanes
+//     of a B read then hit distinct banks.
+//  4. Epilogue: bias, BN scale/shift, ReLU, branch scale; the tile is staged
+//     in LDS and written with 16-byte row-contiguous stores; GAP partials.
 // Blocks are mapped so that each XCD (and its L2) gets a contiguous band of
 // tiles: neighbouring tiles share their halos through that L2.
 //
@@ -46,18 +61,17 @@ constexpr int DCN_THREADS = 256;
 constexpr int DCN_WM = 2;                          // 16-pixel A fragments per wave
 constexpr int DCN_TILE = 4 * DCN_WM * 16;          // 128 pixels per block
 constexpr int DCN_NPAIR = 9 * DCN_TILE;            // (tap, pixel) samples per block
+constexpr int DCN_PPT = DCN_NPAIR / DCN_THREADS + 1;  // samples per thread (pixel tid % 128, taps tid / 128 + 2u)
+constexpr int DCN_NOFF = 18;                       // offset channels (2 x 9 taps)
+constexpr int DCN_LDS = 160 * 1024;                // gfx950 LDS per CU
+constexpr int DCN_FCAP = 704;                      // footprint pixels (enough for stride <= 2)
 
-template <typename T> struct DcnCfg {              // fp16 / bf16
-  static constexpr int pxs = 40;                   // halves per region pixel (32 + 8 pad)
-  static constexpr int rcap = 736;                 // region pixels (57.5 KB; + 13.5 KB sample info)
-};
-template <> struct DcnCfg<float> {
-  static constexpr int pxs = 36;                   // floats per region pixel (32 + 4 pad)
-  static constexpr int rcap = 320;                 // (45 KB; + 22.5 KB sample info)
-};
+enum { MODE_EXT = 0, MODE_FUSED = 1, MODE_PLAIN = 2 };
 
 struct DcnGeom {
   int ho, wo, th, tw, tiles_x, tiles, grid_x, nchunk, cout_pad;
+  int fh, fw;        // 3x3 footprint of a tile: (th - 1) * stride + 3 rows, likewise columns
+  float inv_tw, inv_fw;
 };
 
 // Tile shape for an Ho x Wo output: TH x TW <= 128 pixels minimising the
@@ -81,11 +95,12 @@ static void pick_tile(int ho, int wo, int* th_out, int* tw_out) {
 
 // ---- sample info ----------------------------------------------------------------------------
 // Fast-path record per (tap, pixel): byte offsets of the four corners inside the
-// staged region (16 bits each) and the corner weights.  Samples that are dead
+// staged region and the corner weights (16-bit paths: 16-bit offsets, fp16
+// weights; fp32 path: 32-bit offsets, fp32 weights).  Samples that are dead
 // (all weights 0) or outside a capped region get zero weights here; the latter
 // are accumulated by a separate pass from global memory (s_slow).
 struct __align__(16) Info16 { unsigned o01, o23; unsigned w01, w23; };  // weights as 2 x half2
-struct __align__(16) Info32 { unsigned o01, o23, pad0, pad1; float w[4]; };
+struct __align__(16) Info32 { unsigned o[4]; float w[4]; };
 
 __device__ __forceinline__ unsigned pack_h2(float a, float b) {
   const half2_t h{(half_t)a, (half_t)b};
@@ -96,20 +111,29 @@ template <typename T> struct InfoOf { typedef Info16 type; };
 template <> struct InfoOf<float> { typedef Info32 type; };
 
 template <typename T>
-__device__ __forceinline__ typename InfoOf<T>::type make_info(unsigned o01, unsigned o23, const float* w) {
+__device__ __forceinline__ typename InfoOf<T>::type make_info(const unsigned* o, const float* w) {
   typename InfoOf<T>::type r;
-  r.o01 = o01;
-  r.o23 = o23;
   if constexpr (sizeof(T) == 4) {
-    r.pad0 = r.pad1 = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.w[i] = w[i];
+    for (int i = 0; i < 4; ++i) {
+      r.o[i] = o[i];
+      r.w[i] = w[i];
+    }
   } else {
+    r.o01 = o[0] | (o[1] << 16);
+    r.o23 = o[2] | (o[3] << 16);
     r.w01 = pack_h2(w[0], w[1]);
     r.w23 = pack_h2(w[2], w[3]);
   }
   return r;
 }
+
+// byte offset of corner j of a record
+__device__ __forceinline__ unsigned corner(const Info16& in, int j) {
+  const unsigned v = j < 2 ? in.o01 : in.o23;
+  return (j & 1) ? v >> 16 : v & 0xffffu;
+}
+__device__ __forceinline__ unsigned corner(const Info32& in, int j) { return in.o[j]; }
 
 // ---- A fragment from four corners ------------------------------------------------------------
 template <typename T> struct DcnFrag;
@@ -183,6 +207,16 @@ __device__ __forceinline__ typename DcnFrag<T>::frag ld8(const T* p) {
 }
 
 template <typename T>
+__device__ __forceinline__ void st8(T* p, const typename DcnFrag<T>::frag& v) {
+  if constexpr (sizeof(T) == 4) {
+    *(floatx4*)p = v.lo;
+    *(floatx4*)(p + 4) = v.hi;
+  } else {
+    *(typename DcnFrag<T>::frag*)p = v;
+  }
+}
+
+template <typename T>
 __device__ __forceinline__ typename DcnFrag<T>::frag zero8() {
   typedef typename DcnFrag<T>::frag F;
   if constexpr (sizeof(T) == 4) {
@@ -220,184 +254,253 @@ __device__ __forceinline__ void sample_geom(float py, float px, float m, int h, 
   }
 }
 
+// ---- LDS budget per instantiation --------------------------------------------------------------
+template <typename T, typename OutT, int NBF, int MODE> struct DcnLds {
+  static constexpr bool BLDS = sizeof(T) == 2;     // 16-bit paths stage the weights in LDS
+  static constexpr int NB = NBF * 16;
+  static constexpr int PXS = sizeof(T) == 2 ? 40 : 36;  // elements per region pixel (32 + pad: conflict-free rows)
+  static constexpr int PXB = PXS * (int)sizeof(T);
+  static constexpr int BCOLS = NB > 32 ? NB : 32;  // >= 32: FUSED stages the offset weights here too
+  static constexpr int BSM = BLDS ? 9 * BCOLS * 32 : 8;
+  static constexpr int NINFO = MODE == MODE_PLAIN ? 1 : DCN_NPAIR;
+  static constexpr int NOFF = MODE == MODE_FUSED ? DCN_TILE * DCN_NOFF : 1;
+  static constexpr int SROW = NB + 16 / (int)sizeof(OutT);  // epilogue staging row (elements)
+  static constexpr int FIXED = BSM * (int)sizeof(T) + NINFO * ((int)sizeof(typename InfoOf<T>::type) + 1) +
+                               NOFF * 4 + 2 * 4 * NB * 4 + 256;
+  static constexpr int STAGE_PX = (DCN_TILE * SROW * (int)sizeof(OutT) + PXB - 1) / PXB;
+  static constexpr int RCAP_WANT = STAGE_PX > 768 ? STAGE_PX : 768;  // region staging uses RCAP / 64 pieces per thread
+  static constexpr int RCAP = (DCN_LDS - FIXED) / PXB < RCAP_WANT ? (DCN_LDS - FIXED) / PXB : RCAP_WANT;
+  static_assert(RCAP >= DCN_FCAP, "footprint must fit the region buffer");
+  static_assert(MODE == MODE_PLAIN || sizeof(T) == 4 || RCAP * PXB <= 65536, "16-bit corner offsets");
+  static_assert(RCAP * PXB >= DCN_TILE * SROW * (int)sizeof(OutT), "epilogue tile must fit the region buffer");
+};
+
+// Chunk staging: NPIX region pixels x 32 channels, 16-byte pieces, prefetched in registers.
+template <typename T, int CAP> struct RegionTile {
+  static constexpr int RPT = (CAP + DCN_THREADS / 4 - 1) / (DCN_THREADS / 4);
+  typename DcnFrag<T>::frag v[RPT];
+  // rows x cols pixels starting at (y0, x0) (may extend outside the image: zeros)
+  __device__ __forceinline__ void load(const T* xb, int y0, int x0, int cols, int npix, float inv_cols, int h, int w,
+                                       int x_cs, int chs, bool chs_ok, int tid) {
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+      const int q = (tid >> 2) + u * (DCN_THREADS / 4);
+      v[u] = zero8<T>();
+      if (q < npix && chs_ok) {
+        const int qy = (int)(((float)q + 0.5f) * inv_cols);
+        const int gy = y0 + qy, gx = x0 + q - qy * cols;
+        if (gy >= 0 && gy < h && gx >= 0 && gx < w) v[u] = ld8<T>(xb + ((int64_t)gy * w + gx) * x_cs + chs);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(T* region, int pxs, int npix, int tid) {
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+      const int q = (tid >> 2) + u * (DCN_THREADS / 4);
+      if (q < npix) st8<T>(region + q * pxs + (tid & 3) * 8, v[u]);
+    }
+  }
+};
+
+// Chunk weights [9][NBC][32] (16-bit paths), swizzled 16-byte pieces.
+template <typename T, int NBC> struct WeightTile {
+  static constexpr int PIECES = 9 * NBC * 4;
+  static constexpr int BPT = (PIECES + DCN_THREADS - 1) / DCN_THREADS;
+  typename DcnFrag<T>::frag v[BPT];
+  __device__ __forceinline__ void load(const T* wpk, int co0, int cpad, int nchunk, int c, int tid) {
+#pragma unroll
+    for (int u = 0; u < BPT; ++u) {
+      const int e = tid + u * DCN_THREADS;
+      v[u] = zero8<T>();
+      if (e < PIECES) {
+        const int k = e / (NBC * 4), r = e - k * (NBC * 4), co = co0 + (r >> 2);
+        if (co < cpad) v[u] = ld8<T>(wpk + ((int64_t)(co * nchunk + c) * 9 + k) * 32 + (r & 3) * 8);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(T* bsm, int tid) {
+#pragma unroll
+    for (int u = 0; u < BPT; ++u) {
+      const int e = tid + u * DCN_THREADS;
+      if (e < PIECES) {
+        const int k = e / (NBC * 4), r = e - k * (NBC * 4), col = r >> 2;
+        st8<T>(bsm + ((k * NBC + col) * 4 + ((r & 3) ^ ((col >> 1) & 3))) * 8, v[u]);
+      }
+    }
+  }
+};
+
+template <typename T, int NBC>
+__device__ __forceinline__ typename DcnFrag<T>::frag b_read(const T* bsm, int k, int col, int grp) {
+  return ld8<T>(bsm + ((k * NBC + col) * 4 + (grp ^ ((col >> 1) & 3))) * 8);
+}
+
+// ---- plain 3x3 convolution of one tile (footprint staged per chunk) -------------------------------
+// acc[m][b] += sum over taps/chunks of x[footprint] * W[co0 + 16 b + row]; the
+// footprint origin is (fy0, fx0) (may be negative: zero padding).
+template <typename T, int NBP, int PXS, int RCAP>
+__device__ __forceinline__ void plain_conv(floatx4 (&acc)[DCN_WM][NBP], const T* xb, const T* wpk, int co0, int cpad,
+                                           int nchunk, int cin8, int h, int w, int x_cs, int stride, int fy0, int fx0,
+                                           const DcnGeom& g, T* region, T* bsm) {
+  typedef DcnFrag<T> Ops;
+  typedef typename Ops::frag frag;
+  constexpr bool BLDS = sizeof(T) == 2;
+  constexpr int NBC = NBP * 16;
+  constexpr int PXB = PXS * (int)sizeof(T);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = lane & 15, grp = lane >> 4;
+  const int fpix = g.fh * g.fw;
+  // this lane's A rows: output pixel pl -> footprint byte offset of its (0, 0) tap
+  int abase[DCN_WM];
+#pragma unroll
+  for (int m = 0; m < DCN_WM; ++m) {
+    int pl = wave * (16 * DCN_WM) + m * 16 + row;
+    if (pl >= g.th * g.tw) pl = 0;  // padding lane: any in-bounds address, result discarded
+    const int py = (int)(((float)pl + 0.5f) * g.inv_tw), px = pl - py * g.tw;
+    abase[m] = ((py * stride) * g.fw + px * stride) * PXB + grp * 8 * (int)sizeof(T);
+  }
+  const T* wrow[NBP];
+#pragma unroll
+  for (int b = 0; b < NBP; ++b) {
+    const int co = co0 + b * 16 + row;
+    wrow[b] = wpk + (int64_t)(co < cpad ? co : 0) * nchunk * 9 * 32 + grp * 8;
+  }
+  RegionTile<T, DCN_FCAP> rt;
+  WeightTile<T, BLDS ? NBC : 1> wt;
+  const int gq8 = (tid & 3) * 8;
+  rt.load(xb, fy0, fx0, g.fw, fpix, g.inv_fw, h, w, x_cs, gq8, gq8 < cin8, tid);
+  if constexpr (BLDS) wt.load(wpk, co0, cpad, nchunk, 0, tid);
+  rt.store(region, PXS, fpix, tid);
+  if constexpr (BLDS) wt.store(bsm, tid);
+  for (int c = 0; c < nchunk; ++c) {
+    __syncthreads();
+    if (c + 1 < nchunk) {
+      const int chs = (c + 1) * 32 + gq8;
+      rt.load(xb, fy0, fx0, g.fw, fpix, g.inv_fw, h, w, x_cs, chs, chs < cin8, tid);
+      if constexpr (BLDS) wt.load(wpk, co0, cpad, nchunk, c + 1, tid);
+    }
+    const bool ch_ok = c * 32 + grp * 8 < cin8;
+    frag bn[NBP];
+    if constexpr (!BLDS) {
+#pragma unroll
+      for (int b = 0; b < NBP; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9) * 32);
+    }
+    int ky = 0, kx = 0;
+#pragma unroll 1
+    for (int k = 0; k < 9; ++k) {
+      frag bf[NBP];
+      if constexpr (BLDS) {
+#pragma unroll
+        for (int b = 0; b < NBP; ++b) bf[b] = b_read<T, NBC>(bsm, k, b * 16 + row, grp);
+      } else {
+#pragma unroll
+        for (int b = 0; b < NBP; ++b) bf[b] = bn[b];
+        if (k < 8) {
+#pragma unroll
+          for (int b = 0; b < NBP; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9 + k + 1) * 32);
+        }
+      }
+      const int toff = (ky * g.fw + kx) * PXB;
+      frag af[DCN_WM];
+#pragma unroll
+      for (int m = 0; m < DCN_WM; ++m) {
+        af[m] = ld8<T>((const T*)((const char*)region + abase[m] + toff));
+        if (!ch_ok) af[m] = zero8<T>();
+      }
+#pragma unroll
+      for (int m = 0; m < DCN_WM; ++m)
+#pragma unroll
+        for (int b = 0; b < NBP; ++b) acc[m][b] = Ops::mma(af[m], bf[b], acc[m][b]);
+      if (++kx == 3) {
+        kx = 0;
+        ++ky;
+      }
+    }
+    if (c + 1 < nchunk) {
+      __syncthreads();
+      rt.store(region, PXS, fpix, tid);
+      if constexpr (BLDS) wt.store(bsm, tid);
+    }
+  }
+}
+
 // ---- kernel ------------------------------------------------------------------------------------
-// PLAIN = true computes an ordinary 3x3 convolution (integer taps, no offsets or
-// mask): DSC's offset branch, conv_offset (kad_conv.py:55-56).
-template <typename T, typename OutT, int NBF, bool PLAIN>
-__global__ __launch_bounds__(DCN_THREADS, 2) void dcn_fwd_kernel(kad_dcn_args a, DcnGeom g) {
+template <typename T, typename OutT, int NBF, int MODE>
+__global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a, DcnGeom g) {
   typedef DcnFrag<T> Ops;
   typedef typename Ops::frag frag;
   typedef typename InfoOf<T>::type Info;
-  constexpr int PXS = DcnCfg<T>::pxs;
-  constexpr int RCAP = DcnCfg<T>::rcap;
-  static_assert(RCAP * PXS * sizeof(T) >= DCN_NPAIR * 24, "prologue scratch must fit in the region buffer");
-  // region [RCAP][PXS] T; during the prologue it holds the raw samples instead
-  __shared__ __align__(16) T region[RCAP * PXS];
-  __shared__ Info s_info[DCN_NPAIR];                 // [9][128] per-sample corner offsets + weights
-  __shared__ unsigned char s_slow[DCN_NPAIR];        // [9][128] 1 = sample outside the capped region
+  typedef DcnLds<T, OutT, NBF, MODE> L;
+  constexpr int NB = L::NB, PXS = L::PXS, PXB = L::PXB, RCAP = L::RCAP;
+  constexpr bool BLDS = L::BLDS;
+  __shared__ __align__(16) T region[RCAP * PXS];     // input region / footprint; epilogue tile at the end
+  __shared__ __align__(16) T bsm[L::BSM];            // chunk weights [9][cols][32] (16-bit paths)
+  __shared__ Info s_info[L::NINFO];                  // [9][128] corner offsets + weights
+  __shared__ unsigned char s_slow[L::NINFO];         // [9][128] 1 = sample outside the capped region
+  __shared__ float s_off[L::NOFF];                   // FUSED: [128][18] offsets of the tile
+  __shared__ float s_par[4][NB];                     // bias, post_mul, post_add, post_scale
+  __shared__ float gap_red[4][NB];
   __shared__ int s_box[4];       // ymin, ymax, xmin, xmax (clamped corners of live samples)
   __shared__ int s_reg[5];       // region y0, x0, rows, cols, capped flag
-  __shared__ float gap_red[4][NBF * 16];
-  float4* raw_w = (float4*)region;                   // [9][128] corner weights
-  int* raw_yx = (int*)(raw_w + DCN_NPAIR);           // [9][128] clamped top-left corner (y << 15 | x)
-  int* raw_st = raw_yx + DCN_NPAIR;                  // [9][128] corner steps (dy << 1 | dx)
 
   // XCD-aware tile order: block b runs on XCD b % 8; give each XCD a contiguous band.
   const int bx = blockIdx.x;
   const int tile = (bx & 7) * (g.grid_x >> 3) + (bx >> 3);
   if (tile >= g.tiles) return;  // whole block, before any barrier
-  const int co0 = blockIdx.y * NBF * 16;
+  const int co0 = blockIdx.y * NB;
   const int n = blockIdx.z;
   const int tyi = tile / g.tiles_x;
   const int ty0 = tyi * g.th, tx0 = (tile - tyi * g.tiles_x) * g.tw;
   const int P = g.ho * g.wo;
+  const int npx = g.th * g.tw;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = lane & 15, grp = lane >> 4;
+  const T* xb = (const T*)a.x + (int64_t)n * a.h * a.w * a.x_cs;
+  const int cin8 = round_up(a.cin, 8);
+  const int fy0 = ty0 * a.stride - a.pad, fx0 = tx0 * a.stride - a.pad;
 
+  // ---- 0. independent loads ------------------------------------------------------------------------
+  float par[4] = {0.f, 1.f, 0.f, 1.f};
+  if (tid < NB) {
+    const int co = co0 + tid;
+    if (co < a.cout) {
+      if (a.bias) par[0] = a.bias[co];
+      if (a.post_mul) par[1] = a.post_mul[co];
+      if (a.post_add) par[2] = a.post_add[co];
+      if (a.post_scale) par[3] = a.post_scale[co];
+    }
+  }
+  // this thread's prologue pixel (taps tid / 128 + 2u)
+  const int ppl = tid & (DCN_TILE - 1);
+  const int ppy = (int)(((float)ppl + 0.5f) * g.inv_tw), ppx = ppl - ppy * g.tw;
+  const int poy = ty0 + ppy, pox = tx0 + ppx;
+  const bool plive = ppl < npx && poy < g.ho && pox < g.wo;
+  const int64_t pp = (int64_t)poy * g.wo + pox;
+  float pre_dy[DCN_PPT], pre_dx[DCN_PPT], pre_m[DCN_PPT];
+  if constexpr (MODE != MODE_PLAIN) {
+#pragma unroll
+    for (int u = 0; u < DCN_PPT; ++u) {
+      const int k = (tid >> 7) + 2 * u;
+      pre_dy[u] = pre_dx[u] = 0.f;
+      pre_m[u] = 1.f;
+      if (k < 9 && plive) {
+        if constexpr (MODE == MODE_EXT) {
+          pre_dy[u] = a.offset[n * a.off_sn + pp * a.off_sp + (2 * k) * a.off_sc];
+          pre_dx[u] = a.offset[n * a.off_sn + pp * a.off_sp + (2 * k + 1) * a.off_sc];
+        }
+        if (a.mask) pre_m[u] = a.mask[n * a.mask_sn + pp * a.mask_sp + k * a.mask_sc];
+      }
+    }
+  }
+  if (tid < NB) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_par[j][tid] = par[j];
+  }
   if (tid == 0) {
     s_box[0] = 0x7fffffff;
     s_box[1] = -1;
     s_box[2] = 0x7fffffff;
     s_box[3] = -1;
   }
-  __syncthreads();
-  // ---- 1. samples: clamped corners, weights, bounding box ------------------------------------------
-  int bymin = 0x7fffffff, bymax = -1, bxmin = 0x7fffffff, bxmax = -1;
-  // offsets and mask of this thread's samples, all loads issued before any use
-  constexpr int PPT = (DCN_NPAIR + DCN_THREADS - 1) / DCN_THREADS;
-  float pre_dy[PPT], pre_dx[PPT], pre_m[PPT];
-#pragma unroll
-  for (int u = 0; u < PPT; ++u) {
-    const int q = tid + u * DCN_THREADS;
-    pre_dy[u] = pre_dx[u] = 0.f;
-    pre_m[u] = 1.f;
-    if (!PLAIN && q < DCN_NPAIR) {
-      const int k = q / DCN_TILE, pl = q - k * DCN_TILE;
-      const int oy = ty0 + pl / g.tw, ox = tx0 + pl - (pl / g.tw) * g.tw;
-      if (pl < g.th * g.tw && oy < g.ho && ox < g.wo) {
-        const int64_t p = oy * g.wo + ox;
-        pre_dy[u] = a.offset[n * a.off_sn + p * a.off_sp + (2 * k) * a.off_sc];
-        pre_dx[u] = a.offset[n * a.off_sn + p * a.off_sp + (2 * k + 1) * a.off_sc];
-        if (a.mask) pre_m[u] = a.mask[n * a.mask_sn + p * a.mask_sp + k * a.mask_sc];
-      }
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < PPT; ++u) {
-    const int q = tid + u * DCN_THREADS;
-    if (q >= DCN_NPAIR) break;
-    const int k = q / DCN_TILE, pl = q - k * DCN_TILE;
-    const int oy = ty0 + pl / g.tw, ox = tx0 + pl - (pl / g.tw) * g.tw;
-    float w[4] = {0.f, 0.f, 0.f, 0.f};
-    int cy0 = 0, cx0 = 0, sy = 0, sx = 0;
-    const bool live_px = pl < g.th * g.tw && oy < g.ho && ox < g.wo;
-    const int ky = k / 3, kx = k - (k / 3) * 3;
-    if (live_px && PLAIN) {
-      const int iy = oy * a.stride - a.pad + ky, ix = ox * a.stride - a.pad + kx;
-      if (iy >= 0 && iy < a.h && ix >= 0 && ix < a.w) {
-        cy0 = iy;
-        cx0 = ix;
-        w[0] = 1.f;
-      }
-    } else if (live_px) {
-      const float py = (float)(oy * a.stride - a.pad + ky) + pre_dy[u];
-      const float px = (float)(ox * a.stride - a.pad + kx) + pre_dx[u];
-      sample_geom(py, px, pre_m[u], a.h, a.w, cy0, cx0, sy, sx, w);
-    }
-    const bool live = w[0] != 0.f || w[1] != 0.f || w[2] != 0.f || w[3] != 0.f;
-    if (live) {
-      bymin = min(bymin, cy0);
-      bymax = max(bymax, cy0 + sy);
-      bxmin = min(bxmin, cx0);
-      bxmax = max(bxmax, cx0 + sx);
-    }
-    raw_yx[q] = (cy0 << 15) | cx0;
-    raw_w[q] = float4{w[0], w[1], w[2], w[3]};
-    raw_st[q] = (sy << 1) | sx;
-  }
-  // wave-level then block-level bounding box (integer min / max: order-independent)
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    bymin = min(bymin, __shfl_xor(bymin, o));
-    bymax = max(bymax, __shfl_xor(bymax, o));
-    bxmin = min(bxmin, __shfl_xor(bxmin, o));
-    bxmax = max(bxmax, __shfl_xor(bxmax, o));
-  }
-  if (lane == 0) {
-    atomicMin(&s_box[0], bymin);
-    atomicMax(&s_box[1], bymax);
-    atomicMin(&s_box[2], bxmin);
-    atomicMax(&s_box[3], bxmax);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int ry0 = s_box[0], ry1 = s_box[1], rx0 = s_box[2], rx1 = s_box[3];
-    int capped = 0;
-    if (ry1 < ry0 || rx1 < rx0) {  // no live sample at all
-      ry0 = ry1 = rx0 = rx1 = 0;
-    } else if ((ry1 - ry0 + 1) * (rx1 - rx0 + 1) > RCAP) {
-      // keep the tile's own footprint plus the widest halo m that fits
-      const int fy0 = max(ty0 * a.stride - a.pad, 0), fy1 = min((ty0 + g.th - 1) * a.stride - a.pad + 2, a.h - 1);
-      const int fx0 = max(tx0 * a.stride - a.pad, 0), fx1 = min((tx0 + g.tw - 1) * a.stride - a.pad + 2, a.w - 1);
-      int m = 0;
-      while (m < 4096) {
-        const int y0n = max(ry0, fy0 - m - 1), y1n = min(ry1, fy1 + m + 1);
-        const int x0n = max(rx0, fx0 - m - 1), x1n = min(rx1, fx1 + m + 1);
-        if ((y1n - y0n + 1) * (x1n - x0n + 1) > RCAP) break;
-        ++m;
-      }
-      const int y0n = max(ry0, fy0 - m), y1n = min(ry1, fy1 + m);
-      const int x0n = max(rx0, fx0 - m), x1n = min(rx1, fx1 + m);
-      if ((y1n - y0n + 1) * (x1n - x0n + 1) <= RCAP && y1n >= y0n && x1n >= x0n) {
-        ry0 = y0n;
-        ry1 = y1n;
-        rx0 = x0n;
-        rx1 = x1n;
-      } else {  // degenerate (very wide tile footprint): a 1 x 1 region, everything global
-        ry1 = ry0;
-        rx1 = rx0;
-      }
-      capped = 1;
-    }
-    s_reg[0] = ry0;
-    s_reg[1] = rx0;
-    s_reg[2] = ry1 - ry0 + 1;
-    s_reg[3] = rx1 - rx0 + 1;
-    s_reg[4] = capped;
-  }
-  __syncthreads();
-  const int ry0 = s_reg[0], rx0 = s_reg[1], rh = s_reg[2], rw = s_reg[3];
-  const bool block_may_slow = s_reg[4] != 0;
-  // ---- 2. sample info: corner byte offsets in the region + weights; slow samples listed apart -------
-  constexpr int PXB = PXS * (int)sizeof(T);          // bytes per region pixel
-  for (int q = tid; q < DCN_NPAIR; q += DCN_THREADS) {
-    const int yx = raw_yx[q], st = raw_st[q];
-    const float4 wv = raw_w[q];
-    float w[4] = {wv.x, wv.y, wv.z, wv.w};
-    const int cy0 = yx >> 15, cx0 = yx & 0x7fff;
-    const int sy = st >> 1, sx = st & 1;
-    const int ly = cy0 - ry0, lx = cx0 - rx0;
-    const bool dead = w[0] == 0.f && w[1] == 0.f && w[2] == 0.f && w[3] == 0.f;
-    unsigned o01 = 0, o23 = 0;
-    unsigned char slow = 0;
-    if (!dead && ly >= 0 && ly + sy < rh && lx >= 0 && lx + sx < rw) {
-      const unsigned b0 = (unsigned)((ly * rw + lx) * PXB);
-      const unsigned bx = (unsigned)(sx * PXB), by = (unsigned)(sy * rw * PXB);
-      o01 = b0 | ((b0 + bx) << 16);
-      o23 = (b0 + by) | ((b0 + by + bx) << 16);
-    } else if (!dead) {
-      slow = 1;                         // the fast path skips it; the slow pass adds it
-      w[0] = w[1] = w[2] = w[3] = 0.f;
-    } else {
-      w[0] = w[1] = w[2] = w[3] = 0.f;
-    }
-    s_info[q] = make_info<T>(o01, o23, w);
-    s_slow[q] = slow;
-  }
-
-  const T* xb = (const T*)a.x + (int64_t)n * a.h * a.w * a.x_cs;
-  const T* wp = (const T*)a.wpack;
-  const int cin8 = round_up(a.cin, 8);
 
   floatx4 acc[DCN_WM][NBF];
 #pragma unroll
@@ -405,166 +508,307 @@ __global__ __launch_bounds__(DCN_THREADS, 2) void dcn_fwd_kernel(kad_dcn_args a,
 #pragma unroll
     for (int b = 0; b < NBF; ++b) acc[m][b] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  const int rpix = rh * rw;
-  const int step = DCN_THREADS / 4;
-  const int ibase = wave * (16 * DCN_WM) + row;      // this lane's pixel slot within a tap row of s_info
-  const T* wrow[NBF];                                // this lane's weight row (output channel) per fragment
+  if constexpr (MODE == MODE_PLAIN) {
+    // ---- 1. plain 3x3 convolution -----------------------------------------------------------------
+    plain_conv<T, NBF, PXS, RCAP>(acc, xb, (const T*)a.wpack, co0, g.cout_pad, g.nchunk, cin8, a.h, a.w, a.x_cs,
+                                  a.stride, fy0, fx0, g, region, bsm);
+  } else {
+    if constexpr (MODE == MODE_FUSED) {
+      // ---- 1. offsets = conv_offset(x) over the tile ----------------------------------------------------
+      floatx4 oacc[DCN_WM][2];
 #pragma unroll
-  for (int b = 0; b < NBF; ++b) {
-    const int co = co0 + b * 16 + row;
-    wrow[b] = wp + (int64_t)(co < g.cout_pad ? co : 0) * g.nchunk * 9 * 32 + grp * 8;
-  }
-  for (int c = 0; c < g.nchunk; ++c) {
-    __syncthreads();  // previous chunk (or the prologue's raw samples) fully consumed
-    // ---- 3a. stage the region slice [rpix][32 ch], four 16-byte loads in flight per thread -------------
-    {
-      const int gq = tid & 3;
-      const int chs = c * 32 + gq * 8;
-      const bool chs_ok = chs < cin8;
-      const float inv_rw = 1.f / (float)rw;
-      for (int base = tid >> 2; base < rpix; base += 4 * step) {
-        frag v[4];
+      for (int m = 0; m < DCN_WM; ++m) oacc[m][0] = oacc[m][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+      plain_conv<T, 2, PXS, RCAP>(oacc, xb, (const T*)a.off_wpack, 0, 32, g.nchunk, cin8, a.h, a.w, a.x_cs,
+                                  a.stride, fy0, fx0, g, region, bsm);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int q = base + u * step;
-          v[u] = zero8<T>();
-          if (q < rpix && chs_ok) {
-            const int qy = (int)(((float)q + 0.5f) * inv_rw);
-            const int qx = q - qy * rw;
-            v[u] = ld8<T>(xb + ((int64_t)(ry0 + qy) * a.w + rx0 + qx) * a.x_cs + chs);
-          }
-        }
+      for (int b = 0; b < 2; ++b) {
+        const int ch = b * 16 + row;
+        if (ch < DCN_NOFF) {
+          const float ob = a.off_bias ? a.off_bias[ch] : 0.f;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int q = base + u * step;
-          if (q < rpix) {
-            T* d = region + q * PXS + gq * 8;
-            if constexpr (sizeof(T) == 4) {
-              *(floatx4*)d = v[u].lo;
-              *(floatx4*)(d + 4) = v[u].hi;
-            } else {
-              *(frag*)d = v[u];
-            }
-          }
+          for (int m = 0; m < DCN_WM; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              s_off[(wave * (16 * DCN_WM) + m * 16 + grp * 4 + i) * DCN_NOFF + ch] = oacc[m][b][i] + ob;
         }
       }
+      __syncthreads();  // offsets visible; footprint buffers free
+    }
+    // ---- 2. samples: clamped corners, weights, bounding box (registers) --------------------------------
+    int bymin = 0x7fffffff, bymax = -1, bxmin = 0x7fffffff, bxmax = -1;
+    int smp_yx[DCN_PPT], smp_st[DCN_PPT];
+    float smp_w[DCN_PPT][4];
+#pragma unroll
+    for (int u = 0; u < DCN_PPT; ++u) {
+      const int k = (tid >> 7) + 2 * u;
+      float* w = smp_w[u];
+      w[0] = w[1] = w[2] = w[3] = 0.f;
+      int cy0 = 0, cx0 = 0, sy = 0, sx = 0;
+      if (k < 9 && plive) {
+        const int ky = k / 3, kx = k - (k / 3) * 3;
+        float dy = pre_dy[u], dx = pre_dx[u];
+        if constexpr (MODE == MODE_FUSED) {
+          dy = s_off[ppl * DCN_NOFF + 2 * k];
+          dx = s_off[ppl * DCN_NOFF + 2 * k + 1];
+        }
+        const float py = (float)(poy * a.stride - a.pad + ky) + dy;
+        const float px = (float)(pox * a.stride - a.pad + kx) + dx;
+        sample_geom(py, px, pre_m[u], a.h, a.w, cy0, cx0, sy, sx, w);
+      }
+      const bool live = w[0] != 0.f || w[1] != 0.f || w[2] != 0.f || w[3] != 0.f;
+      if (live) {
+        bymin = min(bymin, cy0);
+        bymax = max(bymax, cy0 + sy);
+        bxmin = min(bxmin, cx0);
+        bxmax = max(bxmax, cx0 + sx);
+      }
+      smp_yx[u] = (cy0 << 15) | cx0;
+      smp_st[u] = (sy << 1) | sx;
+    }
+    // wave-level then block-level bounding box (integer min / max: order-independent)
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      bymin = min(bymin, __shfl_xor(bymin, o));
+      bymax = max(bymax, __shfl_xor(bymax, o));
+      bxmin = min(bxmin, __shfl_xor(bxmin, o));
+      bxmax = max(bxmax, __shfl_xor(bxmax, o));
+    }
+    __syncthreads();  // s_box initialised
+    if (lane == 0) {
+      atomicMin(&s_box[0], bymin);
+      atomicMax(&s_box[1], bymax);
+      atomicMin(&s_box[2], bxmin);
+      atomicMax(&s_box[3], bxmax);
     }
     __syncthreads();
-    // ---- 3b. nine taps of this chunk: weights and sample records prefetched one tap ahead -----------
-    const bool ch_ok = c * 32 + grp * 8 < cin8;
-    frag bf[NBF], bn[NBF];
-    Info ic[DCN_WM], inx[DCN_WM];
-#pragma unroll
-    for (int b = 0; b < NBF; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9) * 32);
-#pragma unroll
-    for (int m = 0; m < DCN_WM; ++m) inx[m] = s_info[m * 16 + ibase];
-#pragma unroll 1
-    for (int k = 0; k < 9; ++k) {
-#pragma unroll
-      for (int b = 0; b < NBF; ++b) bf[b] = bn[b];
-#pragma unroll
-      for (int m = 0; m < DCN_WM; ++m) ic[m] = inx[m];
-      if (k < 8) {
-#pragma unroll
-        for (int b = 0; b < NBF; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9 + k + 1) * 32);
-#pragma unroll
-        for (int m = 0; m < DCN_WM; ++m) inx[m] = s_info[(k + 1) * DCN_TILE + m * 16 + ibase];
-      }
-      frag af[DCN_WM];
-#pragma unroll
-      for (int m = 0; m < DCN_WM; ++m) {
-        const char* rb = (const char*)region + grp * 8 * (int)sizeof(T);
-        if (PLAIN) {
-          af[m] = Ops::blend(ld8<T>((const T*)(rb + (ic[m].o01 & 0xffffu))), zero8<T>(), zero8<T>(), zero8<T>(),
-                             ic[m]);
-        } else {
-          const frag v0 = ld8<T>((const T*)(rb + (ic[m].o01 & 0xffffu)));
-          const frag v1 = ld8<T>((const T*)(rb + (ic[m].o01 >> 16)));
-          const frag v2 = ld8<T>((const T*)(rb + (ic[m].o23 & 0xffffu)));
-          const frag v3 = ld8<T>((const T*)(rb + (ic[m].o23 >> 16)));
-          af[m] = Ops::blend(v0, v1, v2, v3, ic[m]);
+    if (tid == 0) {
+      int ry0 = s_box[0], ry1 = s_box[1], rx0 = s_box[2], rx1 = s_box[3];
+      int capped = 0;
+      if (ry1 < ry0 || rx1 < rx0) {  // no live sample at all
+        ry0 = ry1 = rx0 = rx1 = 0;
+      } else if ((ry1 - ry0 + 1) * (rx1 - rx0 + 1) > RCAP) {
+        // keep the tile's own footprint plus the widest halo m that fits
+        const int fy0c = max(fy0, 0), fy1 = min(fy0 + g.fh - 1, a.h - 1);
+        const int fx0c = max(fx0, 0), fx1 = min(fx0 + g.fw - 1, a.w - 1);
+        int m = 0;
+        while (m < 4096) {
+          const int y0n = max(ry0, fy0c - m - 1), y1n = min(ry1, fy1 + m + 1);
+          const int x0n = max(rx0, fx0c - m - 1), x1n = min(rx1, fx1 + m + 1);
+          if ((y1n - y0n + 1) * (x1n - x0n + 1) > RCAP) break;
+          ++m;
         }
-        if (!ch_ok) af[m] = zero8<T>();
+        const int y0n = max(ry0, fy0c - m), y1n = min(ry1, fy1 + m);
+        const int x0n = max(rx0, fx0c - m), x1n = min(rx1, fx1 + m);
+        if ((y1n - y0n + 1) * (x1n - x0n + 1) <= RCAP && y1n >= y0n && x1n >= x0n) {
+          ry0 = y0n;
+          ry1 = y1n;
+          rx0 = x0n;
+          rx1 = x1n;
+        } else {  // degenerate (very wide tile footprint): a 1 x 1 region, everything global
+          ry1 = ry0;
+          rx1 = rx0;
+        }
+        capped = 1;
       }
-#pragma unroll
-      for (int m = 0; m < DCN_WM; ++m)
-#pragma unroll
-        for (int b = 0; b < NBF; ++b) acc[m][b] = Ops::mma(af[m], bf[b], acc[m][b]);
+      s_reg[0] = ry0;
+      s_reg[1] = rx0;
+      s_reg[2] = ry1 - ry0 + 1;
+      s_reg[3] = rx1 - rx0 + 1;
+      s_reg[4] = capped;
     }
-  }
+    __syncthreads();
+    const int ry0 = s_reg[0], rx0 = s_reg[1], rh = s_reg[2], rw = s_reg[3];
+    const bool block_may_slow = s_reg[4] != 0;
+    const int rpix = rh * rw;
+    const float inv_rw = 1.f / (float)rw;
+    const int gq8 = (tid & 3) * 8;
+    const T* wp = (const T*)a.wpack;
 
-  // ---- 3c. samples outside a capped region: straight from global memory (rare) -----------------------
-  if (block_may_slow) {
+    // ---- 3. chunk 0 in flight while the sample records are written ------------------------------------
+    RegionTile<T, RCAP> rt;
+    WeightTile<T, BLDS ? NB : 1> wt;
+    rt.load(xb, ry0, rx0, rw, rpix, inv_rw, a.h, a.w, a.x_cs, gq8, gq8 < cin8, tid);
+    if constexpr (BLDS) wt.load(wp, co0, g.cout_pad, g.nchunk, 0, tid);
+#pragma unroll
+    for (int u = 0; u < DCN_PPT; ++u) {
+      const int k = (tid >> 7) + 2 * u;
+      if (k >= 9) break;
+      const int q = k * DCN_TILE + ppl;
+      float* w = smp_w[u];
+      const int cy0 = smp_yx[u] >> 15, cx0 = smp_yx[u] & 0x7fff;
+      const int sy = smp_st[u] >> 1, sx = smp_st[u] & 1;
+      const int ly = cy0 - ry0, lx = cx0 - rx0;
+      const bool dead = w[0] == 0.f && w[1] == 0.f && w[2] == 0.f && w[3] == 0.f;
+      unsigned o[4] = {0u, 0u, 0u, 0u};
+      unsigned char slow = 0;
+      if (!dead && ly >= 0 && ly + sy < rh && lx >= 0 && lx + sx < rw) {
+        const unsigned b0 = (unsigned)((ly * rw + lx) * PXB);
+        const unsigned bxs = (unsigned)(sx * PXB), bys = (unsigned)(sy * rw * PXB);
+        o[0] = b0;
+        o[1] = b0 + bxs;
+        o[2] = b0 + bys;
+        o[3] = b0 + bys + bxs;
+      } else {
+        slow = dead ? 0 : 1;            // the fast path skips it; the slow pass adds it
+        w[0] = w[1] = w[2] = w[3] = 0.f;
+      }
+      s_info[q] = make_info<T>(o, w);
+      s_slow[q] = slow;
+    }
+    rt.store(region, PXS, rpix, tid);
+    if constexpr (BLDS) wt.store(bsm, tid);
+
+    const int ibase = wave * (16 * DCN_WM) + row;      // this lane's pixel slot within a tap row of s_info
+    const T* wrow[NBF];                                // this lane's weight row (output channel) per fragment
+#pragma unroll
+    for (int b = 0; b < NBF; ++b) {
+      const int co = co0 + b * 16 + row;
+      wrow[b] = wp + (int64_t)(co < g.cout_pad ? co : 0) * g.nchunk * 9 * 32 + grp * 8;
+    }
     for (int c = 0; c < g.nchunk; ++c) {
-      const int ch = c * 32 + grp * 8;
-      if (ch >= cin8) continue;  // uniform per lane group; no barrier inside
+      __syncthreads();
+      if (c + 1 < g.nchunk) {  // in flight during this chunk's taps
+        const int chs = (c + 1) * 32 + gq8;
+        rt.load(xb, ry0, rx0, rw, rpix, inv_rw, a.h, a.w, a.x_cs, chs, chs < cin8, tid);
+        if constexpr (BLDS) wt.load(wp, co0, g.cout_pad, g.nchunk, c + 1, tid);
+      }
+      const bool ch_ok = c * 32 + grp * 8 < cin8;
+      frag bn[NBF];
+      if constexpr (!BLDS) {
+#pragma unroll
+        for (int b = 0; b < NBF; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9) * 32);
+      }
+      Info ic[DCN_WM], inx[DCN_WM];
+#pragma unroll
+      for (int m = 0; m < DCN_WM; ++m) inx[m] = s_info[m * 16 + ibase];
 #pragma unroll 1
       for (int k = 0; k < 9; ++k) {
-        frag af[DCN_WM];
-        bool any = false;
 #pragma unroll
-        for (int m = 0; m < DCN_WM; ++m) {
-          const int q = k * DCN_TILE + m * 16 + ibase;
-          af[m] = zero8<T>();
-          if (s_slow[q]) {
-            // recompute the sample's geometry from the offsets (rare path)
-            const int pl = m * 16 + ibase;
-            const int oy = ty0 + pl / g.tw, ox = tx0 + pl - (pl / g.tw) * g.tw;
-            const int64_t p = oy * g.wo + ox;
-            const float dy = a.offset[n * a.off_sn + p * a.off_sp + (2 * k) * a.off_sc];
-            const float dx = a.offset[n * a.off_sn + p * a.off_sp + (2 * k + 1) * a.off_sc];
-            const float mk = a.mask ? a.mask[n * a.mask_sn + p * a.mask_sp + k * a.mask_sc] : 1.f;
-            int cy0, cx0, sy, sx;
-            float w[4];
-            sample_geom((float)(oy * a.stride - a.pad + k / 3) + dy, (float)(ox * a.stride - a.pad + k % 3) + dx, mk,
-                        a.h, a.w, cy0, cx0, sy, sx, w);
-            const typename InfoOf<T>::type in = make_info<T>(0u, 0u, w);
-            const T* g0 = xb + ((int64_t)cy0 * a.w + cx0) * a.x_cs + ch;
-            af[m] = Ops::blend(ld8<T>(g0), ld8<T>(g0 + sx * a.x_cs), ld8<T>(g0 + (int64_t)sy * a.w * a.x_cs),
-                               ld8<T>(g0 + ((int64_t)sy * a.w + sx) * a.x_cs), in);
-            any = true;
+        for (int m = 0; m < DCN_WM; ++m) ic[m] = inx[m];
+        if (k < 8) {
+#pragma unroll
+          for (int m = 0; m < DCN_WM; ++m) inx[m] = s_info[(k + 1) * DCN_TILE + m * 16 + ibase];
+        }
+        frag bf[NBF];
+        if constexpr (BLDS) {
+#pragma unroll
+          for (int b = 0; b < NBF; ++b) bf[b] = b_read<T, NB>(bsm, k, b * 16 + row, grp);
+        } else {
+#pragma unroll
+          for (int b = 0; b < NBF; ++b) bf[b] = bn[b];
+          if (k < 8) {
+#pragma unroll
+            for (int b = 0; b < NBF; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9 + k + 1) * 32);
           }
         }
-        if (__builtin_amdgcn_ballot_w64(any) == 0) continue;
+        frag af[DCN_WM];
 #pragma unroll
-        for (int b = 0; b < NBF; ++b) {
-          const frag bw = ld8<T>(wrow[b] + (c * 9 + k) * 32);
+        for (int m = 0; m < DCN_WM; ++m) {
+          const char* rb = (const char*)region + grp * 8 * (int)sizeof(T);
+          const frag v0 = ld8<T>((const T*)(rb + corner(ic[m], 0)));
+          const frag v1 = ld8<T>((const T*)(rb + corner(ic[m], 1)));
+          const frag v2 = ld8<T>((const T*)(rb + corner(ic[m], 2)));
+          const frag v3 = ld8<T>((const T*)(rb + corner(ic[m], 3)));
+          af[m] = Ops::blend(v0, v1, v2, v3, ic[m]);
+          if (!ch_ok) af[m] = zero8<T>();
+        }
 #pragma unroll
-          for (int m = 0; m < DCN_WM; ++m) acc[m][b] = Ops::mma(af[m], bw, acc[m][b]);
+        for (int m = 0; m < DCN_WM; ++m)
+#pragma unroll
+          for (int b = 0; b < NBF; ++b) acc[m][b] = Ops::mma(af[m], bf[b], acc[m][b]);
+      }
+      if (c + 1 < g.nchunk) {
+        __syncthreads();  // every wave is done with this chunk's region and weights
+        rt.store(region, PXS, rpix, tid);
+        if constexpr (BLDS) wt.store(bsm, tid);
+      }
+    }
+
+    // ---- 3c. samples outside a capped region: straight from global memory (rare) ----------------------
+    if (block_may_slow) {
+      // The wave stays converged up to every MFMA (MFMA needs all 64 lanes):
+      // lanes past Cin contribute zero fragments instead of branching away.
+      for (int c = 0; c < g.nchunk; ++c) {
+        const int ch = c * 32 + grp * 8;
+        const bool ch_ok = ch < cin8;
+#pragma unroll 1
+        for (int k = 0; k < 9; ++k) {
+          frag af[DCN_WM];
+          bool any = false;
+#pragma unroll
+          for (int m = 0; m < DCN_WM; ++m) {
+            const int q = k * DCN_TILE + m * 16 + ibase;
+            af[m] = zero8<T>();
+            if (ch_ok && s_slow[q]) {
+              // recompute the sample's geometry (rare path)
+              const int pl = m * 16 + ibase;
+              const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+              const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
+              const int64_t p = (int64_t)oy * g.wo + ox;
+              float dy, dx;
+              if constexpr (MODE == MODE_FUSED) {
+                dy = s_off[pl * DCN_NOFF + 2 * k];
+                dx = s_off[pl * DCN_NOFF + 2 * k + 1];
+              } else {
+                dy = a.offset[n * a.off_sn + p * a.off_sp + (2 * k) * a.off_sc];
+                dx = a.offset[n * a.off_sn + p * a.off_sp + (2 * k + 1) * a.off_sc];
+              }
+              const float mk = a.mask ? a.mask[n * a.mask_sn + p * a.mask_sp + k * a.mask_sc] : 1.f;
+              int cy0, cx0, sy, sx;
+              float w[4];
+              sample_geom((float)(oy * a.stride - a.pad + k / 3) + dy, (float)(ox * a.stride - a.pad + k % 3) + dx,
+                          mk, a.h, a.w, cy0, cx0, sy, sx, w);
+              const unsigned o0[4] = {0u, 0u, 0u, 0u};
+              const Info in = make_info<T>(o0, w);
+              const T* g0 = xb + ((int64_t)cy0 * a.w + cx0) * a.x_cs + ch;
+              af[m] = Ops::blend(ld8<T>(g0), ld8<T>(g0 + sx * a.x_cs), ld8<T>(g0 + (int64_t)sy * a.w * a.x_cs),
+                                 ld8<T>(g0 + ((int64_t)sy * a.w + sx) * a.x_cs), in);
+              any = true;
+            }
+          }
+          if (__builtin_amdgcn_ballot_w64(any) == 0) continue;
+#pragma unroll
+          for (int b = 0; b < NBF; ++b) {
+            const frag bw = ld8<T>(wrow[b] + (c * 9 + k) * 32);
+#pragma unroll
+            for (int m = 0; m < DCN_WM; ++m) acc[m][b] = Ops::mma(af[m], bw, acc[m][b]);
+          }
         }
       }
     }
   }
 
-  // ---- 4. epilogue ---------------------------------------------------------------------------------
+  // ---- 4. epilogue: values -> LDS tile -> row-contiguous stores; GAP partials ------------------------
+  constexpr int SROW = L::SROW;
+  OutT* ost = (OutT*)region;
+  __syncthreads();  // every wave is done reading the region
+  bool pix_ok[DCN_WM][4];
+#pragma unroll
+  for (int m = 0; m < DCN_WM; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pl = wave * (16 * DCN_WM) + m * 16 + grp * 4 + i;
+      const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+      pix_ok[m][i] = pl < npx && ty0 + oyl < g.ho && tx0 + pl - oyl * g.tw < g.wo;
+    }
   float gsum[NBF];
 #pragma unroll
   for (int b = 0; b < NBF; ++b) {
     gsum[b] = 0.f;
-    const int co = co0 + b * 16 + row;
-    const bool co_ok = co < a.cout;
-    const float bias = (co_ok && a.bias) ? a.bias[co] : 0.f;
-    const float mul = (co_ok && a.post_mul) ? a.post_mul[co] : 1.f;
-    const float add = (co_ok && a.post_add) ? a.post_add[co] : 0.f;
-    const float scl = (co_ok && a.post_scale) ? a.post_scale[co] : 1.f;
+    const int col = b * 16 + row;
+    const bool co_ok = co0 + col < a.cout;
+    const float bias = s_par[0][col], mul = s_par[1][col], add = s_par[2][col], scl = s_par[3][col];
 #pragma unroll
     for (int m = 0; m < DCN_WM; ++m) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int pl = wave * (16 * DCN_WM) + m * 16 + grp * 4 + i;
-        const int oy = ty0 + pl / g.tw, ox = tx0 + pl - (pl / g.tw) * g.tw;
         float v = (acc[m][b][i] + bias) * mul + add;
         if (a.relu) v = fmaxf(v, 0.f);
         v *= scl;
-        if (co_ok && pl < g.th * g.tw && oy < g.ho && ox < g.wo) {
-          const int p = oy * g.wo + ox;
-          const OutT o = from_f32<OutT>(v);
-          if (a.out_layout == KAD_NHWC)
-            ((OutT*)a.out)[((int64_t)n * P + p) * a.out_cs + co] = o;
-          else
-            ((OutT*)a.out)[((int64_t)n * a.cout + co) * P + p] = o;
-          gsum[b] += to_f32(o);
-        }
+        const OutT o = from_f32<OutT>(v);
+        ost[pl * SROW + col] = o;
+        if (co_ok && pix_ok[m][i]) gsum[b] += to_f32(o);
       }
     }
   }
@@ -576,13 +820,52 @@ __global__ __launch_bounds__(DCN_THREADS, 2) void dcn_fwd_kernel(kad_dcn_args a,
       v += __shfl_xor(v, 32);
       if (grp == 0) gap_red[wave][b * 16 + row] = v;
     }
-    __syncthreads();
-    for (int j = tid; j < NBF * 16; j += DCN_THREADS) {
-      const int co = co0 + j;
-      if (co < a.cout) {
-        const float v = (gap_red[0][j] + gap_red[1][j]) + (gap_red[2][j] + gap_red[3][j]);
-        a.gap_partial[((int64_t)n * g.tiles + tile) * a.cout + co] = v;
+  }
+  __syncthreads();
+  OutT* out = (OutT*)a.out;
+  constexpr int VEC = 16 / (int)sizeof(OutT);
+  const bool vec_ok = a.out_layout == KAD_NHWC && (a.out_cs * (int)sizeof(OutT)) % 16 == 0 &&
+                      ((uintptr_t)a.out & 15) == 0;
+  if (vec_ok) {
+    constexpr int VPP = NB / VEC;  // 16-byte vectors per pixel
+    for (int j = tid; j < DCN_TILE * VPP; j += DCN_THREADS) {
+      const int pl = j / VPP, v = j - pl * VPP;
+      const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+      const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
+      const int co = co0 + v * VEC;
+      if (pl >= npx || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
+      const OutT* src = ost + pl * SROW + v * VEC;
+      OutT* dst = out + ((int64_t)n * P + (int64_t)oy * g.wo + ox) * a.out_cs + co;
+      if (co + VEC <= a.cout) {
+        *(intx4*)dst = *(const intx4*)src;
+      } else {
+        for (int e = 0; e < a.cout - co; ++e) dst[e] = src[e];
       }
+    }
+  } else if (a.out_layout == KAD_NHWC) {
+    for (int j = tid; j < DCN_TILE * NB; j += DCN_THREADS) {
+      const int pl = j / NB, col = j - pl * NB;
+      const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+      const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
+      const int co = co0 + col;
+      if (pl >= npx || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
+      out[((int64_t)n * P + (int64_t)oy * g.wo + ox) * a.out_cs + co] = ost[pl * SROW + col];
+    }
+  } else {  // NCHW: consecutive lanes along the tile's pixels
+    for (int j = tid; j < DCN_TILE * NB; j += DCN_THREADS) {
+      const int col = j / DCN_TILE, pl = j - col * DCN_TILE;
+      const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+      const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
+      const int co = co0 + col;
+      if (pl >= npx || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
+      out[((int64_t)n * a.cout + co) * P + (int64_t)oy * g.wo + ox] = ost[pl * SROW + col];
+    }
+  }
+  if (a.gap_partial && tid < NB) {
+    const int co = co0 + tid;
+    if (co < a.cout) {
+      const float v = (gap_red[0][tid] + gap_red[1][tid]) + (gap_red[2][tid] + gap_red[3][tid]);
+      a.gap_partial[((int64_t)n * g.tiles + tile) * a.cout + co] = v;
     }
   }
 }
@@ -613,47 +896,40 @@ static DcnGeom make_geom(const kad_dcn_args& a, int ho, int wo) {
   g.grid_x = round_up(g.tiles, 8);
   g.nchunk = ceil_div(a.cin, 32);
   g.cout_pad = round_up(a.cout, 16);
+  g.fh = (g.th - 1) * a.stride + 3;
+  g.fw = (g.tw - 1) * a.stride + 3;
+  g.inv_tw = 1.f / (float)g.tw;
+  g.inv_fw = 1.f / (float)g.fw;
   return g;
 }
 
-template <typename T, typename OutT, int NBF, bool PLAIN>
-static int launch_dcn(const kad_dcn_args& a, hipStream_t st, int ho, int wo) {
-  const DcnGeom g = make_geom(a, ho, wo);
+template <typename T, typename OutT, int NBF, int MODE>
+static int launch_dcn(const kad_dcn_args& a, hipStream_t st, const DcnGeom& g) {
   dim3 grid(g.grid_x, ceil_div(a.cout, NBF * 16), a.n);
-  hipLaunchKernelGGL((dcn_fwd_kernel<T, OutT, NBF, PLAIN>), grid, dim3(DCN_THREADS), 0, st, a, g);
-  return check_launch(PLAIN ? "kad_conv3x3_fwd" : "kad_dcn_fwd");
+  hipLaunchKernelGGL((dcn_fwd_kernel<T, OutT, NBF, MODE>), grid, dim3(DCN_THREADS), 0, st, a, g);
+  return check_launch(MODE == MODE_PLAIN ? "kad_conv3x3_fwd" : MODE == MODE_FUSED ? "kad_dsc_fwd" : "kad_dcn_fwd");
 }
 
-template <typename T>
-static int dispatch_dcn(const kad_dcn_args& a, hipStream_t st, int ho, int wo) {
+template <typename T, typename OutT, int MODE>
+static int dispatch_dcn(const kad_dcn_args& a, hipStream_t st, const DcnGeom& g) {
   const int nbf = ceil_div(a.cout, 16);
   switch (nbf < 8 ? nbf : 8) {
-    case 1: return launch_dcn<T, T, 1, false>(a, st, ho, wo);
-    case 2: return launch_dcn<T, T, 2, false>(a, st, ho, wo);
-    case 3: return launch_dcn<T, T, 3, false>(a, st, ho, wo);
-    case 4: return launch_dcn<T, T, 4, false>(a, st, ho, wo);
-    case 5: return launch_dcn<T, T, 5, false>(a, st, ho, wo);
-    case 6: return launch_dcn<T, T, 6, false>(a, st, ho, wo);
-    case 7: return launch_dcn<T, T, 7, false>(a, st, ho, wo);
-    default: return launch_dcn<T, T, 8, false>(a, st, ho, wo);
+    case 1: return launch_dcn<T, OutT, 1, MODE>(a, st, g);
+    case 2: return launch_dcn<T, OutT, 2, MODE>(a, st, g);
+    case 3: return launch_dcn<T, OutT, 3, MODE>(a, st, g);
+    case 4: return launch_dcn<T, OutT, 4, MODE>(a, st, g);
+    case 5: return launch_dcn<T, OutT, 5, MODE>(a, st, g);
+    case 6: return launch_dcn<T, OutT, 6, MODE>(a, st, g);
+    case 7: return launch_dcn<T, OutT, 7, MODE>(a, st, g);
+    default: return launch_dcn<T, OutT, 8, MODE>(a, st, g);
   }
 }
 
-template <typename T>
-static int dispatch_conv3x3(const kad_dcn_args& a, hipStream_t st, int ho, int wo) {
-  const int nbf = ceil_div(a.cout, 16);
-  switch (nbf < 8 ? nbf : 8) {
-    case 1: return launch_dcn<T, float, 1, true>(a, st, ho, wo);
-    case 2: return launch_dcn<T, float, 2, true>(a, st, ho, wo);
-    case 3: return launch_dcn<T, float, 3, true>(a, st, ho, wo);
-    case 4: return launch_dcn<T, float, 4, true>(a, st, ho, wo);
-    default: return launch_dcn<T, float, 8, true>(a, st, ho, wo);
-  }
-}
-
-static int validate_dcn(const kad_dcn_args* a, bool need_offset, int* ho_out, int* wo_out) {
+static int validate_dcn(const kad_dcn_args* a, int mode, DcnGeom* g_out) {
   KAD_CHECK_ARG(a, "null args");
-  KAD_CHECK_ARG(a->x && a->wpack && a->out && (a->offset || !need_offset), "null tensor pointer");
+  KAD_CHECK_ARG(a->x && a->wpack && a->out, "null tensor pointer");
+  KAD_CHECK_ARG(mode != MODE_EXT || a->offset, "null offset pointer");
+  KAD_CHECK_ARG(mode != MODE_FUSED || a->off_wpack, "null off_wpack pointer");
   KAD_CHECK_ARG(a->n > 0 && a->cin > 0 && a->cout > 0 && a->h > 0 && a->w > 0,
                 "bad shape n=%d cin=%d cout=%d h=%d w=%d", a->n, a->cin, a->cout, a->h, a->w);
   KAD_CHECK_ARG(a->h < 32768 && a->w < 16384, "image %dx%d too large (H < 32768, W < 16384)", a->h, a->w);
@@ -665,10 +941,12 @@ static int validate_dcn(const kad_dcn_args* a, bool need_offset, int* ho_out, in
   const int ho = (a->h + 2 * a->pad - 3) / a->stride + 1;
   const int wo = (a->w + 2 * a->pad - 3) / a->stride + 1;
   KAD_CHECK_ARG(ho > 0 && wo > 0, "empty output");
-  const uintptr_t align = (uintptr_t)a->x | (uintptr_t)a->wpack;
-  KAD_CHECK_ARG(align % 16 == 0, "x and wpack must be 16-byte aligned");
-  *ho_out = ho;
-  *wo_out = wo;
+  const uintptr_t align = (uintptr_t)a->x | (uintptr_t)a->wpack | (uintptr_t)a->off_wpack;
+  KAD_CHECK_ARG(align % 16 == 0, "x and packed weights must be 16-byte aligned");
+  *g_out = make_geom(*a, ho, wo);
+  if (mode != MODE_EXT)
+    KAD_CHECK_ARG(g_out->fh * g_out->fw <= DCN_FCAP, "stride %d not supported here (3x3 footprint of a tile %dx%d > %d px)",
+                  a->stride, g_out->fh, g_out->fw, DCN_FCAP);
   return KAD_OK;
 }
 
@@ -705,27 +983,40 @@ extern "C" int kad_dcn_pack_weights(const float* w, void* wpack, int cin, int co
 }
 
 extern "C" int kad_conv3x3_fwd(const kad_dcn_args* a, void* stream) {
-  int ho = 0, wo = 0;
-  int rc = validate_dcn(a, false, &ho, &wo);
+  DcnGeom g;
+  int rc = validate_dcn(a, MODE_PLAIN, &g);
   if (rc) return fail(rc, "kad_conv3x3_fwd: %s", kad_last_error());
   hipStream_t st = (hipStream_t)stream;
   switch (a->dtype) {
-    case KAD_F32: return dispatch_conv3x3<float>(*a, st, ho, wo);
-    case KAD_F16: return dispatch_conv3x3<half_t>(*a, st, ho, wo);
-    case KAD_BF16: return dispatch_conv3x3<bf16_t>(*a, st, ho, wo);
+    case KAD_F32: return dispatch_dcn<float, float, MODE_PLAIN>(*a, st, g);
+    case KAD_F16: return dispatch_dcn<half_t, float, MODE_PLAIN>(*a, st, g);
+    case KAD_BF16: return dispatch_dcn<bf16_t, float, MODE_PLAIN>(*a, st, g);
     default: return fail(KAD_EINVAL, "kad_conv3x3_fwd: unknown dtype %d", a->dtype);
   }
 }
 
 extern "C" int kad_dcn_fwd(const kad_dcn_args* a, void* stream) {
-  int ho = 0, wo = 0;
-  int rc = validate_dcn(a, true, &ho, &wo);
+  DcnGeom g;
+  int rc = validate_dcn(a, MODE_EXT, &g);
   if (rc) return fail(rc, "kad_dcn_fwd: %s", kad_last_error());
   hipStream_t st = (hipStream_t)stream;
   switch (a->dtype) {
-    case KAD_F32: return dispatch_dcn<float>(*a, st, ho, wo);
-    case KAD_F16: return dispatch_dcn<half_t>(*a, st, ho, wo);
-    case KAD_BF16: return dispatch_dcn<bf16_t>(*a, st, ho, wo);
+    case KAD_F32: return dispatch_dcn<float, float, MODE_EXT>(*a, st, g);
+    case KAD_F16: return dispatch_dcn<half_t, half_t, MODE_EXT>(*a, st, g);
+    case KAD_BF16: return dispatch_dcn<bf16_t, bf16_t, MODE_EXT>(*a, st, g);
     default: return fail(KAD_EINVAL, "kad_dcn_fwd: unknown dtype %d", a->dtype);
+  }
+}
+
+extern "C" int kad_dsc_fwd(const kad_dcn_args* a, void* stream) {
+  DcnGeom g;
+  int rc = validate_dcn(a, MODE_FUSED, &g);
+  if (rc) return fail(rc, "kad_dsc_fwd: %s", kad_last_error());
+  hipStream_t st = (hipStream_t)stream;
+  switch (a->dtype) {
+    case KAD_F32: return dispatch_dcn<float, float, MODE_FUSED>(*a, st, g);
+    case KAD_F16: return dispatch_dcn<half_t, half_t, MODE_FUSED>(*a, st, g);
+    case KAD_BF16: return dispatch_dcn<bf16_t, bf16_t, MODE_FUSED>(*a, st, g);
+    default: return fail(KAD_EINVAL, "kad_dsc_fwd: unknown dtype %d", a->dtype);
   }
 }

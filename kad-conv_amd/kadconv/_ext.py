@@ -35,6 +35,7 @@ class DcnArgs(ctypes.Structure):
     _fields_ = [
         ('x', c_vp), ('offset', c_vp), ('mask', c_vp), ('wpack', c_vp), ('bias', c_vp),
         ('post_mul', c_vp), ('post_add', c_vp), ('post_scale', c_vp), ('out', c_vp), ('gap_partial', c_vp),
+        ('off_wpack', c_vp), ('off_bias', c_vp),
         ('off_sn', c_i64), ('off_sp', c_i64), ('off_sc', c_i64),
         ('mask_sn', c_i64), ('mask_sp', c_i64), ('mask_sc', c_i64),
         ('n', c_int), ('cin', c_int), ('cout', c_int), ('h', c_int), ('w', c_int), ('stride', c_int), ('pad', c_int),
@@ -85,6 +86,7 @@ SIGNATURES = {
     'kad_dcn_tiles': (c_int, [c_int, c_int]),
     'kad_dcn_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_conv3x3_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
+    'kad_dsc_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_gemm_wpack_elems': (c_i64, [c_int, c_int]),
     'kad_gemm_pack_weights': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     'kad_gemm1x1_fwd': (c_int, [ctypes.POINTER(GemmArgs), c_vp]),
@@ -207,6 +209,34 @@ def dcn_fwd(x_nhwc, cin, offset, offset_strides, mask, mask_strides, wpack, cout
     if wpack.dtype != x_nhwc.dtype or out.dtype != x_nhwc.dtype:
         raise TypeError('x, packed weights and out must share a dtype')
     _check(load().kad_dcn_fwd(ctypes.byref(a), _stream()), 'kad_dcn_fwd')
+    return out
+
+
+def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, out, *, stride=1, pad=1,
+            bias=None, post_mul=None, post_add=None, post_scale=None, relu=False, out_layout=KAD_NHWC,
+            gap_partial=None):
+    """conv_offset + deformable conv in one launch (offsets never leave the chip)."""
+    _need_gpu(x_nhwc, off_wpack, wpack, out)
+    N, H, W, cs = x_nhwc.shape
+    a = DcnArgs()
+    a.x, a.mask, a.wpack = _ptr(x_nhwc), _ptr(mask), _ptr(wpack)
+    a.off_wpack, a.off_bias = _ptr(off_wpack), _ptr(off_bias)
+    a.bias, a.post_mul, a.post_add, a.post_scale = _ptr(bias), _ptr(post_mul), _ptr(post_add), _ptr(post_scale)
+    a.out, a.gap_partial = _ptr(out), _ptr(gap_partial)
+    if mask is not None:
+        a.mask_sn, a.mask_sp, a.mask_sc = mask_strides
+    a.n, a.cin, a.cout, a.h, a.w, a.stride, a.pad = N, cin, cout, H, W, stride, pad
+    a.x_cs = cs
+    a.out_layout = out_layout
+    a.out_cs = out.shape[-1] if out_layout == KAD_NHWC else cout
+    a.dtype = kad_dtype(x_nhwc.dtype)
+    a.relu = 1 if relu else 0
+    for t in (off_bias, mask, bias, post_mul, post_add, post_scale, gap_partial):
+        if t is not None and t.dtype != torch.float32:
+            raise TypeError('offset bias/mask/epilogue/gap tensors must be float32')
+    if wpack.dtype != x_nhwc.dtype or off_wpack.dtype != x_nhwc.dtype or out.dtype != x_nhwc.dtype:
+        raise TypeError('x, packed weights and out must share a dtype')
+    _check(load().kad_dsc_fwd(ctypes.byref(a), _stream()), 'kad_dsc_fwd')
     return out
 
 

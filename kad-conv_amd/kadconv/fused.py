@@ -10,8 +10,8 @@ BatchNorm folded into the DCN epilogue, LCSA parameters in one block.  Its
                     x (NCHW/NHWC) -> y_i (NHWC), plus LCSA row/column partial sums
   kad_lcsa_prep     row means, strip-conv coefficients alpha/beta
   kad_lcsa_mask     sigmoid(LCSA) mask (MFMA GEMM)        -> [N, H_i, W_i, 9] fp32
-  kad_conv3x3_fwd   conv_offset                           -> [N, H_i, W_i, 18] fp32
-  kad_dcn_fwd       DCN + bias, BN, ReLU, branch scale, GAP partials -> z_i (NHWC)
+  kad_dsc_fwd       conv_offset (kept on chip) + DCN + bias, BN, ReLU, branch
+                    scale, GAP partials                   -> z_i (NHWC)
   kad_se_mlp        channel attention from the GAP partials -> att_i
 
 then one ``kad_branch_merge``: bilinear upsample, x att, concat and + x.
@@ -111,11 +111,10 @@ class DSCPlan:
             st.append(('lcsa_prep' + tag, lambda: _ext.lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, self.cin, h, w)))
             st.append(('lcsa_mask' + tag, lambda: _ext.lcsa_mask(arow, colm, self.lcsa, emat, ebias, mask, n,
                                                                  self.cin, h, w)))
-        off = torch.empty(n, h, w, 18, dtype=torch.float32, device=dev)
-        st.append(('offset_conv' + tag, lambda: _ext.conv3x3_fwd(y, self.cin, owp, 18, off, bias=self.off_b)))
         b = self.bias if bias is None else bias
-        st.append(('dcn' + tag, lambda: _ext.dcn_fwd(
-            y, self.cin, off, (P * 18, 18, 1), mask, (P * 9, 9, 1), wp, self.cout, out, bias=b, post_mul=post_mul,
+        # conv_offset + deformable conv in one kernel: the offsets stay on chip
+        st.append(('dsc' + tag, lambda: _ext.dsc_fwd(
+            y, self.cin, owp, self.off_b, mask, (P * 9, 9, 1), wp, self.cout, out, bias=b, post_mul=post_mul,
             post_add=post_add, post_scale=post_scale, relu=relu, out_layout=out_layout, gap_partial=gap)))
         return st
 

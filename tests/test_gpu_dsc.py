@@ -1,0 +1,165 @@
+"""Parity of the one-launch DSC core (kad_dsc_fwd: conv_offset computed inside the
+tile and consumed by the deformable convolution, kad_conv.py:63-67 minus the
+mask branch) and of the plain 3x3 convolution entry (kad_conv3x3_fwd,
+kad_conv.py:55-56) against the CPU oracle.
+
+The oracle side computes the offsets with F.conv2d in float64 on the same
+quantised input and weights, then O.deform_conv2d (pinned by tests/test_oracle_dcn.py).
+Tolerances: fp32 max|d| <= 1e-4 max|ref|; fp16/bf16 max|d| <= 1e-2."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kadconv_oracle as O
+from tests._util import check_close, nhwc_padded, quant
+
+pytestmark = pytest.mark.gpu
+
+DT = {'f32': torch.float32, 'f16': torch.float16, 'bf16': torch.bfloat16}
+
+
+def _inputs(N, C, Co, H, W, seed, off_std=2.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(N, C, H, W, generator=g)
+    # offsets ~N(0, off_std) px on unit-variance input
+    ow = torch.randn(18, C, 3, 3, generator=g) * (off_std / (9 * C) ** 0.5)
+    ob = torch.randn(18, generator=g) * 0.3
+    bound = 1 / (9 * C) ** 0.5
+    w = (torch.rand(Co, C, 3, 3, generator=g) * 2 - 1) * bound
+    b = (torch.rand(Co, generator=g) * 2 - 1) * bound
+    return x, ow, ob, w, b
+
+
+def _mask(N, Ho, Wo, seed):
+    g = torch.Generator().manual_seed(seed + 1000)
+    return torch.sigmoid(torch.randn(N, 9, Ho, Wo, generator=g))
+
+
+def _ref(x, ow, ob, w, b, mask, dtype, stride=1):
+    xq = quant(x, dtype)
+    off = F.conv2d(xq, quant(ow, dtype), ob.double(), stride=stride, padding=1)
+    return O.deform_conv2d(xq, off, quant(w, dtype), b.double(), stride=stride, padding=1,
+                           mask=None if mask is None else mask.double())
+
+
+def _run_dsc(x, ow, ob, w, b, mask, dtype, stride=1, out_layout='nchw', epi=None, gap=None):
+    from kadconv import _ext
+    dev = 'cuda'
+    N, C, H, W = x.shape
+    Co = w.shape[0]
+    Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
+    xq = nhwc_padded(x.to(dtype).to(dev))
+    md = None if mask is None else mask.permute(0, 2, 3, 1).contiguous().to(dev)
+    wp = _ext.dcn_pack_weights(w.to(dtype).to(dev), dtype)
+    owp = _ext.dcn_pack_weights(ow.to(dtype).to(dev), dtype)
+    kw = {}
+    if epi is not None:
+        kw = {k: v.to(dev) for k, v in epi.items() if k != 'relu'}
+        kw['relu'] = epi.get('relu', False)
+    if out_layout == 'nchw':
+        out = torch.empty(N, Co, Ho, Wo, dtype=dtype, device=dev)
+        _ext.dsc_fwd(xq, C, owp, ob.to(dev), md, (Ho * Wo * 9, 9, 1), wp, Co, out, stride=stride, bias=b.to(dev),
+                     out_layout=_ext.KAD_NCHW, gap_partial=gap, **kw)
+        return out
+    cs = (Co + 7) // 8 * 8
+    out = torch.full((N, Ho, Wo, cs), 7.0, dtype=dtype, device=dev)
+    _ext.dsc_fwd(xq, C, owp, ob.to(dev), md, (Ho * Wo * 9, 9, 1), wp, Co, out, stride=stride, bias=b.to(dev),
+                 out_layout=_ext.KAD_NHWC, gap_partial=gap, **kw)
+    if cs > Co:  # channels past Cout belong to the caller: untouched
+        assert (out[..., Co:] == 7.0).all()
+    return out[..., :Co].permute(0, 3, 1, 2)
+
+
+@pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
+@pytest.mark.parametrize('shape', [(2, 8, 8, 9, 11), (1, 22, 22, 20, 20), (2, 86, 86, 17, 23), (1, 40, 72, 13, 7),
+                                   (1, 33, 130, 12, 70)])
+def test_dsc_small(dt, shape):
+    N, C, Co, H, W = shape
+    dtype = DT[dt]
+    x, ow, ob, w, b = _inputs(N, C, Co, H, W, seed=sum(shape))
+    mask = _mask(N, H, W, seed=sum(shape))
+    print(f'dsc_small dt={dt} shape={shape}', flush=True)
+    got = _run_dsc(x, ow, ob, w, b, mask, dtype)
+    torch.cuda.synchronize()
+    check_close(got, _ref(x, ow, ob, w, b, mask, dtype), dtype, f'{dt} {shape}')
+
+
+@pytest.mark.parametrize('dt', ['f16', 'bf16', 'f32'])
+@pytest.mark.parametrize('off_std', [0.6, 4.0])
+def test_dsc_branch0_shape(dt, off_std):
+    """KADConv(256) branch 0 at the metric's spatial size (c = 86, 100 x 100),
+    NHWC out with a padded channel stride; off_std 4 px forces capped regions
+    and the global-memory sample pass."""
+    dtype = DT[dt]
+    x, ow, ob, w, b = _inputs(2, 86, 86, 100, 100, seed=86, off_std=off_std)
+    mask = _mask(2, 100, 100, seed=86)
+    print(f'dsc_branch0 dt={dt} off_std={off_std}', flush=True)
+    got = _run_dsc(x, ow, ob, w, b, mask, dtype, out_layout='nhwc')
+    torch.cuda.synchronize()
+    check_close(got, _ref(x, ow, ob, w, b, mask, dtype), dtype, f'{dt} off_std={off_std}')
+
+
+@pytest.mark.parametrize('dt', ['f32', 'f16'])
+def test_dsc_stride2_epilogue_nomask(dt):
+    dtype = DT[dt]
+    x, ow, ob, w, b = _inputs(2, 24, 40, 15, 12, seed=11)
+    g = torch.Generator().manual_seed(5)
+    epi = {'post_mul': torch.rand(40, generator=g) + 0.5, 'post_add': torch.randn(40, generator=g) * 0.1,
+           'post_scale': torch.randn(40, generator=g), 'relu': True}
+    print(f'dsc_stride2 dt={dt}', flush=True)
+    got = _run_dsc(x, ow, ob, w, b, None, dtype, stride=2, epi=epi)
+    torch.cuda.synchronize()
+    ref = _ref(x, ow, ob, w, b, None, dtype, stride=2)
+    ref = torch.relu(ref * epi['post_mul'].double().view(1, -1, 1, 1) + epi['post_add'].double().view(1, -1, 1, 1))
+    ref = ref * epi['post_scale'].double().view(1, -1, 1, 1)
+    check_close(got, ref, dtype, f'stride2 {dt}')
+
+
+def test_dsc_gap_partials_sum_to_mean():
+    from kadconv import _ext
+    x, ow, ob, w, b = _inputs(2, 16, 20, 30, 30, seed=3)
+    mask = _mask(2, 30, 30, seed=3)
+    gap = torch.full((2, _ext.dcn_tiles(30, 30), 20), float('nan'), device='cuda')
+    out = _run_dsc(x, ow, ob, w, b, mask, torch.float32, out_layout='nhwc', gap=gap)
+    torch.cuda.synchronize()
+    got = gap.sum(1).cpu().double() / 900
+    ref = out.double().mean(dim=(2, 3)).cpu()
+    assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
+@pytest.mark.parametrize('shape,stride', [((2, 86, 18, 100, 100), 1), ((1, 40, 130, 13, 7), 1),
+                                          ((2, 24, 18, 15, 12), 2), ((1, 8, 3, 5, 64), 2)])
+def test_conv3x3(dt, shape, stride):
+    """kad_conv3x3_fwd (fp32 output, NHWC and NCHW) against F.conv2d in float64."""
+    from kadconv import _ext
+    dtype = DT[dt]
+    N, C, Co, H, W = shape
+    g = torch.Generator().manual_seed(C + Co)
+    x = torch.randn(N, C, H, W, generator=g)
+    w = torch.randn(Co, C, 3, 3, generator=g) / (9 * C) ** 0.5
+    b = torch.randn(Co, generator=g)
+    ref = F.conv2d(quant(x, dtype), quant(w, dtype), b.double(), stride=stride, padding=1)
+    Ho, Wo = ref.shape[2:]
+    dev = 'cuda'
+    xq = nhwc_padded(x.to(dtype).to(dev))
+    wp = _ext.dcn_pack_weights(w.to(dtype).to(dev), dtype)
+    print(f'conv3x3 dt={dt} shape={shape} stride={stride}', flush=True)
+    out = torch.empty(N, Ho, Wo, Co, dtype=torch.float32, device=dev)
+    _ext.conv3x3_fwd(xq, C, wp, Co, out, stride=stride, bias=b.to(dev))
+    out2 = torch.empty(N, Co, Ho, Wo, dtype=torch.float32, device=dev)
+    _ext.conv3x3_fwd(xq, C, wp, Co, out2, stride=stride, bias=b.to(dev), out_layout=_ext.KAD_NCHW)
+    torch.cuda.synchronize()
+    # fp32 accumulation of fp16/bf16 products: fp32 bar for every dtype
+    check_close(out.permute(0, 3, 1, 2), ref, torch.float32, f'conv3x3 nhwc {dt} {shape}')
+    check_close(out2, ref, torch.float32, f'conv3x3 nchw {dt} {shape}')
+
+
+def test_dsc_rejects_stride3():
+    from kadconv import _ext
+    x = torch.zeros(1, 64, 64, 8, dtype=torch.float16, device='cuda')
+    wp = torch.zeros(_ext.dcn_wpack_elems(8, 8), dtype=torch.float16, device='cuda')
+    owp = torch.zeros(_ext.dcn_wpack_elems(8, 18), dtype=torch.float16, device='cuda')
+    out = torch.empty(1, 22, 22, 8, dtype=torch.float16, device='cuda')
+    with pytest.raises(RuntimeError, match='stride 3'):
+        _ext.dsc_fwd(x, 8, owp, None, None, (0, 0, 0), wp, 8, out, stride=3)

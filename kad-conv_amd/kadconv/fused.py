@@ -183,7 +183,14 @@ class KADConvPlan:
         return x.shape[2] >= s and x.shape[3] >= s
 
     def stages(self, x):
-        """The fused forward as (name, launch) pairs; returns (stages, out)."""
+        """The fused forward as (name, launch) pairs in stream order; returns (stages, out)."""
+        pre, branches, post, out = self.schedule(x)
+        return pre + [s for b in branches for s in b] + post, out
+
+    def schedule(self, x):
+        """(pre, [per-branch stages], post, out): the branch chains only depend on
+        `pre` (the pyramid) and `post` (the merge) depends on all of them, so
+        forward() runs the chains on side streams concurrently."""
         N, C, H, W = x.shape
         dev, dtype = x.device, x.dtype
         nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
@@ -211,23 +218,54 @@ class KADConvPlan:
             pyr.append({'wpack': br.proj_packed(dtype), 'bias': br.proj_b, 'cout': br.c, 'out': y,
                         'rowpart': rows, 'colpart': cols})
         st.append(('pyramid', lambda: _ext.pyramid_proj(xin, in_layout, C, pyr)))
+        chains = []
         for i, br in enumerate(self.branches):
             h, w = H >> i, W >> i
             P = h * w
             z = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
             tiles = _ext.dcn_tiles(h, w)
             gap = torch.empty(N, tiles, br.c, dtype=torch.float32, device=dev)
-            st += br.dsc.stages(ys[i], N, h, w, z, _ext.KAD_NHWC, post_mul=br.bn_a, post_add=br.bn_b,
-                                post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i])
+            ch = br.dsc.stages(ys[i], N, h, w, z, _ext.KAD_NHWC, post_mul=br.bn_a, post_add=br.bn_b,
+                               post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i])
             att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
-            st.append((f'se{i}', lambda gap=gap, tiles=tiles, P=P, br=br, att=att: _ext.se_mlp(
+            ch.append((f'se{i}', lambda gap=gap, tiles=tiles, P=P, br=br, att=att: _ext.se_mlp(
                 gap, tiles, 1.0 / P, br.w1, br.b1, br.w2, br.b2, att, N, br.c, br.hid)))
+            chains.append(ch)
             merged.append({'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att})
-        st.append(('merge', lambda: _ext.branch_merge(out_v, out_layout, merged, residual=xin)))
-        return st, out
+        post = [('merge', lambda: _ext.branch_merge(out_v, out_layout, merged, residual=xin))]
+        return st, chains, post, out
+
+    def _side_streams(self, dev):
+        """One side stream per branch chain (default priority), created once per device."""
+        key = torch.device(dev).index
+        streams = getattr(self, '_side', {})
+        if key not in streams:
+            streams[key] = [torch.cuda.Stream(device=dev) for _ in self.branches]
+            self._side = streams
+        return streams[key]
 
     def forward(self, x):
-        st, out = self.stages(x)
-        for _, fn in st:
+        """pyramid on the caller's stream, the branch chains forked onto side
+        streams (concurrent on the GPU; HIP-graph capture records the fork/join
+        as graph edges), merge after the join."""
+        pre, chains, post, out = self.schedule(x)
+        for _, fn in pre:
+            fn()
+        main = torch.cuda.current_stream(x.device)
+        side = self._side_streams(x.device)
+        fork = torch.cuda.Event()
+        fork.record(main)
+        joins = []
+        for s, chain in zip(side, chains):
+            s.wait_event(fork)
+            with torch.cuda.stream(s):
+                for _, fn in chain:
+                    fn()
+            ev = torch.cuda.Event()
+            ev.record(s)
+            joins.append(ev)
+        for ev in joins:
+            main.wait_event(ev)
+        for _, fn in post:
             fn()
         return out

@@ -257,6 +257,7 @@ typedef struct kad_merge_args {
   const void *residual;    /* same layout as out, or NULL */
   const float *gate;       /* [C] per-channel output multiplier, or NULL */
   int n, c, h, w, layout, dtype, nbranch;
+  int c_begin, c_end;      /* output channels written: [c_begin, c_end); 0, 0 = all of [0, C) */
   const void *br_z[KAD_MAX_BRANCHES];    /* NHWC [N][h_b][w_b][cs_b], dtype */
   const float *br_att[KAD_MAX_BRANCHES]; /* [N][c_b] or NULL */
   int br_c[KAD_MAX_BRANCHES], br_c_off[KAD_MAX_BRANCHES];
@@ -265,7 +266,9 @@ typedef struct kad_merge_args {
 } kad_merge_args;
 
 /* out[n, c] = gate[c] * (residual + sum over branches b with c in [c_off_b, c_off_b + c_b):
- *   coeff_b * att_b[n, c - c_off_b] * bilinear_up(z_b)[c - c_off_b]).
+ *   coeff_b * att_b[n, c - c_off_b] * bilinear_up(z_b)[c - c_off_b])
+ * for c in [c_begin, c_end); other channels of out are not touched, so one
+ * call per branch can merge each branch as soon as it is ready.
  * KADConv's tail `F.interpolate(..., align_corners=False)`, `torch.cat` and `+ x`
  * (kad_conv.py:117-121); reference k_upsample_bilinear_att + k_cat_residual_att0
  * (acceleration/kadc_fused_sm75.py:1245-1331). */

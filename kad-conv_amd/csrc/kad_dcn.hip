@@ -260,7 +260,8 @@ template <typename T, typename OutT, int NBF, int MODE> struct DcnLds {
   static constexpr int NB = NBF * 16;
   static constexpr int PXS = sizeof(T) == 2 ? 40 : 36;  // elements per region pixel (32 + pad: conflict-free rows)
   static constexpr int PXB = PXS * (int)sizeof(T);
-  static constexpr int BCOLS = NB > 32 ? NB : 32;  // >= 32: FUSED stages the offset weights here too
+  // FUSED 16-bit stages the 18 offset filters of up to 3 chunks here first (9 x 18 x 104 elements)
+  static constexpr int BCOLS = (MODE == MODE_FUSED && BLDS) ? (NB > 64 ? NB : 64) : (NB > 32 ? NB : 32);
   static constexpr int BSM = BLDS ? 9 * BCOLS * 32 : 8;
   static constexpr int NINFO = MODE == MODE_PLAIN ? 1 : DCN_NPAIR;
   static constexpr int NOFF = MODE == MODE_FUSED ? DCN_TILE * DCN_NOFF : 1;
@@ -268,61 +269,106 @@ template <typename T, typename OutT, int NBF, int MODE> struct DcnLds {
   static constexpr int FIXED = BSM * (int)sizeof(T) + NINFO * ((int)sizeof(typename InfoOf<T>::type) + 1) +
                                NOFF * 4 + 2 * 4 * NB * 4 + 256;
   static constexpr int STAGE_PX = (DCN_TILE * SROW * (int)sizeof(OutT) + PXB - 1) / PXB;
-  static constexpr int RCAP_WANT = STAGE_PX > 768 ? STAGE_PX : 768;  // region staging uses RCAP / 64 pieces per thread
-  static constexpr int RCAP = (DCN_LDS - FIXED) / PXB < RCAP_WANT ? (DCN_LDS - FIXED) / PXB : RCAP_WANT;
+  // region staging uses RCAP / 64 pieces per thread; the epilogue tile reuses the region
+  static constexpr int RCAP_WANT = (STAGE_PX > 768 ? STAGE_PX : 768) + 63 - ((STAGE_PX > 768 ? STAGE_PX : 768) + 63) % 64;
+  static constexpr int RCAP_FIT = (DCN_LDS - FIXED) / PXB < RCAP_WANT ? (DCN_LDS - FIXED) / PXB : RCAP_WANT;
+  static constexpr int RCAP = RCAP_FIT / 64 * 64;    // staging slots come in 64-pixel rows
   static_assert(RCAP >= DCN_FCAP, "footprint must fit the region buffer");
   static_assert(MODE == MODE_PLAIN || sizeof(T) == 4 || RCAP * PXB <= 65536, "16-bit corner offsets");
   static_assert(RCAP * PXB >= DCN_TILE * SROW * (int)sizeof(OutT), "epilogue tile must fit the region buffer");
 };
 
-// Chunk staging: NPIX region pixels x 32 channels, 16-byte pieces, prefetched in registers.
+// ---- buffer loads ------------------------------------------------------------------------------
+// A raw buffer load returns 0 for a byte offset at or past the descriptor's
+// size, so pieces outside the image (padding ring, channels past Cin, unused
+// staging slots) are staged as zeros with no branch; per-thread byte offsets are
+// computed once per block and only shifted per channel chunk.
+constexpr uint32_t DCN_OOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <typename T>
+__device__ __forceinline__ typename DcnFrag<T>::frag buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  typedef typename DcnFrag<T>::frag F;
+  if constexpr (sizeof(T) == 4) {
+    F f;
+    f.lo = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+    f.hi = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, 0, 0));
+    return f;
+  } else {
+    return __builtin_bit_cast(F, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+  }
+}
+
+// Chunk staging: up to CAP region pixels x 32 channels, 8-channel pieces,
+// prefetched in registers; piece u of thread t is pixel t / 4 + 64 u, channel
+// group t % 4.  CAP is a multiple of 64 and the LDS buffer holds CAP pixels, so
+// every slot is stored (unused slots receive zeros).
 template <typename T, int CAP> struct RegionTile {
-  static constexpr int RPT = (CAP + DCN_THREADS / 4 - 1) / (DCN_THREADS / 4);
+  static_assert(CAP % (DCN_THREADS / 4) == 0, "CAP must be a multiple of 64");
+  static constexpr int RPT = CAP / (DCN_THREADS / 4);
   typename DcnFrag<T>::frag v[RPT];
-  // rows x cols pixels starting at (y0, x0) (may extend outside the image: zeros)
-  __device__ __forceinline__ void load(const T* xb, int y0, int x0, int cols, int npix, float inv_cols, int h, int w,
-                                       int x_cs, int chs, bool chs_ok, int tid) {
+  uint32_t voff[RPT];  // byte offset of the piece's chunk-0 channels in the image, or DCN_OOB
+  // npix = rows x cols pixels starting at (y0, x0); parts outside the image read 0
+  __device__ __forceinline__ void setup(int y0, int x0, int cols, int npix, float inv_cols, int h, int w, int x_cs,
+                                        int tid) {
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       const int q = (tid >> 2) + u * (DCN_THREADS / 4);
-      v[u] = zero8<T>();
-      if (q < npix && chs_ok) {
+      uint32_t o = DCN_OOB;
+      if (q < npix) {
         const int qy = (int)(((float)q + 0.5f) * inv_cols);
         const int gy = y0 + qy, gx = x0 + q - qy * cols;
-        if (gy >= 0 && gy < h && gx >= 0 && gx < w) v[u] = ld8<T>(xb + ((int64_t)gy * w + gx) * x_cs + chs);
+        if (gy >= 0 && gy < h && gx >= 0 && gx < w)
+          o = (uint32_t)(((gy * w + gx) * x_cs + (tid & 3) * 8) * (int)sizeof(T));
       }
+      voff[u] = o;
     }
   }
-  __device__ __forceinline__ void store(T* region, int pxs, int npix, int tid) {
+  // chunk c; chs_ok = this thread's channel group holds real channels in chunk c
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int c, bool chs_ok) {
+    const uint32_t cofs = (uint32_t)(c * 32 * (int)sizeof(T));
 #pragma unroll
-    for (int u = 0; u < RPT; ++u) {
-      const int q = (tid >> 2) + u * (DCN_THREADS / 4);
-      if (q < npix) st8<T>(region + q * pxs + (tid & 3) * 8, v[u]);
-    }
+    for (int u = 0; u < RPT; ++u) v[u] = buf_ld8<T>(r, chs_ok ? voff[u] + cofs : DCN_OOB);
+  }
+  __device__ __forceinline__ void store(T* region, int pxs, int tid) {
+    T* base = region + (tid >> 2) * pxs + (tid & 3) * 8;
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) st8<T>(base + u * (DCN_THREADS / 4) * pxs, v[u]);
   }
 };
 
-// Chunk weights [9][NBC][32] (16-bit paths), swizzled 16-byte pieces.
+// Chunk weights [9][NBC][32] (16-bit paths), swizzled 16-byte pieces, from the
+// packed layout [Cout_pad][nchunk][9][32].
 template <typename T, int NBC> struct WeightTile {
   static constexpr int PIECES = 9 * NBC * 4;
   static constexpr int BPT = (PIECES + DCN_THREADS - 1) / DCN_THREADS;
   typename DcnFrag<T>::frag v[BPT];
-  __device__ __forceinline__ void load(const T* wpk, int co0, int cpad, int nchunk, int c, int tid) {
+  uint32_t voff[BPT];
+  __device__ __forceinline__ void setup(int co0, int cpad, int nchunk, int tid) {
 #pragma unroll
     for (int u = 0; u < BPT; ++u) {
       const int e = tid + u * DCN_THREADS;
-      v[u] = zero8<T>();
+      uint32_t o = DCN_OOB;
       if (e < PIECES) {
         const int k = e / (NBC * 4), r = e - k * (NBC * 4), co = co0 + (r >> 2);
-        if (co < cpad) v[u] = ld8<T>(wpk + ((int64_t)(co * nchunk + c) * 9 + k) * 32 + (r & 3) * 8);
+        if (co < cpad) o = (uint32_t)((((co * nchunk) * 9 + k) * 32 + (r & 3) * 8) * (int)sizeof(T));
       }
+      voff[u] = o;
     }
+  }
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int c) {
+    const uint32_t cofs = (uint32_t)(c * 9 * 32 * (int)sizeof(T));
+#pragma unroll
+    for (int u = 0; u < BPT; ++u) v[u] = buf_ld8<T>(r, voff[u] + cofs);
   }
   __device__ __forceinline__ void store(T* bsm, int tid) {
 #pragma unroll
     for (int u = 0; u < BPT; ++u) {
       const int e = tid + u * DCN_THREADS;
-      if (e < PIECES) {
+      if ((u + 1) * DCN_THREADS <= PIECES || e < PIECES) {
         const int k = e / (NBC * 4), r = e - k * (NBC * 4), col = r >> 2;
         st8<T>(bsm + ((k * NBC + col) * 4 + ((r & 3) ^ ((col >> 1) & 3))) * 8, v[u]);
       }
@@ -337,10 +383,12 @@ __device__ __forceinline__ typename DcnFrag<T>::frag b_read(const T* bsm, int k,
 
 // ---- plain 3x3 convolution of one tile (footprint staged per chunk) -------------------------------
 // acc[m][b] += sum over taps/chunks of x[footprint] * W[co0 + 16 b + row]; the
-// footprint origin is (fy0, fx0) (may be negative: zero padding).
-template <typename T, int NBP, int PXS, int RCAP>
-__device__ __forceinline__ void plain_conv(floatx4 (&acc)[DCN_WM][NBP], const T* xb, const T* wpk, int co0, int cpad,
-                                           int nchunk, int cin8, int h, int w, int x_cs, int stride, int fy0, int fx0,
+// footprint origin is (fy0, fx0) (may be negative: zero padding).  rx covers
+// the image, rw the packed weights [cpad][nchunk][9][32].
+template <typename T, int NBP, int PXS>
+__device__ __forceinline__ void plain_conv(floatx4 (&acc)[DCN_WM][NBP], __amdgpu_buffer_rsrc_t rx,
+                                           __amdgpu_buffer_rsrc_t rw, const T* wpk, int co0, int cpad, int nchunk,
+                                           int cin8, int h, int w, int x_cs, int stride, int fy0, int fx0,
                                            const DcnGeom& g, T* region, T* bsm) {
   typedef DcnFrag<T> Ops;
   typedef typename Ops::frag frag;
@@ -367,18 +415,20 @@ __device__ __forceinline__ void plain_conv(floatx4 (&acc)[DCN_WM][NBP], const T*
   RegionTile<T, DCN_FCAP> rt;
   WeightTile<T, BLDS ? NBC : 1> wt;
   const int gq8 = (tid & 3) * 8;
-  rt.load(xb, fy0, fx0, g.fw, fpix, g.inv_fw, h, w, x_cs, gq8, gq8 < cin8, tid);
-  if constexpr (BLDS) wt.load(wpk, co0, cpad, nchunk, 0, tid);
-  rt.store(region, PXS, fpix, tid);
+  rt.setup(fy0, fx0, g.fw, fpix, g.inv_fw, h, w, x_cs, tid);
+  rt.load(rx, 0, gq8 < cin8);
+  if constexpr (BLDS) {
+    wt.setup(co0, cpad, nchunk, tid);
+    wt.load(rw, 0);
+  }
+  rt.store(region, PXS, tid);
   if constexpr (BLDS) wt.store(bsm, tid);
   for (int c = 0; c < nchunk; ++c) {
     __syncthreads();
     if (c + 1 < nchunk) {
-      const int chs = (c + 1) * 32 + gq8;
-      rt.load(xb, fy0, fx0, g.fw, fpix, g.inv_fw, h, w, x_cs, chs, chs < cin8, tid);
-      if constexpr (BLDS) wt.load(wpk, co0, cpad, nchunk, c + 1, tid);
+      rt.load(rx, c + 1, (c + 1) * 32 + gq8 < cin8);
+      if constexpr (BLDS) wt.load(rw, c + 1);
     }
-    const bool ch_ok = c * 32 + grp * 8 < cin8;
     frag bn[NBP];
     if constexpr (!BLDS) {
 #pragma unroll
@@ -402,10 +452,7 @@ __device__ __forceinline__ void plain_conv(floatx4 (&acc)[DCN_WM][NBP], const T*
       const int toff = (ky * g.fw + kx) * PXB;
       frag af[DCN_WM];
 #pragma unroll
-      for (int m = 0; m < DCN_WM; ++m) {
-        af[m] = ld8<T>((const T*)((const char*)region + abase[m] + toff));
-        if (!ch_ok) af[m] = zero8<T>();
-      }
+      for (int m = 0; m < DCN_WM; ++m) af[m] = ld8<T>((const T*)((const char*)region + abase[m] + toff));
 #pragma unroll
       for (int m = 0; m < DCN_WM; ++m)
 #pragma unroll
@@ -417,9 +464,107 @@ __device__ __forceinline__ void plain_conv(floatx4 (&acc)[DCN_WM][NBP], const T*
     }
     if (c + 1 < nchunk) {
       __syncthreads();
-      rt.store(region, PXS, fpix, tid);
+      rt.store(region, PXS, tid);
       if constexpr (BLDS) wt.store(bsm, tid);
     }
+  }
+}
+
+// ---- conv_offset of one tile, 16-bit input ------------------------------------------------------------
+// Up to 3 channel chunks per round trip: the footprint [fpix][GS] goes to
+// `region` and the 18 offset filters [9 taps][18][GS] to `bsm` (GS = 32 G + 8
+// elements: rows 16 bytes apart in bank space, conflict-free for consecutive
+// pixels / filters), all loads of a group issued at once; then 9 G k-steps of
+// 2 x 2 MFMA with no barrier in between.  oacc[m][b]: offset channel 16 b + row.
+template <typename T, int REGION_BYTES, int BSM_BYTES>
+__device__ __forceinline__ void offset_conv16(floatx4 (&oacc)[DCN_WM][2], __amdgpu_buffer_rsrc_t rx,
+                                              __amdgpu_buffer_rsrc_t rw, int nchunk, int cin8, int h, int w,
+                                              int x_cs, int stride, int fy0, int fx0, const DcnGeom& g, T* region,
+                                              T* bsm) {
+  typedef DcnFrag<T> Ops;
+  typedef typename Ops::frag frag;
+  constexpr int NTF = 12, NTW = 8;           // footprint / filter pieces per thread per round
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = lane & 15, grp = lane >> 4;
+  const int fpix = g.fh * g.fw;
+  int apix[DCN_WM];
+#pragma unroll
+  for (int m = 0; m < DCN_WM; ++m) {
+    int pl = wave * (16 * DCN_WM) + m * 16 + row;
+    if (pl >= g.th * g.tw) pl = 0;
+    const int py = (int)(((float)pl + 0.5f) * g.inv_tw), px = pl - py * g.tw;
+    apix[m] = (py * stride) * g.fw + px * stride;
+  }
+  for (int c0 = 0; c0 < nchunk;) {
+    int G = nchunk - c0 < 3 ? nchunk - c0 : 3;
+    while (G > 1 && (fpix * (32 * G + 8) * (int)sizeof(T) > REGION_BYTES ||
+                     9 * DCN_NOFF * (32 * G + 8) * (int)sizeof(T) > BSM_BYTES))
+      --G;
+    const int GS = 32 * G + 8, P4 = 4 * G;
+    const float inv_p4 = 1.f / (float)P4;
+    const int np = fpix * P4, nw = 9 * DCN_NOFF * P4;
+    // one descriptor per pass (a buffer descriptor must be wave-uniform)
+    for (int fb = 0, wb = 0; fb < np || wb < nw; fb += NTF * DCN_THREADS, wb += NTW * DCN_THREADS) {
+      frag vf[NTF], vw[NTW];
+#pragma unroll
+      for (int t = 0; t < NTF; ++t) {  // footprint piece: pixel q, 8 channels r of the group
+        const int e = fb + tid + t * DCN_THREADS;
+        uint32_t o = DCN_OOB;
+        if (e < np) {
+          const int q = (int)(((float)e + 0.5f) * inv_p4), r = e - q * P4;
+          const int qy = (int)(((float)q + 0.5f) * g.inv_fw), qx = q - qy * g.fw;
+          const int gy = fy0 + qy, gx = fx0 + qx, ch = c0 * 32 + r * 8;
+          if (gy >= 0 && gy < h && gx >= 0 && gx < w && ch < cin8)
+            o = (uint32_t)(((gy * w + gx) * x_cs + ch) * (int)sizeof(T));
+        }
+        vf[t] = buf_ld8<T>(rx, o);
+      }
+#pragma unroll
+      for (int t = 0; t < NTW; ++t) {  // filter piece: tap k, filter col, 8 channels r
+        const int f = wb + tid + t * DCN_THREADS;
+        uint32_t o = DCN_OOB;
+        if (f < nw) {
+          const int kc = (int)(((float)f + 0.5f) * inv_p4), r = f - kc * P4;
+          const int k = kc / DCN_NOFF, col = kc - k * DCN_NOFF;
+          o = (uint32_t)((((col * nchunk + c0 + (r >> 2)) * 9 + k) * 32 + (r & 3) * 8) * (int)sizeof(T));
+        }
+        vw[t] = buf_ld8<T>(rw, o);
+      }
+#pragma unroll
+      for (int t = 0; t < NTF; ++t) {
+        const int e = fb + tid + t * DCN_THREADS;
+        if (e < np) {
+          const int q = (int)(((float)e + 0.5f) * inv_p4), r = e - q * P4;
+          st8<T>(region + q * GS + r * 8, vf[t]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NTW; ++t) {
+        const int f = wb + tid + t * DCN_THREADS;
+        if (f < nw) {
+          const int kc = (int)(((float)f + 0.5f) * inv_p4), r = f - kc * P4;
+          st8<T>(bsm + kc * GS + r * 8, vw[t]);
+        }
+      }
+    }
+    __syncthreads();
+    for (int gi = 0; gi < G; ++gi) {
+      const int cofs = gi * 32 + grp * 8;
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {  // unrolled: the scheduler runs LDS reads ahead of the MFMAs
+        const frag b0 = ld8<T>(bsm + (k * DCN_NOFF + row) * GS + cofs);
+        frag b1 = zero8<T>();
+        if (row < DCN_NOFF - 16) b1 = ld8<T>(bsm + (k * DCN_NOFF + 16 + row) * GS + cofs);
+        const int toff = (k / 3) * g.fw + k % 3;
+#pragma unroll
+        for (int m = 0; m < DCN_WM; ++m) {
+          const frag af = ld8<T>(region + (apix[m] + toff) * GS + cofs);
+          oacc[m][0] = Ops::mma(af, b0, oacc[m][0]);
+          oacc[m][1] = Ops::mma(af, b1, oacc[m][1]);
+        }
+      }
+    }
+    __syncthreads();  // footprint / filters consumed before the next group (or the caller) reuses them
+    c0 += G;
   }
 }
 
@@ -456,6 +601,9 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   const int row = lane & 15, grp = lane >> 4;
   const T* xb = (const T*)a.x + (int64_t)n * a.h * a.w * a.x_cs;
   const int cin8 = round_up(a.cin, 8);
+  const T* wp = (const T*)a.wpack;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xb, (uint32_t)(a.h * a.w * a.x_cs * (int)sizeof(T)));
+  const __amdgpu_buffer_rsrc_t rwp = make_rsrc(wp, (uint32_t)(g.cout_pad * g.nchunk * 9 * 32 * (int)sizeof(T)));
   const int fy0 = ty0 * a.stride - a.pad, fx0 = tx0 * a.stride - a.pad;
 
   // ---- 0. independent loads ------------------------------------------------------------------------
@@ -491,9 +639,10 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       }
     }
   }
-  if (tid < NB) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) s_par[j][tid] = par[j];
+  if (tid < NB) {  // v = acc * mul + (bias * mul + add)
+    s_par[0][tid] = par[0] * par[1] + par[2];
+    s_par[1][tid] = par[1];
+    s_par[3][tid] = par[3];
   }
   if (tid == 0) {
     s_box[0] = 0x7fffffff;
@@ -510,16 +659,21 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
 
   if constexpr (MODE == MODE_PLAIN) {
     // ---- 1. plain 3x3 convolution -----------------------------------------------------------------
-    plain_conv<T, NBF, PXS, RCAP>(acc, xb, (const T*)a.wpack, co0, g.cout_pad, g.nchunk, cin8, a.h, a.w, a.x_cs,
-                                  a.stride, fy0, fx0, g, region, bsm);
+    plain_conv<T, NBF, PXS>(acc, rx, rwp, wp, co0, g.cout_pad, g.nchunk, cin8, a.h, a.w, a.x_cs, a.stride, fy0, fx0,
+                            g, region, bsm);
   } else {
     if constexpr (MODE == MODE_FUSED) {
       // ---- 1. offsets = conv_offset(x) over the tile ----------------------------------------------------
       floatx4 oacc[DCN_WM][2];
 #pragma unroll
       for (int m = 0; m < DCN_WM; ++m) oacc[m][0] = oacc[m][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-      plain_conv<T, 2, PXS, RCAP>(oacc, xb, (const T*)a.off_wpack, 0, 32, g.nchunk, cin8, a.h, a.w, a.x_cs,
-                                  a.stride, fy0, fx0, g, region, bsm);
+      const __amdgpu_buffer_rsrc_t rwo = make_rsrc(a.off_wpack, (uint32_t)(32 * g.nchunk * 9 * 32 * (int)sizeof(T)));
+      if constexpr (BLDS)
+        offset_conv16<T, RCAP * PXB, L::BSM * (int)sizeof(T)>(oacc, rx, rwo, g.nchunk, cin8, a.h, a.w, a.x_cs,
+                                                               a.stride, fy0, fx0, g, region, bsm);
+      else
+        plain_conv<T, 2, PXS>(oacc, rx, rwo, (const T*)a.off_wpack, 0, 32, g.nchunk, cin8, a.h, a.w, a.x_cs,
+                              a.stride, fy0, fx0, g, region, bsm);
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         const int ch = b * 16 + row;
@@ -622,13 +776,16 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
     const int rpix = rh * rw;
     const float inv_rw = 1.f / (float)rw;
     const int gq8 = (tid & 3) * 8;
-    const T* wp = (const T*)a.wpack;
 
     // ---- 3. chunk 0 in flight while the sample records are written ------------------------------------
     RegionTile<T, RCAP> rt;
     WeightTile<T, BLDS ? NB : 1> wt;
-    rt.load(xb, ry0, rx0, rw, rpix, inv_rw, a.h, a.w, a.x_cs, gq8, gq8 < cin8, tid);
-    if constexpr (BLDS) wt.load(wp, co0, g.cout_pad, g.nchunk, 0, tid);
+    rt.setup(ry0, rx0, rw, rpix, inv_rw, a.h, a.w, a.x_cs, tid);
+    rt.load(rx, 0, gq8 < cin8);
+    if constexpr (BLDS) {
+      wt.setup(co0, g.cout_pad, g.nchunk, tid);
+      wt.load(rwp, 0);
+    }
 #pragma unroll
     for (int u = 0; u < DCN_PPT; ++u) {
       const int k = (tid >> 7) + 2 * u;
@@ -655,7 +812,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       s_info[q] = make_info<T>(o, w);
       s_slow[q] = slow;
     }
-    rt.store(region, PXS, rpix, tid);
+    rt.store(region, PXS, tid);
     if constexpr (BLDS) wt.store(bsm, tid);
 
     const int ibase = wave * (16 * DCN_WM) + row;      // this lane's pixel slot within a tap row of s_info
@@ -668,11 +825,10 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
     for (int c = 0; c < g.nchunk; ++c) {
       __syncthreads();
       if (c + 1 < g.nchunk) {  // in flight during this chunk's taps
-        const int chs = (c + 1) * 32 + gq8;
-        rt.load(xb, ry0, rx0, rw, rpix, inv_rw, a.h, a.w, a.x_cs, chs, chs < cin8, tid);
-        if constexpr (BLDS) wt.load(wp, co0, g.cout_pad, g.nchunk, c + 1, tid);
+        rt.load(rx, c + 1, (c + 1) * 32 + gq8 < cin8);
+        if constexpr (BLDS) wt.load(rwp, c + 1);
       }
-      const bool ch_ok = c * 32 + grp * 8 < cin8;
+      // lanes whose channel group lies past Cin read staged zeros: no masking needed
       frag bn[NBF];
       if constexpr (!BLDS) {
 #pragma unroll
@@ -710,7 +866,6 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
           const frag v2 = ld8<T>((const T*)(rb + corner(ic[m], 2)));
           const frag v3 = ld8<T>((const T*)(rb + corner(ic[m], 3)));
           af[m] = Ops::blend(v0, v1, v2, v3, ic[m]);
-          if (!ch_ok) af[m] = zero8<T>();
         }
 #pragma unroll
         for (int m = 0; m < DCN_WM; ++m)
@@ -719,7 +874,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       }
       if (c + 1 < g.nchunk) {
         __syncthreads();  // every wave is done with this chunk's region and weights
-        rt.store(region, PXS, rpix, tid);
+        rt.store(region, PXS, tid);
         if constexpr (BLDS) wt.store(bsm, tid);
       }
     }
@@ -797,13 +952,13 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
     gsum[b] = 0.f;
     const int col = b * 16 + row;
     const bool co_ok = co0 + col < a.cout;
-    const float bias = s_par[0][col], mul = s_par[1][col], add = s_par[2][col], scl = s_par[3][col];
+    const float shift = s_par[0][col], mul = s_par[1][col], scl = s_par[3][col];
 #pragma unroll
     for (int m = 0; m < DCN_WM; ++m) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int pl = wave * (16 * DCN_WM) + m * 16 + grp * 4 + i;
-        float v = (acc[m][b][i] + bias) * mul + add;
+        float v = fmaf(acc[m][b][i], mul, shift);
         if (a.relu) v = fmaxf(v, 0.f);
         v *= scl;
         const OutT o = from_f32<OutT>(v);
@@ -933,6 +1088,9 @@ static int validate_dcn(const kad_dcn_args* a, int mode, DcnGeom* g_out) {
   KAD_CHECK_ARG(a->n > 0 && a->cin > 0 && a->cout > 0 && a->h > 0 && a->w > 0,
                 "bad shape n=%d cin=%d cout=%d h=%d w=%d", a->n, a->cin, a->cout, a->h, a->w);
   KAD_CHECK_ARG(a->h < 32768 && a->w < 16384, "image %dx%d too large (H < 32768, W < 16384)", a->h, a->w);
+  KAD_CHECK_ARG((int64_t)a->h * a->w * a->x_cs * dtype_size(a->dtype) < ((int64_t)1 << 31) &&
+                    (int64_t)round_up(a->cout, 16) * ceil_div(a->cin, 32) * 288 * dtype_size(a->dtype) < ((int64_t)1 << 31),
+                "one image (or the packed weights) exceeds 2 GB");
   KAD_CHECK_ARG(a->stride >= 1 && a->pad >= 0, "bad stride=%d pad=%d", a->stride, a->pad);
   KAD_CHECK_ARG(a->x_cs % 8 == 0 && a->x_cs >= round_up(a->cin, 8),
                 "x channel stride %d must be a multiple of 8 and >= roundup(cin=%d, 8)", a->x_cs, a->cin);

@@ -137,8 +137,8 @@ __global__ __launch_bounds__(256) void merge_nchw_kernel(kad_merge_args a) {
   const int tid = threadIdx.x;
   const int xb = blockIdx.x * MG_XS;
   const int y = blockIdx.y;
-  const int nch = ceil_div(a.c, MG_CH);
-  const int c0 = (blockIdx.z % nch) * MG_CH;
+  const int nch = ceil_div(a.c_end - a.c_begin, MG_CH);
+  const int c0 = a.c_begin + (blockIdx.z % nch) * MG_CH;
   const int n = blockIdx.z / nch;
   const int xe = (xb + MG_XS < a.w) ? xb + MG_XS : a.w;
   int sx_lo[KAD_MAX_BRANCHES];
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void merge_nchw_kernel(kad_merge_args a) {
 #pragma unroll
     for (int b = 0; b < KAD_MAX_BRANCHES; ++b) {
       float sc = 0.f;
-      if (b < a.nbranch && c < a.c) {
+      if (b < a.nbranch && c < a.c_end) {
         const int cb = c - a.br_c_off[b];
         if (cb >= 0 && cb < a.br_c[b]) {
           owner |= 1 << b;
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void merge_nchw_kernel(kad_merge_args a) {
       s_scale[b][tid] = sc;
     }
     s_owner[tid] = owner;
-    s_gate[tid] = (a.gate && c < a.c) ? a.gate[c] : 1.f;
+    s_gate[tid] = (a.gate && c < a.c_end) ? a.gate[c] : 1.f;
   }
 #pragma unroll
   for (int b = 0; b < KAD_MAX_BRANCHES; ++b) {
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void merge_nchw_kernel(kad_merge_args a) {
   for (int k = 0; k < MG_CH / 4; ++k) {
     const int cl = (tid >> 6) + 4 * k;
     const int c = c0 + cl;
-    if (c >= a.c) continue;
+    if (c >= a.c_end) continue;
     const int64_t oi = (((int64_t)n * a.c + c) * a.h + y) * a.w + x;
     float v = res ? to_f32(res[oi]) : 0.f;
     const int owner = s_owner[cl];
@@ -367,8 +367,9 @@ __global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
   const int y = blockIdx.x, n = blockIdx.y;
   RowSrc rs[KAD_MAX_BRANCHES];
   for (int b = 0; b < a.nbranch; ++b) rs[b] = row_src(a, b, y);
-  for (int e = threadIdx.x; e < a.w * a.c; e += 256) {
-    const int c = e % a.c, x = e / a.c;
+  const int cw = a.c_end - a.c_begin;
+  for (int e = threadIdx.x; e < a.w * cw; e += 256) {
+    const int c = a.c_begin + e % cw, x = e / cw;
     const int64_t oi = (((int64_t)n * a.h + y) * a.w + x) * a.c + c;
     float v = a.residual ? to_f32(((const T*)a.residual)[oi]) : 0.f;
     for (int b = 0; b < a.nbranch; ++b) {
@@ -487,8 +488,13 @@ extern "C" int kad_channel_scale(const void* x, const float* att, void* out, int
   return check_launch("kad_channel_scale");
 }
 
-extern "C" int kad_branch_merge(const kad_merge_args* a, void* stream) {
-  KAD_CHECK_ARG(a && a->out, "kad_branch_merge: null pointer");
+extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
+  KAD_CHECK_ARG(a_in && a_in->out, "kad_branch_merge: null pointer");
+  kad_merge_args win = *a_in;
+  if (win.c_begin == 0 && win.c_end == 0) win.c_end = win.c;
+  const kad_merge_args* a = &win;
+  KAD_CHECK_ARG(a->c_begin >= 0 && a->c_begin < a->c_end && a->c_end <= a->c,
+                "kad_branch_merge: channel window [%d, %d) outside [0, %d)", a->c_begin, a->c_end, a->c);
   KAD_CHECK_ARG(a->n > 0 && a->c > 0 && a->h > 0 && a->w > 0, "kad_branch_merge: bad shape");
   KAD_CHECK_ARG(a->nbranch >= 0 && a->nbranch <= KAD_MAX_BRANCHES, "kad_branch_merge: nbranch %d out of range",
                 a->nbranch);
@@ -502,16 +508,16 @@ extern "C" int kad_branch_merge(const kad_merge_args* a, void* stream) {
   for (int b = 0; b < a->nbranch; ++b)
     KAD_CHECK_ARG(a->br_h[b] <= a->h && a->br_w[b] <= a->w, "kad_branch_merge: branch %d larger than the output", b);
   hipStream_t st = (hipStream_t)stream;
-  // disjoint, ordered channel ranges covering [0, C): the row kernel (one branch per block)
+  // disjoint, ordered channel ranges covering exactly the window: the row kernel (one branch per block)
   bool disjoint = a->nbranch > 0;
-  int cover = 0, nchunks = 0, maxbw = 0;
+  int cover = a->c_begin, nchunks = 0, maxbw = 0;
   for (int b = 0; b < a->nbranch; ++b) {
     disjoint = disjoint && a->br_c_off[b] == cover;
     cover += a->br_c[b];
     nchunks += ceil_div(a->br_c[b], 32);
     maxbw = a->br_w[b] > maxbw ? a->br_w[b] : maxbw;
   }
-  disjoint = disjoint && cover == a->c;
+  disjoint = disjoint && cover == a->c_end;
   const int tsz = a->dtype == KAD_F32 ? 4 : 2;
   const size_t row_lds = (size_t)2 * maxbw * 40 * tsz + (size_t)32 * ceil_div(a->w, 4) * 4 * tsz;
   if (a->layout == KAD_NCHW && disjoint && row_lds <= 64 * 1024) {
@@ -523,7 +529,7 @@ extern "C" int kad_branch_merge(const kad_merge_args* a, void* stream) {
       default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
     }
   } else if (a->layout == KAD_NCHW) {
-    dim3 grid(ceil_div(a->w, MG_XS), a->h, a->n * ceil_div(a->c, MG_CH));
+    dim3 grid(ceil_div(a->w, MG_XS), a->h, a->n * ceil_div(a->c_end - a->c_begin, MG_CH));
     switch (a->dtype) {
       case KAD_F32: hipLaunchKernelGGL(merge_nchw_kernel<float>, grid, dim3(256), 0, st, *a); break;
       case KAD_F16: hipLaunchKernelGGL(merge_nchw_kernel<half_t>, grid, dim3(256), 0, st, *a); break;

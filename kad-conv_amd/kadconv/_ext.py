@@ -69,7 +69,7 @@ class MergeArgs(ctypes.Structure):
     _fields_ = [
         ('out', c_vp), ('residual', c_vp), ('gate', c_vp),
         ('n', c_int), ('c', c_int), ('h', c_int), ('w', c_int), ('layout', c_int), ('dtype', c_int),
-        ('nbranch', c_int),
+        ('nbranch', c_int), ('c_begin', c_int), ('c_end', c_int),
         ('br_z', c_vp * MAX_BRANCHES), ('br_att', c_vp * MAX_BRANCHES),
         ('br_c', c_int * MAX_BRANCHES), ('br_c_off', c_int * MAX_BRANCHES),
         ('br_h', c_int * MAX_BRANCHES), ('br_w', c_int * MAX_BRANCHES), ('br_cs', c_int * MAX_BRANCHES),
@@ -408,8 +408,9 @@ def to_nhwc(x, out):
     return out
 
 
-def branch_merge(out, layout, branches, residual=None, gate=None):
-    """branches: list of dicts {z (NHWC [N,h,w,cs]), c, c_off, att (fp32 [N,c] or None), coeff}."""
+def branch_merge(out, layout, branches, residual=None, gate=None, channels=None):
+    """branches: list of dicts {z (NHWC [N,h,w,cs]), c, c_off, att (fp32 [N,c] or None), coeff};
+    channels = (begin, end): the output channels written (default: all)."""
     _need_gpu(out, residual, gate)
     if len(branches) > MAX_BRANCHES:
         raise ValueError(f'at most {MAX_BRANCHES} branches')
@@ -420,6 +421,8 @@ def branch_merge(out, layout, branches, residual=None, gate=None):
         N, H, W, C = out.shape
     a.out, a.residual, a.gate = _ptr(out), _ptr(residual), _ptr(gate)
     a.n, a.c, a.h, a.w, a.layout, a.dtype, a.nbranch = N, C, H, W, layout, kad_dtype(out.dtype), len(branches)
+    if channels is not None:
+        a.c_begin, a.c_end = channels
     for i, b in enumerate(branches):
         z = b['z']
         _need_gpu(z, b.get('att'))

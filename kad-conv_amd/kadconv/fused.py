@@ -14,7 +14,9 @@ BatchNorm folded into the DCN epilogue, LCSA parameters in one block.  Its
                     scale, GAP partials                   -> z_i (NHWC)
   kad_se_mlp        channel attention from the GAP partials -> att_i
 
-then one ``kad_branch_merge``: bilinear upsample, x att, concat and + x.
+and ``kad_branch_merge`` of the branch's own output channels: bilinear upsample,
+x att, + x (the concat is the channel window each merge writes).  The three
+chains run on side streams (fork after the pyramid, join at the end).
 
 The reference does the same stage split on A100 at batch 1 with Triton, cuDNN
 and one CUDA kernel (acceleration/kadc_fused_parallel.py:74-103,268-286;
@@ -188,9 +190,9 @@ class KADConvPlan:
         return pre + [s for b in branches for s in b] + post, out
 
     def schedule(self, x):
-        """(pre, [per-branch stages], post, out): the branch chains only depend on
-        `pre` (the pyramid) and `post` (the merge) depends on all of them, so
-        forward() runs the chains on side streams concurrently."""
+        """(pre, [per-branch stages], post, out): the branch chains (LCSA, DSC,
+        SE, and the merge of the branch's own output channels) only depend on
+        `pre` (the pyramid), so forward() runs them on side streams concurrently."""
         N, C, H, W = x.shape
         dev, dtype = x.device, x.dtype
         nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
@@ -204,7 +206,6 @@ class KADConvPlan:
             out = torch.empty_like(x)
             out_v, out_layout = out, _ext.KAD_NCHW
         st = []
-        merged = []
         ys, sums = [], []
         pyr = []
         ntx, nty = _ext.pyramid_tiles(H, W)
@@ -230,10 +231,12 @@ class KADConvPlan:
             att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
             ch.append((f'se{i}', lambda gap=gap, tiles=tiles, P=P, br=br, att=att: _ext.se_mlp(
                 gap, tiles, 1.0 / P, br.w1, br.b1, br.w2, br.b2, att, N, br.c, br.hid)))
+            # this branch's channels of the output, as soon as the branch is done
+            mb = [{'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att}]
+            ch.append((f'merge{i}', lambda mb=mb, br=br: _ext.branch_merge(
+                out_v, out_layout, mb, residual=xin, channels=(br.c_off, br.c_off + br.c))))
             chains.append(ch)
-            merged.append({'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att})
-        post = [('merge', lambda: _ext.branch_merge(out_v, out_layout, merged, residual=xin))]
-        return st, chains, post, out
+        return st, chains, [], out
 
     def _side_streams(self, dev):
         """One side stream per branch chain (default priority), created once per device."""

@@ -89,7 +89,8 @@ typedef struct kad_dcn_args {
   int n, cin, cout, h, w, stride, pad;
   int x_cs;               /* channel stride of x (multiple of 8; >= Cin) */
   int out_layout;         /* KAD_NHWC or KAD_NCHW */
-  int out_cs;             /* channel stride of out for NHWC (>= Cout) */
+  int out_cs;             /* NHWC: channel stride of out; NCHW: channel planes per image of out
+                             (both >= Cout: a channel slice of a wider tensor can be written) */
   int dtype;              /* KAD_F32 / KAD_F16 / KAD_BF16 (x, wpack, out) */
   int relu;               /* nonzero: ReLU between post_add and post_scale */
 } kad_dcn_args;
@@ -273,6 +274,14 @@ typedef struct kad_merge_args {
  * (kad_conv.py:117-121); reference k_upsample_bilinear_att + k_cat_residual_att0
  * (acceleration/kadc_fused_sm75.py:1245-1331). */
 int kad_branch_merge(const kad_merge_args *a, void *stream);
+
+/* In place, for the full-resolution branch whose DSC wrote its output straight
+ * into channels [c_off, c_off + c) of out (img_c channels per image):
+ *   out[n, c_off + j] = att[n, j] * out[n, c_off + j] + residual[n, c_off + j].
+ * residual has out's layout and shape (or NULL).  The reference's
+ * k_cat_residual_att0 (acceleration/kadc_fused_sm75.py:1245-1331) for branch 0. */
+int kad_scale_residual(void *out, const float *att, const void *residual, int n, int c, int h, int w, int img_c,
+                       int c_off, int layout, int dtype, void *stream);
 
 #ifdef __cplusplus
 }

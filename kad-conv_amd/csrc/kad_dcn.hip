@@ -1013,7 +1013,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
       const int co = co0 + col;
       if (pl >= npx || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
-      out[((int64_t)n * a.cout + co) * P + (int64_t)oy * g.wo + ox] = ost[pl * SROW + col];
+      out[((int64_t)n * a.out_cs + co) * P + (int64_t)oy * g.wo + ox] = ost[pl * SROW + col];
     }
   }
   if (a.gap_partial && tid < NB) {
@@ -1094,7 +1094,7 @@ static int validate_dcn(const kad_dcn_args* a, int mode, DcnGeom* g_out) {
   KAD_CHECK_ARG(a->stride >= 1 && a->pad >= 0, "bad stride=%d pad=%d", a->stride, a->pad);
   KAD_CHECK_ARG(a->x_cs % 8 == 0 && a->x_cs >= round_up(a->cin, 8),
                 "x channel stride %d must be a multiple of 8 and >= roundup(cin=%d, 8)", a->x_cs, a->cin);
-  KAD_CHECK_ARG(a->out_layout == KAD_NCHW || (a->out_layout == KAD_NHWC && a->out_cs >= a->cout),
+  KAD_CHECK_ARG((a->out_layout == KAD_NCHW || a->out_layout == KAD_NHWC) && a->out_cs >= a->cout,
                 "bad output layout %d / channel stride %d", a->out_layout, a->out_cs);
   const int ho = (a->h + 2 * a->pad - 3) / a->stride + 1;
   const int wo = (a->w + 2 * a->pad - 3) / a->stride + 1;

@@ -488,6 +488,90 @@ extern "C" int kad_channel_scale(const void* x, const float* att, void* out, int
   return check_launch("kad_channel_scale");
 }
 
+// ---- in-place att * out + residual over a channel slice ---------------------------------------
+// NCHW: block = one channel plane (n, j), 16-byte vectors along the plane, all
+// loads of a thread issued before its stores.
+template <typename T>
+__global__ __launch_bounds__(256) void scale_residual_nchw_kernel(T* out, const float* att, const T* res, int c,
+                                                                  int hw, int img_c, int c_off) {
+  constexpr int V = 16 / (int)sizeof(T), UNR = 4;
+  const int plane = blockIdx.x, n = plane / c, j = plane - n * c;
+  const float at = att[plane];
+  const int64_t base = ((int64_t)n * img_c + c_off + j) * hw;
+  T* o = out + base;
+  const T* r = res ? res + base : nullptr;
+  const int nv = ((hw * (int)sizeof(T)) % 16 == 0) ? hw / V : 0;  // whole-plane vectors when aligned
+  typedef T vec __attribute__((ext_vector_type(V)));
+  for (int v0 = threadIdx.x; v0 < nv; v0 += 256 * UNR) {
+    vec ov[UNR], rv[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int v = v0 + u * 256;
+      if (v < nv) {
+        ov[u] = ((const vec*)o)[v];
+        if (r) rv[u] = ((const vec*)r)[v];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int v = v0 + u * 256;
+      if (v < nv) {
+        vec y;
+#pragma unroll
+        for (int e = 0; e < V; ++e) y[e] = from_f32<T>(at * to_f32(ov[u][e]) + (r ? to_f32(rv[u][e]) : 0.f));
+        ((vec*)o)[v] = y;
+      }
+    }
+  }
+  for (int i = nv * V + threadIdx.x; i < hw; i += 256)  // unaligned planes: scalar
+    o[i] = from_f32<T>(at * to_f32(o[i]) + (r ? to_f32(r[i]) : 0.f));
+}
+
+// NHWC: block = 64 pixels; threads run along the slice's channels.
+template <typename T>
+__global__ __launch_bounds__(256) void scale_residual_nhwc_kernel(T* out, const float* att, const T* res, int c,
+                                                                  int hw, int img_c, int c_off, int64_t npix) {
+  const int64_t p0 = (int64_t)blockIdx.x * 64;
+  for (int e = threadIdx.x; e < 64 * c; e += 256) {
+    const int64_t p = p0 + e / c;
+    const int j = e % c;
+    if (p >= npix) break;
+    const int64_t n = p / hw;
+    const int64_t i = p * img_c + c_off + j;
+    out[i] = from_f32<T>(att[n * c + j] * to_f32(out[i]) + (res ? to_f32(res[i]) : 0.f));
+  }
+}
+
+extern "C" int kad_scale_residual(void* out, const float* att, const void* residual, int n, int c, int h, int w,
+                                  int img_c, int c_off, int layout, int dtype, void* stream) {
+  KAD_CHECK_ARG(out && att, "kad_scale_residual: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0 && c_off >= 0 && c_off + c <= img_c,
+                "kad_scale_residual: bad shape (c=%d c_off=%d img_c=%d)", c, c_off, img_c);
+  KAD_CHECK_ARG(layout == KAD_NCHW || layout == KAD_NHWC, "kad_scale_residual: bad layout");
+  KAD_CHECK_ARG(((uintptr_t)out | (uintptr_t)residual) % 16 == 0, "kad_scale_residual: 16-byte alignment");
+  hipStream_t st = (hipStream_t)stream;
+  const int hw = h * w;
+  if (layout == KAD_NCHW) {
+    dim3 grid(n * c);
+    switch (dtype) {
+      case KAD_F32: hipLaunchKernelGGL(scale_residual_nchw_kernel<float>, grid, dim3(256), 0, st, (float*)out, att, (const float*)residual, c, hw, img_c, c_off); break;
+      case KAD_F16: hipLaunchKernelGGL(scale_residual_nchw_kernel<half_t>, grid, dim3(256), 0, st, (half_t*)out, att, (const half_t*)residual, c, hw, img_c, c_off); break;
+      case KAD_BF16: hipLaunchKernelGGL(scale_residual_nchw_kernel<bf16_t>, grid, dim3(256), 0, st, (bf16_t*)out, att, (const bf16_t*)residual, c, hw, img_c, c_off); break;
+      default: return fail(KAD_EINVAL, "kad_scale_residual: unknown dtype %d", dtype);
+    }
+  } else {
+    const int64_t npix = (int64_t)n * hw;
+    dim3 grid((unsigned)((npix + 63) / 64));
+    switch (dtype) {
+      case KAD_F32: hipLaunchKernelGGL(scale_residual_nhwc_kernel<float>, grid, dim3(256), 0, st, (float*)out, att, (const float*)residual, c, hw, img_c, c_off, npix); break;
+      case KAD_F16: hipLaunchKernelGGL(scale_residual_nhwc_kernel<half_t>, grid, dim3(256), 0, st, (half_t*)out, att, (const half_t*)residual, c, hw, img_c, c_off, npix); break;
+      case KAD_BF16: hipLaunchKernelGGL(scale_residual_nhwc_kernel<bf16_t>, grid, dim3(256), 0, st, (bf16_t*)out, att, (const bf16_t*)residual, c, hw, img_c, c_off, npix); break;
+      default: return fail(KAD_EINVAL, "kad_scale_residual: unknown dtype %d", dtype);
+    }
+  }
+  return check_launch("kad_scale_residual");
+}
+
 extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
   KAD_CHECK_ARG(a_in && a_in->out, "kad_branch_merge: null pointer");
   kad_merge_args win = *a_in;

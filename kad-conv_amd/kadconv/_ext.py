@@ -87,6 +87,7 @@ SIGNATURES = {
     'kad_dcn_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_conv3x3_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_dsc_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
+    'kad_scale_residual': (c_int, [c_vp, c_vp, c_vp] + [c_int] * 8 + [c_vp]),
     'kad_gemm_wpack_elems': (c_i64, [c_int, c_int]),
     'kad_gemm_pack_weights': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     'kad_gemm1x1_fwd': (c_int, [ctypes.POINTER(GemmArgs), c_vp]),
@@ -163,6 +164,18 @@ def _need_gpu(*ts):
 
 
 # ---------------------------------------------------------------------------- DCN
+def _out_cs(out, layout, cout, ho, wo):
+    """Channel stride (NHWC) or channel planes per image (NCHW) of `out`, which may be a
+    channel slice of a wider tensor; pixel / plane strides must be dense."""
+    if layout == KAD_NHWC:
+        if out.stride(3) != 1 or out.stride(1) != out.stride(2) * wo or out.stride(0) != out.stride(1) * ho:
+            raise ValueError('NHWC output must be dense apart from its channel stride')
+        return out.stride(2)
+    if out.stride(3) != 1 or out.stride(2) != wo or out.stride(1) != ho * wo or out.stride(0) % (ho * wo):
+        raise ValueError('NCHW output must be dense channel planes')
+    return out.stride(0) // (ho * wo)
+
+
 def dcn_wpack_elems(cin, cout):
     return load().kad_dcn_wpack_elems(cin, cout)
 
@@ -200,7 +213,7 @@ def dcn_fwd(x_nhwc, cin, offset, offset_strides, mask, mask_strides, wpack, cout
     a.n, a.cin, a.cout, a.h, a.w, a.stride, a.pad = N, cin, cout, H, W, stride, pad
     a.x_cs = cs
     a.out_layout = out_layout
-    a.out_cs = out.shape[-1] if out_layout == KAD_NHWC else cout
+    a.out_cs = _out_cs(out, out_layout, cout, (H + 2 * pad - 3) // stride + 1, (W + 2 * pad - 3) // stride + 1)
     a.dtype = kad_dtype(x_nhwc.dtype)
     a.relu = 1 if relu else 0
     for t in (offset, mask, bias, post_mul, post_add, post_scale, gap_partial):
@@ -228,7 +241,7 @@ def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, o
     a.n, a.cin, a.cout, a.h, a.w, a.stride, a.pad = N, cin, cout, H, W, stride, pad
     a.x_cs = cs
     a.out_layout = out_layout
-    a.out_cs = out.shape[-1] if out_layout == KAD_NHWC else cout
+    a.out_cs = _out_cs(out, out_layout, cout, (H + 2 * pad - 3) // stride + 1, (W + 2 * pad - 3) // stride + 1)
     a.dtype = kad_dtype(x_nhwc.dtype)
     a.relu = 1 if relu else 0
     for t in (off_bias, mask, bias, post_mul, post_add, post_scale, gap_partial):
@@ -251,7 +264,7 @@ def conv3x3_fwd(x_nhwc, cin, wpack, cout, out, *, stride=1, pad=1, bias=None, ou
     a.n, a.cin, a.cout, a.h, a.w, a.stride, a.pad = N, cin, cout, H, W, stride, pad
     a.x_cs = cs
     a.out_layout = out_layout
-    a.out_cs = out.shape[-1] if out_layout == KAD_NHWC else cout
+    a.out_cs = _out_cs(out, out_layout, cout, (H + 2 * pad - 3) // stride + 1, (W + 2 * pad - 3) // stride + 1)
     a.dtype = kad_dtype(x_nhwc.dtype)
     _check(load().kad_conv3x3_fwd(ctypes.byref(a), _stream()), 'kad_conv3x3_fwd')
     return out
@@ -405,6 +418,23 @@ def to_nhwc(x, out):
     N, C, H, W = x.shape
     _check(load().kad_to_nhwc(_ptr(x), _ptr(out), N, C, H, W, out.shape[-1], kad_dtype(x.dtype), _stream()),
            'kad_to_nhwc')
+    return out
+
+
+def scale_residual(out, att, residual, c_off, c, layout):
+    """In place on channels [c_off, c_off + c) of `out` (full tensor, NCHW or NHWC):
+    out = att[n, j] * out + residual."""
+    _need_gpu(out, att, residual)
+    if layout == KAD_NCHW:
+        N, C, H, W = out.shape
+    else:
+        N, H, W, C = out.shape
+    if not out.is_contiguous() or (residual is not None and (residual.shape != out.shape or not residual.is_contiguous())):
+        raise ValueError('scale_residual wants dense out / residual of one shape')
+    if att.dtype != torch.float32 or tuple(att.shape) != (N, c):
+        raise TypeError('att must be float32 [N, c]')
+    _check(load().kad_scale_residual(_ptr(out), _ptr(att), _ptr(residual), N, c, H, W, C, c_off, layout,
+                                     kad_dtype(out.dtype), _stream()), 'kad_scale_residual')
     return out
 
 

@@ -223,18 +223,31 @@ class KADConvPlan:
         for i, br in enumerate(self.branches):
             h, w = H >> i, W >> i
             P = h * w
-            z = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
+            full = (h, w) == (H, W)
             tiles = _ext.dcn_tiles(h, w)
             gap = torch.empty(N, tiles, br.c, dtype=torch.float32, device=dev)
-            ch = br.dsc.stages(ys[i], N, h, w, z, _ext.KAD_NHWC, post_mul=br.bn_a, post_add=br.bn_b,
+            if full:
+                # full resolution: the DSC writes its channel slice of the output directly
+                # (no upsampling needed); attention and residual are applied in place below
+                z = out_v[:, br.c_off:br.c_off + br.c] if out_layout == _ext.KAD_NCHW \
+                    else out_v[..., br.c_off:br.c_off + br.c]
+                z_layout = out_layout
+            else:
+                z = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
+                z_layout = _ext.KAD_NHWC
+            ch = br.dsc.stages(ys[i], N, h, w, z, z_layout, post_mul=br.bn_a, post_add=br.bn_b,
                                post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i])
             att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
             ch.append((f'se{i}', lambda gap=gap, tiles=tiles, P=P, br=br, att=att: _ext.se_mlp(
                 gap, tiles, 1.0 / P, br.w1, br.b1, br.w2, br.b2, att, N, br.c, br.hid)))
-            # this branch's channels of the output, as soon as the branch is done
-            mb = [{'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att}]
-            ch.append((f'merge{i}', lambda mb=mb, br=br: _ext.branch_merge(
-                out_v, out_layout, mb, residual=xin, channels=(br.c_off, br.c_off + br.c))))
+            if full:
+                ch.append((f'merge{i}', lambda br=br, att=att: _ext.scale_residual(
+                    out_v, att, xin, br.c_off, br.c, out_layout)))
+            else:
+                # this branch's channels of the output, as soon as the branch is done
+                mb = [{'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att}]
+                ch.append((f'merge{i}', lambda mb=mb, br=br: _ext.branch_merge(
+                    out_v, out_layout, mb, residual=xin, channels=(br.c_off, br.c_off + br.c))))
             chains.append(ch)
         return st, chains, [], out
 

@@ -113,20 +113,104 @@ __device__ __forceinline__ Raw8 load8_full(const T* p) {
   return r;
 }
 
+// 8 consecutive elements at p (8-byte aligned), the first `valid` (0, 4 or 8)
+// real: two predicated 8-byte loads for 16-bit types, two 16-byte loads for
+// fp32 -- no per-lane branching on alignment (rows with W % 4 == 0).
+template <typename T>
+__device__ __forceinline__ Raw8 load8_w4(const T* p, int valid) {
+  Raw8 r;
+  r.lo = uint4{0u, 0u, 0u, 0u};
+  r.hi = r.lo;
+  if constexpr (sizeof(T) == 2) {
+    uint2 a0 = uint2{0u, 0u}, a1 = uint2{0u, 0u};
+    if (valid >= 4) a0 = ((const uint2*)p)[0];
+    if (valid == 8) a1 = ((const uint2*)p)[1];
+    r.lo = uint4{a0.x, a0.y, a1.x, a1.y};
+  } else {
+    if (valid >= 4) r.lo = ((const uint4*)p)[0];
+    if (valid == 8) r.hi = ((const uint4*)p)[1];
+  }
+  return r;
+}
+
+// An MFMA A/B fragment: 8 elements of T in registers.
+template <typename T> struct PyFrag { T v[8]; };
+
+template <typename T>
+__device__ __forceinline__ PyFrag<T> frag_ld(const T* p) {
+  PyFrag<T> f;
+  if constexpr (sizeof(T) == 2) {
+    *(uint4*)f.v = *(const uint4*)p;
+  } else {
+    *(floatx4*)f.v = *(const floatx4*)p;
+    *(floatx4*)(f.v + 4) = *(const floatx4*)(p + 4);
+  }
+  return f;
+}
+
+template <typename T>
+__device__ __forceinline__ floatx4 py_mma_f(const PyFrag<T>& a, const PyFrag<T>& b, floatx4 c) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[j], b.v[j], c, 0, 0, 0);
+    return c;
+  } else if constexpr (__is_same(T, half_t)) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c,
+                                                  0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+}
+
+// Pooled input of branches 1 and 2, built straight into an A fragment (8
+// channels from lane group offset g8, fp32 sums, one rounding to T): S = 2, the
+// 2 x 2 window with top-left staged pixel q0; S = 4, the upper or lower half (two
+// rows) of a 4 x 4 window divided by 16 -- the two halves are projected by the
+// two pixel-half waves and their products added in the epilogue (linearity).
+template <typename T, int S, int LDA>
+__device__ __forceinline__ PyFrag<T> pooled_frag(const T* xs, int q0, int g8) {
+  float acc8[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc8[j] = 0.f;
+  if constexpr (S == 2) {  // (a + b) + (c + d), as a 2x2 average is usually formed
+    const PyFrag<T> s0 = frag_ld(xs + q0 * LDA + g8), s1 = frag_ld(xs + (q0 + 1) * LDA + g8);
+    const PyFrag<T> s2 = frag_ld(xs + (q0 + PY_TC) * LDA + g8), s3 = frag_ld(xs + (q0 + PY_TC + 1) * LDA + g8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc8[j] = (to_f32(s0.v[j]) + to_f32(s1.v[j])) + (to_f32(s2.v[j]) + to_f32(s3.v[j]));
+  } else {  // half of a 4 x 4 window: rows q0 / PY_TC and the next, 4 columns
+#pragma unroll
+    for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+      for (int dx = 0; dx < S; ++dx) {
+        const PyFrag<T> sv = frag_ld(xs + (q0 + dy * PY_TC + dx) * LDA + g8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc8[j] += to_f32(sv.v[j]);
+      }
+  }
+  PyFrag<T> f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f.v[j] = from_f32<T>(acc8[j] * (1.f / (float)(S * S)));
+  return f;
+}
+
 // HB = MFMA column fragments per wave and branch (columns per block = 32 * HB).
+// The widest column tiles get the whole register file (1 block per CU) instead of spilling.
+template <typename T, int HB> struct PyOcc { static constexpr int v = HB <= (sizeof(T) == 4 ? 2 : 3) ? 2 : 1; };
+
 template <typename T, int HB>
-__global__ __launch_bounds__(PY_THREADS, 2) void pyramid_kernel(kad_pyramid_args a, int cin_pad) {
+__global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(kad_pyramid_args a, int cin_pad) {
   constexpr int LDA = PyLds<T>::lda;
   constexpr int NB = 32 * HB;              // output columns per branch per block
   constexpr int BTASKS = 3 * NB * 4;       // 16-byte weight pieces per K step (3 branches)
   constexpr int BPT = (BTASKS + PY_THREADS - 1) / PY_THREADS;
-  constexpr int OBS = NB + 1;
+  constexpr int OBT = NB + 16 / (int)sizeof(T);   // epilogue staging row of y (T)
   extern __shared__ __align__(16) char smem[];
   T* xs = (T*)smem;                   // [128][LDA]
-  T* p1 = xs + PY_TILE * LDA;         // [32][LDA]
-  T* p2 = p1 + 32 * LDA;              // [16][LDA] (8 used)
-  T* bs = p2 + 16 * LDA;              // [3][NB][LDA]
-  float* ob = (float*)smem;           // epilogue: [128][OBS]
+  T* bs = xs + PY_TILE * LDA;         // [3][NB][LDA]
+  T* obt = (T*)smem;                  // epilogue: [128][OBT] y values of one branch
+  float* colred = (float*)(smem + PY_TILE * OBT * sizeof(T));  // epilogue: [32][NB] column partials
 
   const int tx = blockIdx.x, ty = blockIdx.y % a.nty, cy = blockIdx.y / a.nty, n = blockIdx.z;
   const int r0 = ty * PY_TR, c0 = tx * PY_TC;
@@ -157,6 +241,7 @@ __global__ __launch_bounds__(PY_THREADS, 2) void pyramid_kernel(kad_pyramid_args
   // Per-thread source pointers and validity are fixed across K steps; each step
   // advances them by 32 channels.
   const T* x = (const T*)a.x;
+  const bool w4 = a.in_layout == KAD_NCHW && (a.w % 4) == 0;  // block-uniform: 8-byte aligned rows
   Raw8 xr[2];
   Raw8 br[BPT];
   const T* xp[2];
@@ -201,7 +286,7 @@ __global__ __launch_bounds__(PY_THREADS, 2) void pyramid_kernel(kad_pyramid_args
         const int rem = a.cin - (k0 + xch[t]);
         valid = xvalid[t] ? (rem < 0 ? 0 : (rem > 8 ? 8 : rem)) : 0;
       }
-      xr[t] = load8_raw(xp[t] + (k0 / 32) * xstep, valid);
+      xr[t] = w4 ? load8_w4(xp[t] + (k0 / 32) * xstep, valid) : load8_raw(xp[t] + (k0 / 32) * xstep, valid);
     }
 #pragma unroll
     for (int t = 0; t < BPT; ++t)
@@ -236,183 +321,193 @@ __global__ __launch_bounds__(PY_THREADS, 2) void pyramid_kernel(kad_pyramid_args
     store_step();
     if (k0 + 32 < cin_pad) load_step(k0 + 32);  // in flight while this step computes
     __syncthreads();
-    // ---- 2x2 and 4x4 averages of the slice ---------------------------------------------------
-    if constexpr (sizeof(T) == 2) {
-      // 8 channels per task with 16-byte LDS reads; fp32 sums, one rounding to T
-      if (nb > 1 && tid < 128) {
-        const int g = tid & 3, q = tid >> 2, pr = q >> 4, pc = q & 15;
-        const int b0 = (2 * pr) * PY_TC + 2 * pc;
-        typedef T v8 __attribute__((ext_vector_type(8)));
-        const v8 s0 = *(const v8*)&xs[b0 * LDA + g * 8], s1 = *(const v8*)&xs[(b0 + 1) * LDA + g * 8];
-        const v8 s2 = *(const v8*)&xs[(b0 + PY_TC) * LDA + g * 8], s3 = *(const v8*)&xs[(b0 + PY_TC + 1) * LDA + g * 8];
-        v8 o;
+    // ---- A fragments: the slice (branch 0) and its 2x2 / 4x4 averages (branches 1, 2) ----------
+    // wave (wa, wb) = pixel half x column half
+    PyFrag<T> a0[4], a1, a2;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          o[j] = from_f32<T>(0.25f * ((to_f32(s0[j]) + to_f32(s1[j])) + (to_f32(s2[j]) + to_f32(s3[j]))));
-        *(v8*)&p1[q * LDA + g * 8] = o;
-      }
-      if (nb > 2 && tid >= 128 && tid < 128 + 64) {
-        const int t2 = tid - 128, g = t2 & 3, pc = t2 >> 2;  // pc 0..15 (8 used)
-        typedef T v8 __attribute__((ext_vector_type(8)));
-        float acc8[8];
+    for (int mm = 0; mm < 4; ++mm) a0[mm] = frag_ld(xs + ((wa * 4 + mm) * 16 + row16) * LDA + grp * 8);
+    if (nb > 1) a1 = pooled_frag<T, 2, LDA>(xs, (2 * wa) * PY_TC + 2 * row16, grp * 8);  // pooled (wa, row16)
+    if (nb > 2) {  // pooled pixel row16 of the 1 x 8 tile (rows >= 8 are padding); this wave's two rows
+      if (row16 < 8) {
+        a2 = pooled_frag<T, 4, LDA>(xs, (2 * wa) * PY_TC + 4 * row16, grp * 8);
+      } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc8[j] = 0.f;
-        if (pc < 8) {
-#pragma unroll
-          for (int dy = 0; dy < 4; ++dy)
-#pragma unroll
-            for (int dx = 0; dx < 4; ++dx) {
-              const v8 sv = *(const v8*)&xs[(dy * PY_TC + 4 * pc + dx) * LDA + g * 8];
-#pragma unroll
-              for (int j = 0; j < 8; ++j) acc8[j] += to_f32(sv[j]);
-            }
-        }
-        v8 o;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] = from_f32<T>(acc8[j] * (1.f / 16.f));
-        *(v8*)&p2[pc * LDA + g * 8] = o;
-      }
-    } else {
-      if (nb > 1) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int e = tid + t * PY_THREADS;
-          const int ch = e & 31, q = e >> 5, pr = q >> 4, pc = q & 15;
-          const int b0 = (2 * pr) * PY_TC + 2 * pc;
-          const float sum = to_f32(xs[b0 * LDA + ch]) + to_f32(xs[(b0 + 1) * LDA + ch]) +
-                            to_f32(xs[(b0 + PY_TC) * LDA + ch]) + to_f32(xs[(b0 + PY_TC + 1) * LDA + ch]);
-          p1[q * LDA + ch] = from_f32<T>(0.25f * sum);
-        }
-      }
-      if (nb > 2) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int e = tid + t * PY_THREADS;
-          const int ch = e & 31, pc = e >> 5;
-          float sum = 0.f;
-          if (pc < 8) {
-#pragma unroll
-            for (int dy = 0; dy < 4; ++dy)
-#pragma unroll
-              for (int dx = 0; dx < 4; ++dx) sum += to_f32(xs[(dy * PY_TC + 4 * pc + dx) * LDA + ch]);
-          }
-          p2[pc * LDA + ch] = from_f32<T>(sum * (1.f / 16.f));
-        }
+        for (int j = 0; j < 8; ++j) a2.v[j] = from_f32<T>(0.f);
       }
     }
-    __syncthreads();
-    // ---- MFMA: wave (wa, wb) = pixel half x column half ----------------------------------------
 #pragma unroll
     for (int bb = 0; bb < HB; ++bb) {
       const int bf = wb * HB + bb;
       if (bf < nbf[0]) {
-        const T* bp = bs + (0 * NB + bf * 16 + row16) * LDA + grp * 8;
+        const PyFrag<T> bq = frag_ld(bs + (0 * NB + bf * 16 + row16) * LDA + grp * 8);
 #pragma unroll
-        for (int mm = 0; mm < 4; ++mm)
-          acc0[mm][bb] = py_mma<T>(xs + ((wa * 4 + mm) * 16 + row16) * LDA + grp * 8, bp, acc0[mm][bb]);
+        for (int mm = 0; mm < 4; ++mm) acc0[mm][bb] = py_mma_f<T>(a0[mm], bq, acc0[mm][bb]);
       }
-      if (bf < nbf[1])
-        acc1[bb] = py_mma<T>(p1 + (wa * 16 + row16) * LDA + grp * 8, bs + (1 * NB + bf * 16 + row16) * LDA + grp * 8,
-                             acc1[bb]);
-      if (wa == 0 && bf < nbf[2])
-        acc2[bb] = py_mma<T>(p2 + row16 * LDA + grp * 8, bs + (2 * NB + bf * 16 + row16) * LDA + grp * 8, acc2[bb]);
+      if (bf < nbf[1]) acc1[bb] = py_mma_f<T>(a1, frag_ld(bs + (1 * NB + bf * 16 + row16) * LDA + grp * 8), acc1[bb]);
+      if (bf < nbf[2])
+        acc2[bb] = py_mma_f<T>(a2, frag_ld(bs + (2 * NB + bf * 16 + row16) * LDA + grp * 8), acc2[bb]);
     }
   }
 
-  // ---- epilogue, one branch at a time through LDS -------------------------------------------------
+  // ---- epilogue, one branch at a time -------------------------------------------------------------
+  // acc layout: lane (row16, grp) holds column bf * 16 + row16 and tile pixels
+  //   branch 0: (wa * 4 + mm) * 16 + grp * 4 + i  (tile row 2 wa + mm / 2, column (mm & 1) * 16 + grp * 4 + i)
+  //   branch 1: wa * 16 + grp * 4 + i             (pooled row wa, column grp * 4 + i)
+  //   branch 2: grp * 4 + i (< 8)                 (pooled row 0, column grp * 4 + i)
+  // Row sums come from registers (+ shuffles across the 4 lane groups); column
+  // sums from registers + one LDS exchange between the two pixel-half waves.
+  // Branch-0 pixels outside the image hold exact zeros (zero input); pooled
+  // branches mask windows past the floor-mode output explicitly.
 #pragma unroll
   for (int b = 0; b < 3; ++b) {
     if (ncols[b] == 0) continue;   // uniform across the block
     const int tr = PY_TR >> b, tc = PY_TC >> b;
     const int hbch = a.out_h[b], wbch = a.out_w[b];
-    __syncthreads();
+    const int cout = a.cout[b];
+    const float* bias = a.bias[b];
+    const int vc = (wbch - tx * tc) < tc ? (wbch - tx * tc) : tc;  // valid columns in this tile
+    const int vr = (hbch - ty * tr) < tr ? (hbch - ty * tr) : tr;  // valid rows
+    const bool sums = a.rowpart[b] != nullptr;
+    float* rowp = a.rowpart[b];
+    float* colp = a.colpart[b];
+    __syncthreads();  // the K loop (or the previous branch) is done with the LDS
+    if (b == 2) {  // the lower-half products (wa == 1) join the upper half (wa == 0)
+      if (wa == 1) {
+#pragma unroll
+        for (int bb = 0; bb < HB; ++bb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) colred[((wb * HB + bb) * 16 + grp * 4 + i) * 16 + row16] = acc2[bb][i];
+      }
+      __syncthreads();
+      if (wa == 0) {
+#pragma unroll
+        for (int bb = 0; bb < HB; ++bb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc2[bb][i] += colred[((wb * HB + bb) * 16 + grp * 4 + i) * 16 + row16];
+      }
+    }
 #pragma unroll
     for (int bb = 0; bb < HB; ++bb) {
       const int bf = wb * HB + bb;
-      if (bf >= nbf[b]) continue;
-      const int col = bf * 16 + row16;
+      if (bf >= nbf[b]) continue;  // uniform per wave
+      const int col = bf * 16 + row16, co = col0 + col;
+      const bool real = co < cout;
+      const float bv = (bias && real) ? bias[co] : 0.f;
       if (b == 0) {
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) ob[((wa * 4 + mm) * 16 + grp * 4 + i) * OBS + col] = acc0[mm][bb][i];
+          for (int i = 0; i < 4; ++i)
+            obt[((wa * 4 + mm) * 16 + grp * 4 + i) * OBT + col] = from_f32<T>(acc0[mm][bb][i] + bv);
+        if (sums) {
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {  // tile rows 2 wa + q
+            float sr = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sr += acc0[2 * q][bb][i] + acc0[2 * q + 1][bb][i];
+            sr += __shfl_xor(sr, 16);
+            sr += __shfl_xor(sr, 32);
+            const int r = 2 * wa + q;
+            if (grp == 0 && real && r < vr)
+              rowp[(((int64_t)n * a.ntx + tx) * hbch + ty * tr + r) * cout + co] = sr + vc * bv;
+          }
+          if (wa == 1) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                colred[(h * 16 + grp * 4 + i) * NB + col] = acc0[h][bb][i] + acc0[2 + h][bb][i];
+          }
+        }
       } else if (b == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ob[(wa * 16 + grp * 4 + i) * OBS + col] = acc1[bb][i];
+        for (int i = 0; i < 4; ++i) obt[(wa * 16 + grp * 4 + i) * OBT + col] = from_f32<T>(acc1[bb][i] + bv);
+        if (sums) {
+          float sr = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sr += (grp * 4 + i < vc) ? acc1[bb][i] : 0.f;
+          sr += __shfl_xor(sr, 16);
+          sr += __shfl_xor(sr, 32);
+          if (grp == 0 && real && wa < vr)
+            rowp[(((int64_t)n * a.ntx + tx) * hbch + ty * tr + wa) * cout + co] = sr + vc * bv;
+          if (wa == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) colred[(grp * 4 + i) * NB + col] = (1 < vr) ? acc1[bb][i] : 0.f;
+          }
+        }
       } else if (wa == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ob[(grp * 4 + i) * OBS + col] = acc2[bb][i];
-      }
-    }
-    __syncthreads();
-    const int cout = a.cout[b];
-    const float* bias = a.bias[b];
-    // y_b: NHWC, 8 channels per 16-byte store, bias added (pad channels stay 0)
-    T* y = (T*)a.out[b];
-    const int g8 = ncols[b] >> 3;
-    {
-      const int g = tid & 15;
-      float bv[8];
+        for (int i = 0; i < 4; ++i)
+          if (grp * 4 + i < 8) obt[(grp * 4 + i) * OBT + col] = from_f32<T>(acc2[bb][i] + bv);
+        if (sums) {
+          float sr = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int co = col0 + g * 8 + j;
-        bv[j] = (bias && co < cout) ? bias[co] : 0.f;
-      }
-      if (g < g8) {
-        for (int px = tid >> 4; px < tr * tc; px += PY_THREADS / 16) {
-          const int py_ = px / tc;  // tc is a power of two
-          const int gy = ty * tr + py_, gx = tx * tc + (px - py_ * tc);
-          if (gy >= hbch || gx >= wbch) continue;
-          T* d = y + (((int64_t)n * hbch + gy) * wbch + gx) * a.out_cs[b] + col0 + g * 8;
-          if constexpr (sizeof(T) == 2) {
-            typedef T v8 __attribute__((ext_vector_type(8)));
-            v8 vals;
+          for (int i = 0; i < 4; ++i) sr += (grp * 4 + i < vc) ? acc2[bb][i] : 0.f;
+          sr += __shfl_xor(sr, 16);
+          sr += __shfl_xor(sr, 32);
+          if (grp == 0 && real && vr > 0)
+            rowp[(((int64_t)n * a.ntx + tx) * hbch + ty * tr) * cout + co] = sr + vc * bv;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vals[j] = from_f32<T>(ob[px * OBS + g * 8 + j] + bv[j]);
-            *(v8*)d = vals;
-          } else {
-            floatx4 v0, v1;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              v0[j] = ob[px * OBS + g * 8 + j] + bv[j];
-              v1[j] = ob[px * OBS + g * 8 + 4 + j] + bv[4 + j];
-            }
-            ((floatx4*)d)[0] = v0;
-            ((floatx4*)d)[1] = v1;
+          for (int i = 0; i < 4; ++i) {
+            const int c = grp * 4 + i;
+            if (real && c < vc && vr > 0)
+              colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] = acc2[bb][i] + bv;
           }
         }
       }
     }
-    // axial partial sums of (acc + bias) in fp32: rows over this tile's valid columns,
-    // columns over its valid rows
-    const int ncr = cout - col0 < ncols[b] ? cout - col0 : ncols[b];
-    if (a.rowpart[b] && ncr > 0) {
-      const int vc = (wbch - tx * tc) < tc ? (wbch - tx * tc) : tc;  // valid columns in this tile
-      const int vr = (hbch - ty * tr) < tr ? (hbch - ty * tr) : tr;  // valid rows
-      for (int e = tid; e < tr * NB; e += PY_THREADS) {
-        const int cl = e % NB, r = e / NB;
-        if (cl >= ncr || r >= vr) continue;
-        const float bvl = bias ? bias[col0 + cl] : 0.f;
-        float acc = 0.f;
-        for (int cc = 0; cc < vc; ++cc) acc += ob[(r * tc + cc) * OBS + cl];
-        a.rowpart[b][(((int64_t)n * a.ntx + tx) * hbch + ty * tr + r) * cout + col0 + cl] = acc + vc * bvl;
+    __syncthreads();
+    // column sums of branches 0 and 1: the wa == 0 waves add the wa == 1 partials
+    if (sums && b < 2 && wa == 0) {
+#pragma unroll
+      for (int bb = 0; bb < HB; ++bb) {
+        const int bf = wb * HB + bb;
+        if (bf >= nbf[b]) continue;
+        const int col = bf * 16 + row16, co = col0 + col;
+        if (co >= cout) continue;
+        const float bv = bias ? bias[co] : 0.f;
+        if (b == 0) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int c = h * 16 + grp * 4 + i;
+              if (c < vc)
+                colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] =
+                    (acc0[h][bb][i] + acc0[2 + h][bb][i]) + colred[c * NB + col] + vr * bv;
+            }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int c = grp * 4 + i;
+            if (c < vc && vr > 0)
+              colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] =
+                  acc1[bb][i] + colred[c * NB + col] + vr * bv;
+          }
+        }
       }
-      for (int e = tid; e < tc * NB; e += PY_THREADS) {
-        const int cl = e % NB, cc = e / NB;
-        if (cl >= ncr || cc >= vc) continue;
-        const float bvl = bias ? bias[col0 + cl] : 0.f;
-        float acc = 0.f;
-        for (int r = 0; r < vr; ++r) acc += ob[(r * tc + cc) * OBS + cl];
-        a.colpart[b][(((int64_t)n * a.nty + ty) * wbch + tx * tc + cc) * cout + col0 + cl] = acc + vr * bvl;
-      }
+    }
+    // y_b: NHWC, 16-byte pieces of 8 channels straight from the staged rows (pad channels are 0)
+    T* y = (T*)a.out[b];
+    const int g8 = ncols[b] >> 3;
+    constexpr int G8 = NB / 8;
+    for (int e = tid; e < tr * tc * G8; e += PY_THREADS) {
+      const int px = e / G8, g = e - px * G8;
+      const int py_ = px / tc;  // tc is a power of two
+      const int gy = ty * tr + py_, gx = tx * tc + (px - py_ * tc);
+      if (g >= g8 || gy >= hbch || gx >= wbch) continue;
+      T* d = y + (((int64_t)n * hbch + gy) * wbch + gx) * a.out_cs[b] + col0 + g * 8;
+      const T* sp = obt + px * OBT + g * 8;
+      *(uint4*)d = *(const uint4*)sp;
+      if constexpr (sizeof(T) == 4) *(uint4*)(d + 4) = *(const uint4*)(sp + 4);
     }
   }
 }
 
 template <typename T, int HB>
 static size_t pyramid_lds() {
-  const size_t stage = (size_t)(PY_TILE + 32 + 16 + 3 * 32 * HB) * PyLds<T>::lda * sizeof(T);
-  const size_t epi = (size_t)PY_TILE * (32 * HB + 1) * sizeof(float);
+  const size_t stage = (size_t)(PY_TILE + 3 * 32 * HB) * PyLds<T>::lda * sizeof(T);
+  const size_t epi = (size_t)PY_TILE * (32 * HB + 16 / sizeof(T)) * sizeof(T) + (size_t)32 * 32 * HB * sizeof(float);
   return stage > epi ? stage : epi;
 }
 

@@ -113,17 +113,50 @@ constexpr int LM_THREADS = 256;
 template <typename ET> struct LmCfg { static constexpr int ldu = 40; };  // 32 + 8 halves per (row, col)
 template <> struct LmCfg<float> { static constexpr int ldu = 36; };
 
+// E fragment of one lane (8 channels) and the MFMA against 8 channels of u in LDS.
+template <typename ET> struct LmFrag;
+template <> struct LmFrag<half_t> {
+  typedef half8_t frag;
+  static __device__ __forceinline__ frag ld(const half_t* p) { return *(const half8_t*)p; }
+  static __device__ __forceinline__ floatx4 mma(const frag& a, const half_t* b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, *(const half8_t*)b, c, 0, 0, 0);
+  }
+};
+struct LmF32x8 { floatx4 lo, hi; };
+template <> struct LmFrag<float> {
+  typedef LmF32x8 frag;
+  static __device__ __forceinline__ frag ld(const float* p) { return LmF32x8{*(const floatx4*)p, *(const floatx4*)(p + 4)}; }
+  static __device__ __forceinline__ floatx4 mma(const frag& a, const float* b, floatx4 c) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[j], b[j], c, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[j], b[4 + j], c, 0, 0, 0);
+    return c;
+  }
+};
+
+constexpr int LM_SC = 96;                              // channels per staged group (3 chunks)
+constexpr int LM_SCS = LM_SC + 4;                       // fp32 row stride of the staged group
+
 // grid (ceil(W/16), ceil(H/16), N).  Wave v computes tile rows 4v..4v+3 (4 MFMA
 // column fragments of 16 pixels each) for all 16 (9 used) mask logits.
+// Per group of up to 96 channels, one round trip brings the block's column
+// means (26 columns: 16 + the 11-tap halo), row means (26 rows) and the
+// strip-conv / BN parameters into LDS; alpha / beta of the 16 columns are
+// formed there once.  Per 32-channel chunk: the lanes' E fragments (11 taps) are
+// requested first, u = relu(alpha a + beta) is written to LDS meanwhile, then
+// 11 x 4 MFMAs.
 template <typename ET>
-__global__ __launch_bounds__(LM_THREADS) void lcsa_mask_kernel(const float* arow, const float* colm,
-                                                              const float* params, const ET* emat,
-                                                              const float* ebias, float* mask, int c, int h, int w,
-                                                              int cp) {
+__global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* arow, const float* colm,
+                                                                 const float* params, const ET* emat,
+                                                                 const float* ebias, float* mask, int c, int h,
+                                                                 int w, int cp) {
   constexpr int LDU = LmCfg<ET>::ldu;
   __shared__ __align__(16) ET us[LM_UR * LM_TW * LDU];
-  __shared__ __align__(16) ET es[16 * BAND * LDU];                 // E slice [j][k][32 c]
-  __shared__ __align__(16) float s_alpha[LM_TW][32], s_beta[LM_TW][32], s_a[LM_UR][32];
+  __shared__ __align__(16) float s_col[LM_UR][LM_SCS];   // column means, columns w0 - 5 .. w0 + 20
+  __shared__ __align__(16) float s_a[LM_UR][LM_SCS];     // row means, rows h0 - 5 .. h0 + 20
+  __shared__ float s_w1[LM_SC * BAND], s_b1[LM_SC], s_bna[LM_SC], s_bnb[LM_SC];
+  __shared__ __align__(16) float s_alpha[LM_TW][LM_SCS], s_beta[LM_TW][LM_SCS];
   const float* w1 = params;
   const float* b1 = params + 11 * c;
   const float* bna = params + 12 * c;
@@ -138,101 +171,114 @@ __global__ __launch_bounds__(LM_THREADS) void lcsa_mask_kernel(const float* arow
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  for (int c0 = 0; c0 < cp; c0 += 32) {
-    __syncthreads();
-    // E slice for these 32 channels (16 x 11 rows of 32), 8 elements per task
+  for (int cs = 0; cs < cp; cs += LM_SC) {
+    const int nsc = cp - cs < LM_SC ? cp - cs : LM_SC;   // multiple of 32
+    // ---- 1. one round of loads: column / row means and parameters of this group ----------------
+    // Index space uses the fixed group width LM_SC (constant divisors); channels past
+    // c or past the group read 0.
+    constexpr int NW = (LM_UR * LM_SC + LM_THREADS - 1) / LM_THREADS;    // per window
+    constexpr int NP = (LM_SC * BAND + LM_THREADS - 1) / LM_THREADS;     // w1
+    constexpr int NQ = (3 * LM_SC + LM_THREADS - 1) / LM_THREADS;        // b1 | bn_a | bn_b
+    __syncthreads();  // the previous group's LDS data is consumed
+    float vc_[NW], va_[NW], vw_[NP], vq_[NQ];
 #pragma unroll
-    for (int e = tid; e < 16 * BAND * 4; e += LM_THREADS) {
-      const int g = e & 3, row = e >> 2;  // row = j * 11 + k
-      const ET* src = emat + (int64_t)row * cp + c0 + g * 8;
-      ET* dst = es + row * LDU + g * 8;
-      if constexpr (sizeof(ET) == 2) {
-        *(uint4*)dst = *(const uint4*)src;
-      } else {
-        ((floatx4*)dst)[0] = ((const floatx4*)src)[0];
-        ((floatx4*)dst)[1] = ((const floatx4*)src)[1];
+    for (int u = 0; u < NW; ++u) {
+      const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC, gc = cs + ch;
+      const int gx = w0 - HALF_BAND + r, gy = h0 - HALF_BAND + r;
+      const bool ok = r < LM_UR && ch < nsc && gc < c;
+      vc_[u] = (ok && gx >= 0 && gx < w) ? colm_n[(int64_t)gx * c + gc] : 0.f;
+      va_[u] = (ok && gy >= 0 && gy < h) ? arow_n[(int64_t)gy * c + gc] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+      const int e = tid + u * LM_THREADS;
+      vw_[u] = (e < nsc * BAND && cs * BAND + e < c * BAND) ? w1[cs * BAND + e] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int e = tid + u * LM_THREADS, which = e / LM_SC, ch = e - which * LM_SC, gc = cs + ch;
+      vq_[u] = (which < 3 && ch < nsc && gc < c) ? (which == 0 ? b1 : which == 1 ? bna : bnb)[gc] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC;
+      if (r < LM_UR) {
+        s_col[r][ch] = vc_[u];
+        s_a[r][ch] = va_[u];
       }
     }
-    // strip-conv coefficients of this block's 16 columns (separable 1x11 conv + folded BN)
 #pragma unroll
-    for (int e = tid; e < LM_TW * 32; e += LM_THREADS) {
-      const int ch = e & 31, col = e >> 5;
-      const int gx = w0 + col, gc = c0 + ch;
-      float al = 0.f, be = 0.f;
-      if (gx < w && gc < c) {
-        float S = 0.f, B = 0.f;
+    for (int u = 0; u < NP; ++u) {
+      const int e = tid + u * LM_THREADS;
+      if (e < LM_SC * BAND) s_w1[e] = vw_[u];
+    }
 #pragma unroll
-        for (int k = 0; k < BAND; ++k) {
-          const int xx = gx + k - HALF_BAND;
-          if (xx >= 0 && xx < w) {
-            const float wk = w1[gc * BAND + k];
-            S += wk;
-            B += wk * colm_n[xx * c + gc];
+    for (int u = 0; u < NQ; ++u) {
+      const int e = tid + u * LM_THREADS, which = e / LM_SC, ch = e - which * LM_SC;
+      if (which < 3) (which == 0 ? s_b1 : which == 1 ? s_bna : s_bnb)[ch] = vq_[u];
+    }
+    __syncthreads();
+    // ---- 2. strip-conv coefficients of the 16 columns (separable 1x11 conv + folded BN) ----------
+    for (int e = tid; e < LM_TW * LM_SC; e += LM_THREADS) {
+      const int col = e / LM_SC, ch = e - col * LM_SC, gx = w0 + col;
+      float S = 0.f, B = 0.f;
+#pragma unroll
+      for (int k = 0; k < BAND; ++k) {
+        const int xx = gx + k - HALF_BAND;
+        const float wk = s_w1[ch * BAND + k];
+        if (xx >= 0 && xx < w) {
+          S += wk;
+          B += wk * s_col[col + k][ch];
+        }
+      }
+      const bool ok = gx < w && ch < nsc && cs + ch < c;
+      s_alpha[col][ch] = ok ? s_bna[ch] * S : 0.f;
+      s_beta[col][ch] = ok ? s_bna[ch] * (B + s_b1[ch]) + s_bnb[ch] : 0.f;
+    }
+    // ---- 3. per 32-channel chunk: E in flight while u is formed, then the GEMM ---------------------
+    for (int c0 = 0; c0 < nsc; c0 += 32) {
+      // this lane's E fragments: logit row l16, taps 0..10, channels cs + c0 + grp * 8 .. + 8
+      typedef typename LmFrag<ET>::frag EF;
+      EF ef[BAND];
+#pragma unroll
+      for (int k = 0; k < BAND; ++k) ef[k] = LmFrag<ET>::ld(emat + (int64_t)(l16 * BAND + k) * cp + cs + c0 + grp * 8);
+      __syncthreads();  // alpha / beta ready; the previous chunk's MFMAs are done with us
+      // u = relu(alpha * a + beta), 8 channels per task, one 16-byte LDS store
+      for (int e = tid; e < LM_UR * LM_TW * 4; e += LM_THREADS) {
+        const int g = e & 3, q = e >> 2, col = q & (LM_TW - 1), r = q >> 4;
+        const int gy = h0 - HALF_BAND + r;
+        const bool rv = gy >= 0 && gy < h;
+        const int ch = c0 + g * 8;
+        const floatx4 al0 = *(const floatx4*)&s_alpha[col][ch], al1 = *(const floatx4*)&s_alpha[col][ch + 4];
+        const floatx4 be0 = *(const floatx4*)&s_beta[col][ch], be1 = *(const floatx4*)&s_beta[col][ch + 4];
+        const floatx4 a0 = *(const floatx4*)&s_a[r][ch], a1 = *(const floatx4*)&s_a[r][ch + 4];
+        ET* dst = us + (r * LM_TW + col) * LDU + g * 8;
+        if constexpr (sizeof(ET) == 2) {
+          half8_t v;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v[j] = (half_t)(rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f);
+            v[j + 4] = (half_t)(rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f);
           }
+          *(half8_t*)dst = v;
+        } else {
+          floatx4 v0, v1;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            v0[j] = rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f;
+            v1[j] = rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f;
+          }
+          ((floatx4*)dst)[0] = v0;
+          ((floatx4*)dst)[1] = v1;
         }
-        al = bna[gc] * S;
-        be = bna[gc] * (B + b1[gc]) + bnb[gc];
       }
-      s_alpha[col][ch] = al;
-      s_beta[col][ch] = be;
-    }
+      __syncthreads();
 #pragma unroll
-    for (int e = tid; e < LM_UR * 32; e += LM_THREADS) {
-      const int ch = e & 31, r = e >> 5;
-      const int gy = h0 - HALF_BAND + r, gc = c0 + ch;
-      s_a[r][ch] = (gy >= 0 && gy < h && gc < c) ? arow_n[gy * c + gc] : 0.f;
-    }
-    __syncthreads();
-    // u = relu(alpha * a + beta), 8 channels per task, one 16-byte LDS store
-    for (int e = tid; e < LM_UR * LM_TW * 4; e += LM_THREADS) {
-      const int g = e & 3, q = e >> 2, col = q & (LM_TW - 1), r = q >> 4;
-      const int gy = h0 - HALF_BAND + r;
-      const bool rv = gy >= 0 && gy < h;
-      const floatx4 al0 = *(const floatx4*)&s_alpha[col][g * 8], al1 = *(const floatx4*)&s_alpha[col][g * 8 + 4];
-      const floatx4 be0 = *(const floatx4*)&s_beta[col][g * 8], be1 = *(const floatx4*)&s_beta[col][g * 8 + 4];
-      const floatx4 a0 = *(const floatx4*)&s_a[r][g * 8], a1 = *(const floatx4*)&s_a[r][g * 8 + 4];
-      ET* dst = us + (r * LM_TW + col) * LDU + g * 8;
-      if constexpr (sizeof(ET) == 2) {
-        half8_t v;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[j] = (half_t)(rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f);
-          v[j + 4] = (half_t)(rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f);
-        }
-        *(half8_t*)dst = v;
-      } else {
-        floatx4 v0, v1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v0[j] = rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f;
-          v1[j] = rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f;
-        }
-        ((floatx4*)dst)[0] = v0;
-        ((floatx4*)dst)[1] = v1;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < BAND; ++k) {
-      const ET* ap = es + (l16 * BAND + k) * LDU + grp * 8;
-      if constexpr (sizeof(ET) == 2) {
-        const half8_t af = *(const half8_t*)ap;
+      for (int k = 0; k < BAND; ++k) {
 #pragma unroll
         for (int f = 0; f < 4; ++f) {
           const int r = wave * 4 + f;  // tile row of this fragment
-          const half8_t bfr = *(const half8_t*)&us[((r + k) * LM_TW + l16) * LDU + grp * 8];
-          acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bfr, acc[f], 0, 0, 0);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float av = ap[j];
-#pragma unroll
-          for (int f = 0; f < 4; ++f) {
-            const int r = wave * 4 + f;
-            acc[f] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, us[((r + k) * LM_TW + l16) * LDU + grp * 8 + j],
-                                                          acc[f], 0, 0, 0);
-          }
+          acc[f] = LmFrag<ET>::mma(ef[k], &us[((r + k) * LM_TW + l16) * LDU + grp * 8], acc[f]);
         }
       }
     }

@@ -47,21 +47,85 @@ __global__ __launch_bounds__(256) void se_pool_nhwc_kernel(const T* x, float* pa
 
 // ---- SE MLP: one block per image ---------------------------------------------------------
 // partial: [N][tiles][C] sums (tiles = 1 for plane sums); mean = sum * inv_count.
+// staged = 1 (host checked the LDS size): one coalesced round trip brings the
+// image's partials and both weight matrices into LDS, then every reduction runs
+// from LDS (column sums over tiles with 4 independent chains, 8 threads per
+// hidden unit).  staged = 0: the same math straight from global memory.
+constexpr int SE_MAXLD = 32;   // loads in flight per thread per round
+
 __global__ __launch_bounds__(256) void se_mlp_kernel(const float* partial, int tiles, float inv_count,
                                                     const float* w1, const float* b1, const float* w2,
-                                                    const float* b2, float* att, int c, int hid) {
+                                                    const float* b2, float* att, int c, int hid, int staged) {
   extern __shared__ float lds[];
-  float* g = lds;        // [C]
-  float* hbuf = g + c;   // [hid]
-  const int n = blockIdx.x;
-  for (int ch = threadIdx.x; ch < c; ch += 256) {
+  float* g = lds;            // [C]
+  float* hbuf = g + c;       // [hid]
+  float* sp = hbuf + hid;    // staged: [tiles][C]
+  float* sw1 = sp + tiles * c;   // staged: [hid][C]
+  float* sw2 = sw1 + hid * c;    // staged: [hid][C] (transposed)
+  const int n = blockIdx.x, tid = threadIdx.x;
+  const float* pn = partial + (int64_t)n * tiles * c;
+  if (staged) {
+    const int np = tiles * c, nw = hid * c, ntot = np + 2 * nw;
+    for (int b0 = 0; b0 < ntot; b0 += SE_MAXLD * 256) {
+      float v[SE_MAXLD];
+#pragma unroll
+      for (int u = 0; u < SE_MAXLD; ++u) {
+        const int e = b0 + tid + u * 256;
+        const float* src = e < np ? pn + e : e < np + nw ? w1 + (e - np) : w2 + (e - np - nw);
+        v[u] = e < ntot ? *src : 0.f;   // one load per element
+      }
+#pragma unroll
+      for (int u = 0; u < SE_MAXLD; ++u) {
+        const int e = b0 + tid + u * 256;
+        if (e < np + nw) {
+          sp[e] = v[u];   // sp and sw1 are contiguous
+        } else if (e < ntot) {  // w2 [C][hid] -> sw2 [hid][C]: lanes along channels read distinct banks
+          const int f = e - np - nw, ch = f / hid, j = f - ch * hid;
+          sw2[j * c + ch] = v[u];
+        }
+      }
+    }
+    __syncthreads();
+    for (int ch = tid; ch < c; ch += 256) {
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+      int t = 0;
+      for (; t + 4 <= tiles; t += 4) {
+        s0 += sp[t * c + ch];
+        s1 += sp[(t + 1) * c + ch];
+        s2 += sp[(t + 2) * c + ch];
+        s3 += sp[(t + 3) * c + ch];
+      }
+      for (; t < tiles; ++t) s0 += sp[t * c + ch];
+      g[ch] = ((s0 + s1) + (s2 + s3)) * inv_count;
+    }
+    __syncthreads();
+    // hidden unit j: 8 threads, strided channel slices, shuffle-reduced
+    for (int j0 = 0; j0 < hid; j0 += 32) {
+      const int j = j0 + (tid >> 3), part = tid & 7;
+      float acc = 0.f;
+      if (j < hid)
+        for (int ch = part; ch < c; ch += 8) acc += sw1[j * c + ch] * g[ch];
+      acc += __shfl_xor(acc, 1);
+      acc += __shfl_xor(acc, 2);
+      acc += __shfl_xor(acc, 4);
+      if (j < hid && part == 0) hbuf[j] = fmaxf(acc + (b1 ? b1[j] : 0.f), 0.f);
+    }
+    __syncthreads();
+    for (int ch = tid; ch < c; ch += 256) {
+      float acc = b2 ? b2[ch] : 0.f;
+      for (int j = 0; j < hid; ++j) acc += sw2[j * c + ch] * hbuf[j];
+      att[(int64_t)n * c + ch] = sigmoidf_(acc);
+    }
+    return;
+  }
+  for (int ch = tid; ch < c; ch += 256) {
     float acc = 0.f;
 #pragma unroll 8
-    for (int t = 0; t < tiles; ++t) acc += partial[((int64_t)n * tiles + t) * c + ch];
+    for (int t = 0; t < tiles; ++t) acc += pn[(int64_t)t * c + ch];
     g[ch] = acc * inv_count;
   }
   __syncthreads();
-  for (int j = threadIdx.x; j < hid; j += 256) {
+  for (int j = tid; j < hid; j += 256) {
     float acc = b1 ? b1[j] : 0.f;
     const float* wr = w1 + (int64_t)j * c;
 #pragma unroll 8
@@ -69,7 +133,7 @@ __global__ __launch_bounds__(256) void se_mlp_kernel(const float* partial, int t
     hbuf[j] = fmaxf(acc, 0.f);
   }
   __syncthreads();
-  for (int ch = threadIdx.x; ch < c; ch += 256) {
+  for (int ch = tid; ch < c; ch += 256) {
     float acc = b2 ? b2[ch] : 0.f;
     const float* wr = w2 + (int64_t)ch * hid;
 #pragma unroll 8
@@ -464,10 +528,12 @@ extern "C" int kad_se_mlp(const float* partial, int tiles, float inv_count, cons
                           const float* w2, const float* b2, float* att, int n, int c, int hid, void* stream) {
   KAD_CHECK_ARG(partial && w1 && w2 && att, "kad_se_mlp: null pointer");
   KAD_CHECK_ARG(n > 0 && c > 0 && hid > 0 && tiles > 0, "kad_se_mlp: bad shape");
-  const size_t lds = (size_t)(c + hid) * sizeof(float);
-  KAD_CHECK_ARG(lds <= 64 * 1024, "kad_se_mlp: C + hidden too large");
-  hipLaunchKernelGGL(se_mlp_kernel, dim3(n), dim3(256), lds, (hipStream_t)stream, partial, tiles, inv_count, w1, b1,
-                     w2, b2, att, c, hid);
+  const size_t lds_small = (size_t)(c + hid) * sizeof(float);
+  KAD_CHECK_ARG(lds_small <= 64 * 1024, "kad_se_mlp: C + hidden too large");
+  const size_t lds_staged = lds_small + ((size_t)tiles * c + 2 * (size_t)hid * c) * sizeof(float);
+  const int staged = lds_staged <= 64 * 1024 ? 1 : 0;
+  hipLaunchKernelGGL(se_mlp_kernel, dim3(n), dim3(256), staged ? lds_staged : lds_small, (hipStream_t)stream,
+                     partial, tiles, inv_count, w1, b1, w2, b2, att, c, hid, staged);
   return check_launch("kad_se_mlp");
 }
 

@@ -77,11 +77,23 @@ def time_eager(fn, steps, warmup=3):
     return a.elapsed_time(b) * 1e3 / steps
 
 
+def metric_state(dim, seed=0):
+    """Synthetic weights of the metric's layer as the workload spec defines
+    them: kaiming-uniform convolutions and biases by state-dict name (seed 0),
+    conv_offset ~ N(0, 2 / sqrt(9 c)) with zero bias (offsets ~2 px per unit of
+    input scale), identity branch BatchNorm, branch scale 1."""
+    from oracle import kadconv_oracle as O
+    sd = O.make_kadconv_state(dim, seed=seed, offset_std_px=2.0, bn_random=False)
+    for k in list(sd):
+        if k.startswith('weight.'):
+            sd[k] = torch.ones_like(sd[k])
+    return sd
+
+
 def build_kadconv(dim, dtype, seed=0):
     import kadconv
-    from oracle import kadconv_oracle as O
     m = kadconv.KADConv(dim)
-    m.load_state_dict(O.make_kadconv_state(dim, seed=seed), strict=False)
+    m.load_state_dict(metric_state(dim, seed), strict=False)
     return m.to('cuda', dtype).eval()
 
 
@@ -96,7 +108,7 @@ def cpu_baseline(shape, runs=5, warmup=2):
     from oracle import kadconv_oracle as O
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    sd = O.make_kadconv_state(shape[1])
+    sd = metric_state(shape[1])
     x = torch.randn(*shape, generator=torch.Generator().manual_seed(0))
     ts = []
     with torch.no_grad():
@@ -165,6 +177,72 @@ def per_op(steps, warmup):
     return res
 
 
+TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'dsc0_traffic.json')
+PROBE_COPY_BYTES = 64 << 20
+
+
+def traffic_probe():
+    """A short program for the two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE): a plain 64 MiB device copy (the scale reference) and the
+    dominant kernel (branch-0 DSC of the metric's forward), 5 dispatches each."""
+    import kadconv
+    m = build_kadconv(256, torch.float16)
+    kadconv.enable_fast_inference(m)
+    x = torch.randn(8, 256, 100, 100, generator=torch.Generator().manual_seed(0)).to('cuda', torch.float16)
+    with torch.no_grad():
+        st, _ = m._kad_plan.stages(x)
+        for _, fn in st:
+            fn()
+        dsc0 = dict(st)['dsc0']
+        a = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device='cuda')
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            dsc0()
+        torch.cuda.synchronize()
+    print(json.dumps({'probe': 'done', 'copy_bytes': PROBE_COPY_BYTES}), flush=True)
+
+
+def traffic_from(fetch_csv, write_csv):
+    """HBM bytes per launch of the dominant kernel from the two --pmc runs of
+    traffic_probe(): each counter (KiB per dispatch) is scaled by what it reads
+    for the 64 MiB copy, whose true traffic is 64 MiB read + 64 MiB written."""
+    import csv
+    import statistics
+
+    def per_kernel(path, counter):
+        # dispatches of the largest grid of each kind: the 64 MiB copy and the branch-0 DSC
+        rows = {'copy': [], 'dsc0': []}
+        for r in csv.DictReader(open(path)):
+            if r['Counter_Name'] != counter:
+                continue
+            name = r['Kernel_Name']
+            grid = int(r.get('Grid_Size') or r.get('Grid_Size_X') or 0)
+            kind = 'dsc0' if 'dcn_fwd_kernel' in name else 'copy' if 'copy' in name.lower() else None
+            if kind:
+                rows[kind].append((grid, float(r['Counter_Value'])))
+        out = {}
+        for kind, v in rows.items():
+            gmax = max(g for g, _ in v)
+            out[kind] = statistics.median([x for g, x in v if g == gmax])
+        return out
+
+    f, w = per_kernel(fetch_csv, 'FETCH_SIZE'), per_kernel(write_csv, 'WRITE_SIZE')
+    sf = PROBE_COPY_BYTES / (f['copy'] * 1024.0)
+    sw = PROBE_COPY_BYTES / (w['copy'] * 1024.0)
+    rd, wr = f['dsc0'] * 1024.0 * sf, w['dsc0'] * 1024.0 * sw
+    out = {'kernel': 'dcn_fwd_kernel<half,half,6,FUSED> branch-0 DSC, [8,86,100,100] fp16',
+           'fetch_kib_raw': f['dsc0'], 'write_kib_raw': w['dsc0'],
+           'copy_fetch_kib_raw': f['copy'], 'copy_write_kib_raw': w['copy'],
+           'fetch_scale': sf, 'write_scale': sw,
+           'read_bytes': rd, 'write_bytes': wr, 'bytes_per_launch': rd + wr}
+    json.dump(out, open(TRAFFIC_FILE, 'w'), indent=1)
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -172,7 +250,16 @@ def main():
     ap.add_argument('--warmup', type=int, default=20)
     ap.add_argument('--no-ops', action='store_true', help='skip the per-op table of the other configs')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
+    ap.add_argument('--traffic-probe', action='store_true', help='short program for the rocprofv3 --pmc passes')
+    ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
+                    help='compute profiles/dsc0_traffic.json from the two --pmc counter CSVs')
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_from(*args.traffic_from)
+        return
+    if args.traffic_probe:
+        traffic_probe()
+        return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU: every GPU box of this build has one MI355X and the KAD-Conv forward '
               'shards by batch with no exchange; run with --gpus 1', file=sys.stderr)
@@ -205,9 +292,8 @@ def main():
         achieved = flops / (dcn_us * 1e-6)
 
     traffic = None
-    tfile = os.path.join(ROOT, 'profiles', 'dcn0_traffic.json')
-    if os.path.exists(tfile):
-        traffic = json.load(open(tfile)).get('bytes_per_launch')
+    if os.path.exists(TRAFFIC_FILE):
+        traffic = json.load(open(TRAFFIC_FILE)).get('bytes_per_launch')
 
     out = {
         'metric': 'KAD-Conv fwd us & % roofline at [8,256,100,100] fp16; KAD-CNet-S img/s bs16',
@@ -221,7 +307,8 @@ def main():
         'scaling': 'weak',
         'vs_baseline': None,
         'dtype': 'f16',
-        'data': 'synthetic: x ~ N(0,1) seed 0; random-init weights by state-dict name (seed 0)',
+        'data': 'synthetic: x ~ N(0,1) seed 0; weights by state-dict name (seed 0): kaiming-uniform convs, '
+                'conv_offset ~ N(0, 2/sqrt(9c)), identity BN, branch scale 1',
         'config': {'workload': 'KADConv(256) forward, x [8,256,100,100] fp16, NCHW, HIP-graph replay',
                    'batch': 8, 'channels': 256, 'hw': [100, 100], 'branches': 3},
         'roofline': {'bound': 'mfma', 'achieved': round(achieved / 1e12, 3), 'peak': PEAK_MFMA_F16 / 1e12,

@@ -834,6 +834,43 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
 #pragma unroll
         for (int b = 0; b < NBF; ++b) bn[b] = ld8<T>(wrow[b] + (c * 9) * 32);
       }
+      if constexpr (BLDS) {
+        // Software-pipelined taps (fully unrolled, so the buffers rotate without
+        // moves): the LDS reads of tap k + 1 (weights, corners) and the sample
+        // records of tap k + 2 are in flight while tap k blends and multiplies.
+        const char* rb = (const char*)region + grp * 8 * (int)sizeof(T);
+        Info inf[3][DCN_WM];
+        frag bq[2][NBF], cq[2][DCN_WM][4];
+        auto rd_info = [&](int k, Info (&d)[DCN_WM]) {
+#pragma unroll
+          for (int m = 0; m < DCN_WM; ++m) d[m] = s_info[k * DCN_TILE + m * 16 + ibase];
+        };
+        auto rd_tap = [&](int k, const Info (&in)[DCN_WM], frag (&bd)[NBF], frag (&cd)[DCN_WM][4]) {
+#pragma unroll
+          for (int b = 0; b < NBF; ++b) bd[b] = b_read<T, NB>(bsm, k, b * 16 + row, grp);
+#pragma unroll
+          for (int m = 0; m < DCN_WM; ++m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) cd[m][j] = ld8<T>((const T*)(rb + corner(in[m], j)));
+        };
+        rd_info(0, inf[0]);
+        rd_info(1, inf[1]);
+        rd_tap(0, inf[0], bq[0], cq[0]);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+          const int cur = k & 1, nxt = cur ^ 1;
+          if (k + 2 < 9) rd_info(k + 2, inf[(k + 2) % 3]);
+          if (k + 1 < 9) rd_tap(k + 1, inf[(k + 1) % 3], bq[nxt], cq[nxt]);
+          frag af[DCN_WM];
+#pragma unroll
+          for (int m = 0; m < DCN_WM; ++m)
+            af[m] = Ops::blend(cq[cur][m][0], cq[cur][m][1], cq[cur][m][2], cq[cur][m][3], inf[k % 3][m]);
+#pragma unroll
+          for (int m = 0; m < DCN_WM; ++m)
+#pragma unroll
+            for (int b = 0; b < NBF; ++b) acc[m][b] = Ops::mma(af[m], bq[cur][b], acc[m][b]);
+        }
+      } else {
       Info ic[DCN_WM], inx[DCN_WM];
 #pragma unroll
       for (int m = 0; m < DCN_WM; ++m) inx[m] = s_info[m * 16 + ibase];
@@ -846,10 +883,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
           for (int m = 0; m < DCN_WM; ++m) inx[m] = s_info[(k + 1) * DCN_TILE + m * 16 + ibase];
         }
         frag bf[NBF];
-        if constexpr (BLDS) {
-#pragma unroll
-          for (int b = 0; b < NBF; ++b) bf[b] = b_read<T, NB>(bsm, k, b * 16 + row, grp);
-        } else {
+        {
 #pragma unroll
           for (int b = 0; b < NBF; ++b) bf[b] = bn[b];
           if (k < 8) {
@@ -871,6 +905,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
         for (int m = 0; m < DCN_WM; ++m)
 #pragma unroll
           for (int b = 0; b < NBF; ++b) acc[m][b] = Ops::mma(af[m], bf[b], acc[m][b]);
+      }
       }
       if (c + 1 < g.nchunk) {
         __syncthreads();  // every wave is done with this chunk's region and weights

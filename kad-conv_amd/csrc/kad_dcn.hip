@@ -19,9 +19,11 @@
 //  FUSED  offsets = conv_offset(x) computed in the block   -> kad_dsc_fwd
 //  PLAIN  ordinary 3x3 convolution (no sampling)          -> kad_conv3x3_fwd
 //
-// Block = 256 threads (4 waves) x one output tile of up to 128 pixels (TH x TW,
-// chosen per image size to waste few lanes) x 16 * NBF output channels; wave w
-// owns tile pixels [32 w, 32 w + 32) and all the block's channels.
+// Block = 512 threads (8 waves, two per SIMD, so one wave's LDS / memory waits
+// overlap the other's MFMA and blend work) x one output tile of up to 128
+// pixels (TH x TW, chosen per image size to waste few lanes) x 16 * NBF output
+// channels; wave w owns tile pixels [16 w, 16 w + 16) and all the block's
+// channels.
 //  0. Loads that do not depend on anything are issued first: epilogue
 //     parameters, the mask (and offsets in EXT mode), the first input chunk.
 //  1. PLAIN / FUSED: the tile's 3x3 footprint (tile + 1-pixel ring, zero
@@ -39,7 +41,7 @@
 //     slice [pixels][32 ch] and, on 16-bit paths, the chunk's weights
 //     [9 taps][cols][32] are staged in LDS; for each tap each lane builds its
 //     MFMA A fragment (8 channels of one (pixel, tap)) from four 16-byte LDS
-//     corner reads blended with packed FMAs, and the wave issues 2 x NBF
+//     corner reads blended with packed FMAs, and the wave issues NBF
 //     v_mfma_f32_16x16x32 against 16-byte B fragments.  Weight rows are
 //     64 bytes, so their four 16-byte pieces are stored XOR-swizzled by
 //     column (piece g of column c at slot g ^ ((c >> 1) & 3)): the 16 lanes
@@ -57,14 +59,21 @@
 
 namespace kad {
 
-constexpr int DCN_THREADS = 256;
-constexpr int DCN_WM = 2;                          // 16-pixel A fragments per wave
-constexpr int DCN_TILE = 4 * DCN_WM * 16;          // 128 pixels per block
+#ifndef KAD_DCN_WAVES
+#define KAD_DCN_WAVES 8
+#endif
+constexpr int DCN_WAVES = KAD_DCN_WAVES;           // waves per block (8: two per SIMD)
+constexpr int DCN_THREADS = 64 * DCN_WAVES;
+constexpr int DCN_WM = 8 / DCN_WAVES;              // 16-pixel A fragments per wave
+constexpr int DCN_TILE = DCN_WAVES * DCN_WM * 16;  // 128 pixels per block
 constexpr int DCN_NPAIR = 9 * DCN_TILE;            // (tap, pixel) samples per block
-constexpr int DCN_PPT = DCN_NPAIR / DCN_THREADS + 1;  // samples per thread (pixel tid % 128, taps tid / 128 + 2u)
+constexpr int DCN_KSTEP = DCN_THREADS / DCN_TILE;  // sample (tap, pixel) of thread t: pixel t % 128, taps t / 128 + KSTEP u
+constexpr int DCN_PPT = (9 + DCN_KSTEP - 1) / DCN_KSTEP;  // samples per thread
 constexpr int DCN_NOFF = 18;                       // offset channels (2 x 9 taps)
 constexpr int DCN_LDS = 160 * 1024;                // gfx950 LDS per CU
+constexpr int DCN_SLOT = DCN_THREADS / 4;          // region pixels staged per round (4 threads per pixel)
 constexpr int DCN_FCAP = 704;                      // footprint pixels (enough for stride <= 2)
+static_assert(DCN_TILE == 128 && DCN_SLOT % 64 == 0, "tile / staging geometry");
 
 enum { MODE_EXT = 0, MODE_FUSED = 1, MODE_PLAIN = 2 };
 
@@ -267,15 +276,17 @@ template <typename T, typename OutT, int NBF, int MODE> struct DcnLds {
   static constexpr int NOFF = MODE == MODE_FUSED ? DCN_TILE * DCN_NOFF : 1;
   static constexpr int SROW = NB + 16 / (int)sizeof(OutT);  // epilogue staging row (elements)
   static constexpr int FIXED = BSM * (int)sizeof(T) + NINFO * ((int)sizeof(typename InfoOf<T>::type) + 1) +
-                               NOFF * 4 + 2 * 4 * NB * 4 + 256;
-  static constexpr int STAGE_PX = (DCN_TILE * SROW * (int)sizeof(OutT) + PXB - 1) / PXB;
-  // region staging uses RCAP / 64 pieces per thread; the epilogue tile reuses the region
-  static constexpr int RCAP_WANT = (STAGE_PX > 768 ? STAGE_PX : 768) + 63 - ((STAGE_PX > 768 ? STAGE_PX : 768) + 63) % 64;
+                               NOFF * 4 + 4 * NB * 4 + 256;
+  static constexpr int STAGE_BYTES = DCN_TILE * SROW * (int)sizeof(OutT);  // epilogue tile, then GAP rows [waves][NB]
+  static constexpr int STAGE_PX = (STAGE_BYTES + DCN_WAVES * NB * 4 + PXB - 1) / PXB;
+  // region staging uses RCAP / DCN_SLOT pieces per thread; the epilogue tile reuses the region
+  static constexpr int RCAP_MIN = STAGE_PX > 768 ? STAGE_PX : 768;
+  static constexpr int RCAP_WANT = (RCAP_MIN + 63) / 64 * 64;
   static constexpr int RCAP_FIT = (DCN_LDS - FIXED) / PXB < RCAP_WANT ? (DCN_LDS - FIXED) / PXB : RCAP_WANT;
-  static constexpr int RCAP = RCAP_FIT / 64 * 64;    // staging slots come in 64-pixel rows
+  static constexpr int RCAP = RCAP_FIT / 64 * 64;    // a multiple of 64 pixels
   static_assert(RCAP >= DCN_FCAP, "footprint must fit the region buffer");
   static_assert(MODE == MODE_PLAIN || sizeof(T) == 4 || RCAP * PXB <= 65536, "16-bit corner offsets");
-  static_assert(RCAP * PXB >= DCN_TILE * SROW * (int)sizeof(OutT), "epilogue tile must fit the region buffer");
+  static_assert(RCAP * PXB >= STAGE_BYTES + DCN_WAVES * NB * 4, "epilogue tile must fit the region buffer");
 };
 
 // ---- buffer loads ------------------------------------------------------------------------------
@@ -303,12 +314,14 @@ __device__ __forceinline__ typename DcnFrag<T>::frag buf_ld8(__amdgpu_buffer_rsr
 }
 
 // Chunk staging: up to CAP region pixels x 32 channels, 8-channel pieces,
-// prefetched in registers; piece u of thread t is pixel t / 4 + 64 u, channel
-// group t % 4.  CAP is a multiple of 64 and the LDS buffer holds CAP pixels, so
-// every slot is stored (unused slots receive zeros).
+// prefetched in registers; piece u of thread t is pixel t / 4 + DCN_SLOT u,
+// channel group t % 4.  The LDS buffer holds CAP pixels (a multiple of 64) and
+// every slot below CAP is stored (unused slots receive zeros); only the last
+// round can reach past CAP, when CAP is not a multiple of DCN_SLOT.
 template <typename T, int CAP> struct RegionTile {
-  static_assert(CAP % (DCN_THREADS / 4) == 0, "CAP must be a multiple of 64");
-  static constexpr int RPT = CAP / (DCN_THREADS / 4);
+  static_assert(CAP % 64 == 0, "CAP must be a multiple of 64");
+  static constexpr int RPT = (CAP + DCN_SLOT - 1) / DCN_SLOT;
+  static constexpr bool RAGGED = CAP % DCN_SLOT != 0;
   typename DcnFrag<T>::frag v[RPT];
   uint32_t voff[RPT];  // byte offset of the piece's chunk-0 channels in the image, or DCN_OOB
   // npix = rows x cols pixels starting at (y0, x0); parts outside the image read 0
@@ -316,7 +329,7 @@ template <typename T, int CAP> struct RegionTile {
                                         int tid) {
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
-      const int q = (tid >> 2) + u * (DCN_THREADS / 4);
+      const int q = (tid >> 2) + u * DCN_SLOT;
       uint32_t o = DCN_OOB;
       if (q < npix) {
         const int qy = (int)(((float)q + 0.5f) * inv_cols);
@@ -336,7 +349,8 @@ template <typename T, int CAP> struct RegionTile {
   __device__ __forceinline__ void store(T* region, int pxs, int tid) {
     T* base = region + (tid >> 2) * pxs + (tid & 3) * 8;
 #pragma unroll
-    for (int u = 0; u < RPT; ++u) st8<T>(base + u * (DCN_THREADS / 4) * pxs, v[u]);
+    for (int u = 0; u < RPT; ++u)
+      if (!RAGGED || u + 1 < RPT || (tid >> 2) + u * DCN_SLOT < CAP) st8<T>(base + u * DCN_SLOT * pxs, v[u]);
   }
 };
 
@@ -583,7 +597,6 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   __shared__ unsigned char s_slow[L::NINFO];         // [9][128] 1 = sample outside the capped region
   __shared__ float s_off[L::NOFF];                   // FUSED: [128][18] offsets of the tile
   __shared__ float s_par[4][NB];                     // bias, post_mul, post_add, post_scale
-  __shared__ float gap_red[4][NB];
   __shared__ int s_box[4];       // ymin, ymax, xmin, xmax (clamped corners of live samples)
   __shared__ int s_reg[5];       // region y0, x0, rows, cols, capped flag
 
@@ -617,7 +630,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       if (a.post_scale) par[3] = a.post_scale[co];
     }
   }
-  // this thread's prologue pixel (taps tid / 128 + 2u)
+  // this thread's prologue pixel (taps tid / 128 + KSTEP u)
   const int ppl = tid & (DCN_TILE - 1);
   const int ppy = (int)(((float)ppl + 0.5f) * g.inv_tw), ppx = ppl - ppy * g.tw;
   const int poy = ty0 + ppy, pox = tx0 + ppx;
@@ -627,7 +640,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   if constexpr (MODE != MODE_PLAIN) {
 #pragma unroll
     for (int u = 0; u < DCN_PPT; ++u) {
-      const int k = (tid >> 7) + 2 * u;
+      const int k = tid / DCN_TILE + DCN_KSTEP * u;
       pre_dy[u] = pre_dx[u] = 0.f;
       pre_m[u] = 1.f;
       if (k < 9 && plive) {
@@ -694,7 +707,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
     float smp_w[DCN_PPT][4];
 #pragma unroll
     for (int u = 0; u < DCN_PPT; ++u) {
-      const int k = (tid >> 7) + 2 * u;
+      const int k = tid / DCN_TILE + DCN_KSTEP * u;
       float* w = smp_w[u];
       w[0] = w[1] = w[2] = w[3] = 0.f;
       int cy0 = 0, cx0 = 0, sy = 0, sx = 0;
@@ -788,7 +801,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
     }
 #pragma unroll
     for (int u = 0; u < DCN_PPT; ++u) {
-      const int k = (tid >> 7) + 2 * u;
+      const int k = tid / DCN_TILE + DCN_KSTEP * u;
       if (k >= 9) break;
       const int q = k * DCN_TILE + ppl;
       float* w = smp_w[u];
@@ -971,6 +984,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   // ---- 4. epilogue: values -> LDS tile -> row-contiguous stores; GAP partials ------------------------
   constexpr int SROW = L::SROW;
   OutT* ost = (OutT*)region;
+  float(*gap_red)[NB] = (float(*)[NB])((char*)region + L::STAGE_BYTES);
   __syncthreads();  // every wave is done reading the region
   bool pix_ok[DCN_WM][4];
 #pragma unroll
@@ -1054,7 +1068,9 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   if (a.gap_partial && tid < NB) {
     const int co = co0 + tid;
     if (co < a.cout) {
-      const float v = (gap_red[0][tid] + gap_red[1][tid]) + (gap_red[2][tid] + gap_red[3][tid]);
+      float v = 0.f;
+#pragma unroll
+      for (int i = 0; i < DCN_WAVES; ++i) v += gap_red[i][tid];
       a.gap_partial[((int64_t)n * g.tiles + tile) * a.cout + co] = v;
     }
   }

@@ -44,6 +44,15 @@ template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) { return
 // Logistic function built on the HIP device expf.
 __device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }
 
+// Raw buffer access: a load at a byte offset at or past the descriptor's size
+// returns 0 (no fault), so out-of-range pieces need no branch.  Offsets are
+// 32-bit: callers keep the addressed range below 2^31 bytes, which keeps
+// KAD_OOB out of range.  A descriptor must be wave-uniform.
+constexpr uint32_t KAD_OOB = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ inline int round_up(int a, int b) { return ceil_div(a, b) * b; }
 

@@ -294,11 +294,7 @@ template <typename T, typename OutT, int NBF, int MODE> struct DcnLds {
 // size, so pieces outside the image (padding ring, channels past Cin, unused
 // staging slots) are staged as zeros with no branch; per-thread byte offsets are
 // computed once per block and only shifted per channel chunk.
-constexpr uint32_t DCN_OOB = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
+constexpr uint32_t DCN_OOB = KAD_OOB;
 
 template <typename T>
 __device__ __forceinline__ typename DcnFrag<T>::frag buf_ld8(__amdgpu_buffer_rsrc_t r, uint32_t voff) {

@@ -122,7 +122,9 @@ int kad_dsc_fwd(const kad_dcn_args *a, void *stream);
 /* 1x1 convolution GEMM with fused input average pool and bias/SiLU epilogue */
 /* ------------------------------------------------------------------------ */
 
-/* Elements of the packed weight buffer: [roundup(roundup(Cout,8),128)][roundup(Cin,32)], dtype. */
+/* Elements of the packed weight buffer (dtype): the rows
+ * [roundup(roundup(Cout,8),128)][roundup(Cin,32)], then the same values in the
+ * MFMA fragment order of the NCHW fast path (twice the row layout in all). */
 int64_t kad_gemm_wpack_elems(int cin, int cout);
 
 /* Pack fp32 weights [Cout][Cin] (device) for kad_gemm1x1_fwd. */

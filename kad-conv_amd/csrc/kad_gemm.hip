@@ -176,10 +176,18 @@ __global__ __launch_bounds__(GM_THREADS) void gemm1x1_kernel(kad_gemm_args a, in
 // ---- NCHW fast path -------------------------------------------------------------------------
 // 16-bit NCHW input and output, no pooling, P = H * W a multiple of 4.
 //
-// Block = 256 threads (4 waves) x 128 pixels of one image x 256 output
+// Block = NW waves (4 or 8) x 128 pixels of one image x 64 NW output
 // channels; wave w owns channels [64 w, 64 w + 64) of the block's range and all
-// 128 pixels.  Per 32-channel k-step the input tile [32 ci][128 px] goes to LDS
-// exactly as it lies in memory (16-byte pieces along the pixels, coalesced).
+// 128 pixels (8 waves cover Cout = 512 in one block, so the input tile is read
+// from memory once).  K runs in 32-channel steps.  The input tile of a step,
+// [32 ci][128 px] exactly as it lies in memory (16-byte pieces along the pixels
+// when P % 8 == 0, else 4-byte pieces), goes through a ring of three LDS stages
+// filled by buffer -> LDS loads (no registers in between); each wave's weight
+// fragments (one 16-byte load per lane and fragment from the packed
+// [Cout_pad][Cin_pad] layout, L2-resident) go straight to registers, three
+// buffers rotating with the stages.  Both are issued two steps ahead; a step
+// opens with "own loads of this step landed" (vmcnt) + barrier.  LDS then
+// carries only the input tile: one write and NW reads per step.
 // No transpose pass: MFMA column c of pixel fragment j (j = 0..7) is pixel
 // 8 c + j, so lane (c, g) reads rows 8 g .. 8 g + 7 at pixels 8 c .. 8 c + 7
 // (eight 16-byte LDS reads) and an 8 x 8 transpose of 16-bit values in its own
@@ -187,74 +195,97 @@ __global__ __launch_bounds__(GM_THREADS) void gemm1x1_kernel(kad_gemm_args a, in
 // fragments.  The accumulator of fragment j in lane (c, g) holds channels
 // 4 g + i at pixel 8 c + j, so every lane ends with eight consecutive pixels per
 // output channel: one 16-byte store (two 8-byte stores when P % 8 != 0).
-// A (weights, rows = output channels) is one 16-byte load per lane and
-// fragment from the packed [Cout_pad][Cin_pad] layout, prefetched one k-step
-// ahead like the input tile.  Work items are ordered so the channel blocks of
-// one pixel tile run back to back on the same XCD (shared L2).
-constexpr int GN_PX = 128;         // pixels per tile
-constexpr int GN_WCO = 64;         // output channels per wave
-constexpr int GN_CO = 4 * GN_WCO;  // output channels per block
+// Work items are ordered so the channel blocks of one pixel tile run back to
+// back on the same XCD (shared L2).
+constexpr int GN_PX = 128;              // pixels per tile
+constexpr int GN_WCO = 64;              // output channels per wave
+constexpr int GN_XB = 32 * GN_PX * 2;   // input tile bytes per stage
 
 template <typename T> struct Raw16 { typedef half8_t type; };
 template <> struct Raw16<bf16_t> { typedef bf16x8_t type; };
 
-template <bool V16>
-__device__ __forceinline__ intx4 ld_px8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  if constexpr (V16) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-  } else {  // 8-byte aligned halves
-    typedef int intx2 __attribute__((ext_vector_type(2)));
-    const intx2 lo = __builtin_bit_cast(intx2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-    const intx2 hi = __builtin_bit_cast(intx2, __builtin_amdgcn_raw_buffer_load_b64(r, off + 8, 0, 0));
-    return intx4{lo[0], lo[1], hi[0], hi[1]};
-  }
+#define KAD_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Buffer -> LDS loads of 16 / 4 bytes per lane: lane i's bytes land at dst + size * i.
+// The address is base + soffset (wave-uniform) + voff (per lane).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KAD_LDS(dst), 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KAD_LDS(dst), 4, voff, soff, 0, 0);
 }
 
-template <typename T, bool V16>
-__global__ __launch_bounds__(256, 2) void gemm_nchw_kernel(kad_gemm_args a, int P, int tiles_px, int co_blocks,
-                                                           int total, int cin_pad) {
+template <typename T, bool V16, int NW>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_args a, int P, int tiles_px,
+                                                                    int co_blocks, int total, int cin_pad) {
   typedef typename GemmOps<T>::frag frag;
-  __shared__ __align__(16) T xs[2][32 * GN_PX];  // [ci][px] per stage
+  typedef typename Raw16<T>::type raw_t;
+  constexpr int STAGE = GN_XB;
+  // one object per stage: the compiler tracks the loads into each separately
+  __shared__ __align__(16) char st0[STAGE];
+  __shared__ __align__(16) char st1[STAGE];
+  __shared__ __align__(16) char st2[STAGE];
   const int bid = blockIdx.x;
   const int wi = (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);  // contiguous band of work per XCD
   if (wi >= total) return;  // whole block, before any barrier
   const int cb = wi % co_blocks, t2 = wi / co_blocks;
   const int n = t2 / tiles_px, p0 = (t2 - n * tiles_px) * GN_PX;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, c = lane & 15, g = lane >> 4;
-  const int co_w = cb * GN_CO + wave * GN_WCO;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar offsets below)
+  const int co_w = (cb * NW + wave) * GN_WCO;
   const int nk = cin_pad / 32;
 
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, (uint32_t)((int64_t)a.n * a.cin * P * 2));
   const int cout_pk = round_up(round_up(a.cout, 8), 128);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.wpack, (uint32_t)((int64_t)cout_pk * cin_pad * 2));
-  // staging pieces: rows tid / 16 and 16 + tid / 16, pixels 8 (tid % 16) .. + 8
-  const int sr = tid >> 4, sq = tid & 15;
-  const uint32_t xrow = (uint32_t)(P * 2);
-  const uint32_t xo0 = (uint32_t)((((int64_t)n * a.cin + sr) * P + p0 + 8 * sq) * 2);
-  const uint32_t xo1 = xo0 + 16u * xrow;
-  uint32_t wo[4];
+  // the fragment-ordered copy behind the row layout
+  const __amdgpu_buffer_rsrc_t rw =
+      make_rsrc((const T*)a.wpack + (int64_t)cout_pk * cin_pad, (uint32_t)((int64_t)cout_pk * cin_pad * 2));
+
+  // Input pieces: wave w stages rows RPW w .. + RPW; its load q covers rows
+  // RPW w + RQ q + lr (lr = lane / 16 for 16-byte pieces, else 0) at pixels
+  // p0 + lpx ..; the row base goes in the wave-uniform soffset, the lane part
+  // (pixels, lr rows) in voffset, which is out of range for pixels past the
+  // image row: such lanes read zeros and no load reaches past the tensor.
+  constexpr int RPW = 32 / NW, RQ = V16 ? 4 : 1, XQ = RPW / RQ;
+  const int lr = V16 ? lane >> 4 : 0, lpx = V16 ? 8 * (lane & 15) : 2 * lane;
+  const uint32_t prow = (uint32_t)P * 2u;  // bytes per channel row
+  const uint32_t xlane = p0 + lpx < P ? (uint32_t)lr * prow + (uint32_t)(p0 + lpx) * 2u : KAD_OOB;
+  const int64_t xrow0 = (int64_t)n * a.cin + RPW * wave;  // first row of this wave's pieces (step 0)
+  uint32_t woff[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int co = co_w + 16 * m + c;
-    wo[m] = co < cout_pk ? (uint32_t)((co * cin_pad + 8 * g) * 2) : KAD_OOB;
+    woff[m] = co < cout_pk ? (uint32_t)(((((co_w >> 4) + m) * nk) * 64 + lane) * 16) : KAD_OOB;
   }
-  // Loads for a step past the last one read zeros (out-of-range offsets): the
-  // prefetch is issued unconditionally, so no branch splits the wait counts.
-  auto ld_x = [&](int ks, intx4& v0, intx4& v1) {
-    const int r = ks * 32 + sr;
-    const uint32_t step = (uint32_t)ks * 32u * xrow;
-    v0 = ld_px8<V16>(rx, r < a.cin ? xo0 + step : KAD_OOB);
-    v1 = ld_px8<V16>(rx, r + 16 < a.cin ? xo1 + step : KAD_OOB);
-  };
-  auto ld_w = [&](int ks, frag (&w)[4]) {
+  constexpr int L = XQ + 4;  // loads per wave per step
+  // Loads of step kk: input into stage st, weights into w; a step past the last
+  // one (or a row past Cin) reads zeros, so every path issues the same loads.
+  // Rows past Cin (or steps past the last) get an out-of-range voffset; soffset
+  // stays the uniform row base (< 2^31, so the sum cannot wrap into range).
+  auto issue = [&](int kk, char* st, frag (&w)[4]) {
+    if constexpr (V16) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-      w[m] = __builtin_bit_cast(frag, __builtin_amdgcn_raw_buffer_load_b128(
-                                          rw, (wo[m] == KAD_OOB || ks >= nk) ? KAD_OOB : wo[m] + (uint32_t)ks * 64u, 0, 0));
-  };
-  auto st_x = [&](int s, const intx4& v0, const intx4& v1) {
-    *(intx4*)&xs[s][sr * GN_PX + 8 * sq] = v0;
-    *(intx4*)&xs[s][(sr + 16) * GN_PX + 8 * sq] = v1;
+      for (int q = 0; q < XQ; ++q) {
+        const bool ok = kk < nk && kk * 32 + RPW * wave + RQ * q + lr < a.cin;
+        dma16(rx, st + (RPW * wave + RQ * q) * GN_PX * 2, ok ? xlane : KAD_OOB,
+              (uint32_t)((xrow0 + kk * 32 + RQ * q) * P * 2));
+      }
+    } else {  // rows are wave-uniform: a short rolled loop keeps the offsets in scalars
+      const int rows = kk < nk ? min(a.cin - (kk * 32 + RPW * wave), RPW) : 0;  // valid rows of this wave
+      uint32_t soff = (uint32_t)((xrow0 + kk * 32) * P * 2);
+      char* dst = st + RPW * wave * GN_PX * 2;
+#pragma unroll 1
+      for (int q = 0; q < XQ; ++q) {
+        dma4(rx, dst, q < rows ? xlane : KAD_OOB, soff);
+        soff += prow;
+        dst += GN_PX * 2;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t o = (woff[m] == KAD_OOB || kk >= nk) ? KAD_OOB : woff[m] + (uint32_t)kk * 1024u;
+      w[m] = __builtin_bit_cast(frag, __builtin_amdgcn_raw_buffer_load_b128(rw, o, 0, 0));
+    }
   };
 
   floatx4 acc[4][8];
@@ -263,54 +294,61 @@ __global__ __launch_bounds__(256, 2) void gemm_nchw_kernel(kad_gemm_args a, int 
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[m][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  intx4 v0, v1;
-  frag wa[4], wb[4];
-  ld_x(0, v0, v1);
-  ld_w(0, wa);
-  st_x(0, v0, v1);
-  __syncthreads();
-  // one k-step: prefetch step ks + 1 (input pieces, weights into wnx), multiply
-  // step ks from LDS stage ks & 1 with weights wc, then stage the prefetched tile
-  auto step = [&](int ks, const frag (&wc)[4], frag (&wnx)[4]) {
-    const int s = ks & 1;
-    ld_x(ks + 1, v0, v1);  // rows past Cin (and so every row of step nk) read zeros
-    ld_w(ks + 1, wnx);
-    __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's MFMAs
-    typedef typename Raw16<T>::type raw_t;
+  // step kk: wait for this wave's loads of step kk (those of step kk + 1, L per
+  // wave, may stay in flight) and for every wave's LDS reads of the previous
+  // step, then barrier; refill the stage and weight buffer of the previous step
+  // with step kk + 2; multiply.
+  auto step = [&](int kk, const char* cur, char* refill, const frag (&wf)[4], frag (&wrefill)[4]) {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(L) : "memory");
+    issue(kk + 2, refill, wrefill);
     raw_t raw[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) raw[r] = *(const raw_t*)&xs[s][(8 * g + r) * GN_PX + 8 * c];
+    for (int r = 0; r < 8; ++r) raw[r] = *(const raw_t*)(cur + ((8 * g + r) * GN_PX + 8 * c) * 2);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       frag b;
 #pragma unroll
       for (int r = 0; r < 8; ++r) b[r] = raw[r][j];  // channel 8 g + r of pixel 8 c + j
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc[m][j] = GemmOps<T>::mma(wc[m], b, acc[m][j]);
+      for (int m = 0; m < 4; ++m) acc[m][j] = GemmOps<T>::mma(wf[m], b, acc[m][j]);
     }
-    __builtin_amdgcn_sched_barrier(0);  // the prefetched tile is stored after the MFMAs, not before
-    st_x(s ^ 1, v0, v1);  // stage s ^ 1 was last read before the previous barrier
-    __syncthreads();
   };
-  for (int ks = 0; ks < nk; ks += 2) {  // unrolled by two: the weight buffers swap roles without copies
-    step(ks, wa, wb);
-    if (ks + 1 < nk) step(ks + 1, wb, wa);
+  frag w0[4], w1[4], w2[4];
+  issue(0, st0, w0);
+  issue(1, st1, w1);
+  const int nk3 = nk / 3 * 3;
+  for (int kk = 0; kk < nk3; kk += 3) {  // branch-free body: exact wait counts
+    step(kk, st0, st2, w0, w2);
+    step(kk + 1, st1, st0, w1, w0);
+    step(kk + 2, st2, st1, w2, w1);
   }
+  if (nk3 < nk) step(nk3, st0, st2, w0, w2);
+  if (nk3 + 1 < nk) step(nk3 + 1, st1, st0, w1, w0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the block
 
   // ---- epilogue: bias, activation, eight consecutive pixels per channel ----------------------------
   const int px = p0 + 8 * c;
   const int nvalid = P - px;  // pixels of this lane's run inside the image (>= 8: full run)
+  // every bias first: loads and stores share one in-order counter, so a load
+  // issued after a store would make its wait include that store's write
+  float bias[4][4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int co = co_w + 16 * m + 4 * g + i;
+      bias[m][i] = (a.bias && co < a.cout) ? a.bias[co] : 0.f;
+    }
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int co = co_w + 16 * m + 4 * g + i;
       if (co >= a.cout || nvalid <= 0) continue;
-      const float bias = a.bias ? a.bias[co] : 0.f;
-      typename Raw16<T>::type o;
+      raw_t o;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        float v = acc[m][j][i] + bias;
+        float v = acc[m][j][i] + bias[m][i];
         if (a.act == 1) v = v * __builtin_amdgcn_rcpf(1.f + __expf(-v));  // SiLU; 16-bit output
         o[j] = from_f32<T>(v);
       }
@@ -333,12 +371,22 @@ __global__ __launch_bounds__(256, 2) void gemm_nchw_kernel(kad_gemm_args a, int 
   }
 }
 
+// Packed weights: rows [Cout_pad][Cin_pad] (the general kernel, the pyramid),
+// then the same values in MFMA fragment order for the NCHW fast path: per
+// (16-channel block cb, 32-channel step ks) one 1 KB chunk at
+// ((cb * nk + ks) * 64 + lane) * 8 elements, lane = r + 16 g holding
+// W[16 cb + r][32 ks + 8 g .. + 8], so a wave's fragment load is one
+// contiguous 1 KB read.
 template <typename T>
 __global__ void gemm_pack_kernel(const float* w, T* out, int cin, int cout, int cin_pad, int cout_pad) {
   const int64_t total = (int64_t)cout_pad * cin_pad;
+  const int nk = cin_pad / 32;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
     const int ci = (int)(i % cin_pad), co = (int)(i / cin_pad);
-    out[i] = from_f32<T>((co < cout && ci < cin) ? w[(int64_t)co * cin + ci] : 0.f);
+    const T v = from_f32<T>((co < cout && ci < cin) ? w[(int64_t)co * cin + ci] : 0.f);
+    out[i] = v;
+    const int lane = (co & 15) + 16 * ((ci & 31) >> 3);
+    out[total + ((int64_t)((co >> 4) * nk + (ci >> 5)) * 64 + lane) * 8 + (ci & 7)] = v;
   }
 }
 
@@ -353,17 +401,31 @@ static int launch_gemm(const kad_gemm_args& a, hipStream_t st, int hp, int wp) {
   return check_launch("kad_gemm1x1_fwd");
 }
 
-template <typename T>
-static int launch_gemm_nchw(const kad_gemm_args& a, hipStream_t st) {
+template <typename T, int NW>
+static void launch_gemm_nchw_nw(const kad_gemm_args& a, hipStream_t st) {
   const int P = a.h * a.w;
-  const int tiles_px = ceil_div(P, GN_PX), co_blocks = ceil_div(a.cout, GN_CO);
+  const int tiles_px = ceil_div(P, GN_PX), co_blocks = ceil_div(a.cout, NW * GN_WCO);
   const int total = a.n * tiles_px * co_blocks;
   const int cin_pad = round_up(a.cin, 32);
   dim3 grid(round_up(total, 8));
   if (P % 8 == 0)
-    hipLaunchKernelGGL((gemm_nchw_kernel<T, true>), grid, dim3(256), 0, st, a, P, tiles_px, co_blocks, total, cin_pad);
+    hipLaunchKernelGGL((gemm_nchw_kernel<T, true, NW>), grid, dim3(64 * NW), 0, st, a, P, tiles_px, co_blocks, total,
+                       cin_pad);
   else
-    hipLaunchKernelGGL((gemm_nchw_kernel<T, false>), grid, dim3(256), 0, st, a, P, tiles_px, co_blocks, total, cin_pad);
+    hipLaunchKernelGGL((gemm_nchw_kernel<T, false, NW>), grid, dim3(64 * NW), 0, st, a, P, tiles_px, co_blocks, total,
+                       cin_pad);
+}
+
+// 4-wave blocks, two per CU: independent blocks drift apart, so one block's LDS
+// reads and barrier waits overlap the other's MFMAs (8-wave blocks, one per CU,
+// keep both waves of a SIMD in lockstep and measured slower: 50-55 us against
+// 47.7 us for [16,512,50,50]).  What remains per block (MI355X, 2 blocks per
+// CU): ~1.6k cycles per k-step against 0.5k of MFMA per wave, and an epilogue of
+// ~14k cycles that is mostly SiLU (exp and rcp are quarter-rate: ~6k cycles per
+// wave for its 128 values) run by both blocks of a CU at the same time.
+template <typename T>
+static int launch_gemm_nchw(const kad_gemm_args& a, hipStream_t st) {
+  launch_gemm_nchw_nw<T, 4>(a, st);
   return check_launch("kad_gemm1x1_fwd");
 }
 
@@ -401,8 +463,9 @@ using namespace kad;
 
 extern "C" int64_t kad_gemm_wpack_elems(int cin, int cout) {
   if (cin <= 0 || cout <= 0) return 0;
-  // rows cover every 16-wide column block a launch can touch (NHWC padding included)
-  return (int64_t)round_up(round_up(cout, 8), 128) * round_up(cin, 32);
+  // rows cover every 16-wide column block a launch can touch (NHWC padding included);
+  // row layout followed by the fragment-ordered copy
+  return 2 * (int64_t)round_up(round_up(cout, 8), 128) * round_up(cin, 32);
 }
 
 extern "C" int kad_gemm_pack_weights(const float* w, void* wpack, int cin, int cout, int dtype, void* stream) {

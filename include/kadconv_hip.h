@@ -150,6 +150,15 @@ typedef struct kad_gemm_args {
  * -> kadc_gemm_silu.cu:125-176; acceleration/kadc_fused_sm75.py:504-532,616-629). */
 int kad_gemm1x1_fwd(const kad_gemm_args *a, void *stream);
 
+/* KADDown input pass (the op is builder-defined: no reference counterpart;
+ * definition oracle/kadconv_oracle.py:kaddown_forward).  x NCHW [N][C][H][W]
+ * -> u NCHW [N][nb*C][H/2][W/2], same dtype, with
+ *   u[:, b*C + c] = bilinear_resize(avgpool(x, 2^(b+1))[:, c], (H/2, W/2))
+ * (align_corners=False; b = 0 needs no resize), b < nb <= 3, H, W >= 2^nb.
+ * KADDown is then one kad_gemm1x1_fwd over u with the branch projections
+ * stacked along Cin, softmax(alpha)_b and sigmoid(gate) folded into them. */
+int kad_kaddown_prep(const void *x, void *u, int n, int c, int h, int w, int nb, int dtype, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* One-pass branch pyramid: avg-pool 2^b + 1x1 projection for b = 0..nb-1    */
 /* ------------------------------------------------------------------------ */

@@ -53,6 +53,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// Bilinear resize source index (PyTorch, align_corners=False, output size
+// given): s = max(scale * (dst + 0.5) - 0.5, 0) with scale = in / out; rows
+// i0 = floor(s) and i1 = min(i0 + 1, in - 1), weight of i1 = s - i0.
+__device__ __forceinline__ void src_index(int dst, int in, int out, float scale, int& i0, int& i1, float& l1) {
+  if (in == out) {
+    i0 = i1 = dst;
+    l1 = 0.f;
+    return;
+  }
+  float s = scale * ((float)dst + 0.5f) - 0.5f;
+  if (s < 0.f) s = 0.f;
+  i0 = (int)s;
+  i1 = i0 + ((i0 < in - 1) ? 1 : 0);
+  l1 = s - (float)i0;
+}
+
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ inline int round_up(int a, int b) { return ceil_div(a, b) * b; }
 

@@ -161,19 +161,6 @@ __global__ __launch_bounds__(256) void channel_scale_kernel(const T* x, const fl
 }
 
 // ---- branch merge ------------------------------------------------------------------------
-__device__ __forceinline__ void src_index(int dst, int in, int out, float scale, int& i0, int& i1, float& l1) {
-  if (in == out) {
-    i0 = i1 = dst;
-    l1 = 0.f;
-    return;
-  }
-  float s = scale * ((float)dst + 0.5f) - 0.5f;
-  if (s < 0.f) s = 0.f;
-  i0 = (int)s;
-  i1 = i0 + ((i0 < in - 1) ? 1 : 0);
-  l1 = s - (float)i0;
-}
-
 // Per-branch source rows for output row y (same for every column and channel).
 struct RowSrc { int y0, y1; float ly; };
 

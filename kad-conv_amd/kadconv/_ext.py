@@ -91,6 +91,7 @@ SIGNATURES = {
     'kad_gemm_wpack_elems': (c_i64, [c_int, c_int]),
     'kad_gemm_pack_weights': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     'kad_gemm1x1_fwd': (c_int, [ctypes.POINTER(GemmArgs), c_vp]),
+    'kad_kaddown_prep': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_pyramid_tiles': (c_int, [c_int, c_int, ctypes.POINTER(c_int), ctypes.POINTER(c_int)]),
     'kad_pyramid_proj': (c_int, [ctypes.POINTER(PyramidArgs), c_vp]),
     'kad_lcsa_params_elems': (c_i64, [c_int]),
@@ -305,6 +306,20 @@ def gemm1x1_fwd(x, in_layout, cin, wpack, cout, out, out_layout, *, bias=None, p
         raise TypeError('bias must be float32')
     _check(load().kad_gemm1x1_fwd(ctypes.byref(a), _stream()), 'kad_gemm1x1_fwd')
     return out
+
+
+def kaddown_prep(x, u, nb):
+    """x NCHW [N,C,H,W] -> u NCHW [N,nb*C,H//2,W//2]: the 2^(b+1)-pooled input of
+    branch b resized to (H//2, W//2), stacked along channels."""
+    _need_gpu(x, u)
+    N, C, H, W = x.shape
+    if not x.is_contiguous() or not u.is_contiguous() or tuple(u.shape) != (N, nb * C, H // 2, W // 2):
+        raise ValueError('kaddown_prep: x and u must be contiguous NCHW, u [N, nb*C, H//2, W//2]')
+    if u.dtype != x.dtype:
+        raise TypeError('kaddown_prep: x and u must share a dtype')
+    _check(load().kad_kaddown_prep(_ptr(x), _ptr(u), N, C, H, W, nb, kad_dtype(x.dtype), _stream()),
+           'kad_kaddown_prep')
+    return u
 
 
 # ---------------------------------------------------------------------------- pyramid

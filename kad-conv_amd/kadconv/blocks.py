@@ -47,11 +47,15 @@ class Conv1x1SiLU(nn.Module):
 
     def forward(self, x):
         if _use_hip(self, x):
-            key = (x.dtype, self.conv.weight._version, self.conv.weight.data_ptr())
+            # packed weights and the fp32 bias are cached per parameter version
+            key = (x.dtype, self.conv.weight._version, self.conv.weight.data_ptr(), self.conv.bias._version,
+                   self.conv.bias.data_ptr())
             if key not in self._packed:
-                self._packed = {key: _ext.gemm_pack_weights(self.conv.weight, x.dtype)}
+                self._packed = {key: (_ext.gemm_pack_weights(self.conv.weight, x.dtype),
+                                      self.conv.bias.detach().float().contiguous())}
+            wpack, bias = self._packed[key]
             with torch.no_grad():
-                return ops.conv1x1(x, self.conv.weight, self.conv.bias, act='silu', wpack=self._packed[key])
+                return ops.conv1x1(x, self.conv.weight, bias, act='silu', wpack=wpack)
         return F.silu(self.conv(x))
 
 
@@ -90,41 +94,35 @@ class KADDown(nn.Module):
         return z * torch.sigmoid(self.gate).view(1, -1, 1, 1)
 
     def forward(self, x):
-        s = 2 ** self.n
-        if not _use_hip(self, x) or x.shape[2] < s or x.shape[3] < s or self.n > _ext.MAX_BRANCHES:
+        if not _use_hip(self, x):
             return self._plain(x)
         with torch.no_grad():
             return self._fast(x)
 
     def _fast(self, x):
+        """One input pass (kad_kaddown_prep: the pooled inputs of every branch at
+        (H/2, W/2), stacked along channels) and one 1x1 GEMM over them with the
+        branch projections stacked along Cin; softmax(alpha) and sigmoid(gate)
+        are folded into the packed weights and bias.  A 1x1 projection commutes
+        with the bilinear resize (its weights sum to 1), so this equals the
+        per-branch form of ``_plain``."""
         N, C, H, W = x.shape
         c2 = self.proj[0].weight.shape[0]
-        cs = (c2 + 7) // 8 * 8
-        dtype, dev = x.dtype, x.device
-        # packed weights, softmax coefficients and gate are cached per parameter version
-        # (computing the softmax here per call would force a device->host sync)
+        dtype = x.dtype
+        # folded weights are cached per parameter version (no per-call host work)
         params = [p.weight for p in self.proj] + [p.bias for p in self.proj] + [self.alpha, self.gate]
         key = (dtype,) + tuple((p._version, p.data_ptr()) for p in params)
         if key not in self._packed:
-            self._packed = {key: (
-                [_ext.gemm_pack_weights(p.weight, dtype) for p in self.proj],
-                [p.bias.detach().float().contiguous() for p in self.proj],
-                torch.softmax(self.alpha.detach().double(), dim=0).tolist(),
-                torch.sigmoid(self.gate.detach().float()).contiguous())}
-        packs, biases, coeff, gate = self._packed[key]
-        nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
-        xin, lay = (x.permute(0, 2, 3, 1), _ext.KAD_NHWC) if nhwc else (x.contiguous(), _ext.KAD_NCHW)
-        branches = []
-        for i in range(self.n):
-            s = 2 ** (i + 1)
-            b = torch.empty(N, H // s, W // s, cs, dtype=dtype, device=dev)
-            _ext.gemm1x1_fwd(xin, lay, C, packs[i], c2, b, _ext.KAD_NHWC,
-                             bias=biases[i], pool=s)
-            branches.append({'z': b, 'c': c2, 'c_off': 0, 'att': None, 'coeff': coeff[i]})
-        if nhwc:
-            out = torch.empty(N, c2, H // 2, W // 2, dtype=dtype, device=dev, memory_format=torch.channels_last)
-            _ext.branch_merge(out.permute(0, 2, 3, 1), _ext.KAD_NHWC, branches, gate=gate)
-        else:
-            out = torch.empty(N, c2, H // 2, W // 2, dtype=dtype, device=dev)
-            _ext.branch_merge(out, _ext.KAD_NCHW, branches, gate=gate)
+            a = torch.softmax(self.alpha.detach().float(), dim=0)
+            g = torch.sigmoid(self.gate.detach().float())
+            w = torch.cat([a[i] * self.proj[i].weight.detach().float().reshape(c2, C) for i in range(self.n)], dim=1)
+            b = sum(a[i] * self.proj[i].bias.detach().float() for i in range(self.n))
+            self._packed = {key: (_ext.gemm_pack_weights(w * g[:, None], dtype), (g * b).contiguous())}
+        wpack, bias = self._packed[key]
+        u = torch.empty(N, self.n * C, H // 2, W // 2, dtype=dtype, device=x.device)
+        _ext.kaddown_prep(x.contiguous(), u, self.n)
+        out = torch.empty(N, c2, H // 2, W // 2, dtype=dtype, device=x.device)
+        _ext.gemm1x1_fwd(u, _ext.KAD_NCHW, self.n * C, wpack, c2, out, _ext.KAD_NCHW, bias=bias)
+        if x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous():
+            out = out.contiguous(memory_format=torch.channels_last)
         return out

@@ -67,7 +67,9 @@ def deform_conv2d(input, offset, weight, bias=None, stride=1, padding=0, dilatio
     off = offset.to(torch.float32).contiguous()
     m = mask.to(torch.float32).contiguous() if mask is not None else None
     wp = _ext.dcn_pack_weights(weight, dtype)
-    b = bias.detach().to(torch.float32).contiguous() if bias is not None else None
+    b = None
+    if bias is not None:  # fp32 contiguous biases are used as they are (no per-call copy)
+        b = bias if (bias.dtype == torch.float32 and bias.is_contiguous()) else bias.detach().float().contiguous()
     out = torch.empty(N, Co, Ho, Wo, dtype=dtype, device=input.device)
     _ext.dcn_fwd(x, C, off, (18 * P, 1, P), m, (9 * P, 1, P), wp, Co, out, stride=s[0], pad=p[0], bias=b,
                  out_layout=_ext.KAD_NCHW)

@@ -448,10 +448,10 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
           if (grp == 0 && real && vr > 0)
             rowp[(((int64_t)n * a.ntx + tx) * hbch + ty * tr) * cout + co] = sr + vc * bv;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
+          for (int i = 0; i < 4; ++i) {  // a tile with no row of this branch contributes 0 (the consumer reads every slice)
             const int c = grp * 4 + i;
-            if (real && c < vc && vr > 0)
-              colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] = acc2[bb][i] + bv;
+            if (real && c < vc)
+              colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] = vr > 0 ? acc2[bb][i] + bv : 0.f;
           }
         }
       }
@@ -478,11 +478,11 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
             }
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
+          for (int i = 0; i < 4; ++i) {  // a tile with no row of this branch contributes 0
             const int c = grp * 4 + i;
-            if (c < vc && vr > 0)
+            if (c < vc)
               colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] =
-                  acc1[bb][i] + colred[c * NB + col] + vr * bv;
+                  vr > 0 ? acc1[bb][i] + colred[c * NB + col] + vr * bv : 0.f;
           }
         }
       }

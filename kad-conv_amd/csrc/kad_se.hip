@@ -32,6 +32,42 @@ __global__ __launch_bounds__(256) void se_pool_nchw_kernel(const T* x, float* g,
   if (lane == 0) g[wave] = acc;
 }
 
+// NCHW over the flat tensor in 16-byte pieces (any plane size hw >= 8, which a
+// piece then straddles at most once): wave w sums planes [4 w, 4 w + 4).  Each
+// lane splits a piece at its plane boundary and adds the parts to the plane's
+// running sum; sums are then wave-reduced (fixed order: deterministic).
+template <typename T>
+__global__ __launch_bounds__(256) void se_pool_flat_kernel(const T* x, float* g, int planes, int hw) {
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  const int wv = (blockIdx.x * 256 + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+  const int pb = wv * 4;
+  if (pb >= planes) return;
+  const int pe = pb + 4 < planes ? pb + 4 : planes;
+  const int v_lo = pb * hw / 8, v_hi = (pe * hw + 7) / 8;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int v = v_lo + lane; v < v_hi; v += 64) {
+    const int e0 = v * 8;
+    const t8 xv = *(const t8*)(x + e0);
+    const int p0 = e0 / hw, nb = (p0 + 1) * hw - e0;  // elements of the piece in plane p0
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float xk = to_f32(xv[k]);
+      if (k < nb) s0 += xk; else s1 += xk;
+    }
+    const int k0 = p0 - pb;  // -1 .. 3; parts of planes outside [pb, pe) belong to other waves
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] += (k == k0 ? s0 : 0.f) + (k == k0 + 1 ? s1 : 0.f);
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float v = acc[k];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    if (lane == 0 && pb + k < pe) g[pb + k] = v;
+  }
+}
+
 // NHWC: grid (ceil(P / 256), N); block partial sums over 256 pixels per channel.
 template <typename T>
 __global__ __launch_bounds__(256) void se_pool_nhwc_kernel(const T* x, float* part, int c, int P, int cs,
@@ -47,102 +83,229 @@ __global__ __launch_bounds__(256) void se_pool_nhwc_kernel(const T* x, float* pa
 
 // ---- SE MLP: one block per image ---------------------------------------------------------
 // partial: [N][tiles][C] sums (tiles = 1 for plane sums); mean = sum * inv_count.
-// staged = 1 (host checked the LDS size): one coalesced round trip brings the
-// image's partials and both weight matrices into LDS, then every reduction runs
-// from LDS (column sums over tiles with 4 independent chains, 8 threads per
-// hidden unit).  staged = 0: the same math straight from global memory.
+// Small C (everything fits the 160 KB of LDS, KADConv's branches): 512 threads,
+// one round of up to 32 loads per thread brings the image's partials and both
+// weight matrices into LDS.  Slots past the end load a clamped (valid) address
+// and are dropped at the store, so the loads carry no branches and all are in
+// flight together.  W2 goes to LDS as [C][hid + 1] (row stride odd: a thread
+// per channel reads its row without bank conflicts).  Then, from LDS: tile
+// sums (nsl = 512 / C slices per channel, 4 chains each, slices combined in a
+// fixed order), the hidden layer (8 threads per unit, shuffle-reduced) and the
+// output layer (one thread per channel).
 constexpr int SE_MAXLD = 32;   // loads in flight per thread per round
+constexpr int SE_ST = 512;     // threads of the staged kernel
 
-__global__ __launch_bounds__(256) void se_mlp_kernel(const float* partial, int tiles, float inv_count,
-                                                    const float* w1, const float* b1, const float* w2,
-                                                    const float* b2, float* att, int c, int hid, int staged) {
+__global__ __launch_bounds__(SE_ST) void se_mlp_staged_kernel(const float* partial, int tiles, float inv_count,
+                                                             const float* w1, const float* b1, const float* w2,
+                                                             const float* b2, float* att, int c, int hid) {
   extern __shared__ float lds[];
-  float* g = lds;            // [C]
-  float* hbuf = g + c;       // [hid]
-  float* sp = hbuf + hid;    // staged: [tiles][C]
-  float* sw1 = sp + tiles * c;   // staged: [hid][C]
-  float* sw2 = sw1 + hid * c;    // staged: [hid][C] (transposed)
+  const int nsl = c < SE_ST ? SE_ST / c : 1;
+  float* g = lds;                  // [C]
+  float* hbuf = g + c;             // [hid]
+  float* red = hbuf + hid;         // [nsl][C]
+  float* sp = red + nsl * c;       // [tiles][C]
+  float* sw1 = sp + tiles * c;     // [hid][C] (right behind sp: one contiguous copy)
+  float* sw2 = sw1 + hid * c;      // [C][hid + 1]
   const int n = blockIdx.x, tid = threadIdx.x;
   const float* pn = partial + (int64_t)n * tiles * c;
-  if (staged) {
-    const int np = tiles * c, nw = hid * c, ntot = np + 2 * nw;
-    for (int b0 = 0; b0 < ntot; b0 += SE_MAXLD * 256) {
-      float v[SE_MAXLD];
+  const int np = tiles * c, nw = hid * c, ntot = np + 2 * nw;
+  const float inv_hid = 1.f / (float)hid;
+  for (int b0 = 0; b0 < ntot; b0 += SE_MAXLD * SE_ST) {
+    float v[SE_MAXLD];
 #pragma unroll
-      for (int u = 0; u < SE_MAXLD; ++u) {
-        const int e = b0 + tid + u * 256;
-        const float* src = e < np ? pn + e : e < np + nw ? w1 + (e - np) : w2 + (e - np - nw);
-        v[u] = e < ntot ? *src : 0.f;   // one load per element
-      }
+    for (int u = 0; u < SE_MAXLD; ++u) {
+      int e = b0 + tid + u * SE_ST;
+      e = e < ntot ? e : ntot - 1;
+      const float* src = e < np ? pn + e : e < np + nw ? w1 + (e - np) : w2 + (e - np - nw);
+      v[u] = *src;
+    }
 #pragma unroll
-      for (int u = 0; u < SE_MAXLD; ++u) {
-        const int e = b0 + tid + u * 256;
-        if (e < np + nw) {
-          sp[e] = v[u];   // sp and sw1 are contiguous
-        } else if (e < ntot) {  // w2 [C][hid] -> sw2 [hid][C]: lanes along channels read distinct banks
-          const int f = e - np - nw, ch = f / hid, j = f - ch * hid;
-          sw2[j * c + ch] = v[u];
-        }
+    for (int u = 0; u < SE_MAXLD; ++u) {
+      const int e = b0 + tid + u * SE_ST;
+      if (e < np + nw) {
+        sp[e] = v[u];
+      } else if (e < ntot) {  // w2 [C][hid] -> [C][hid + 1]
+        const int f = e - np - nw, ch = (int)(((float)f + 0.5f) * inv_hid), j = f - ch * hid;
+        sw2[ch * (hid + 1) + j] = v[u];
       }
     }
-    __syncthreads();
-    for (int ch = tid; ch < c; ch += 256) {
-      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-      int t = 0;
-      for (; t + 4 <= tiles; t += 4) {
-        s0 += sp[t * c + ch];
-        s1 += sp[(t + 1) * c + ch];
-        s2 += sp[(t + 2) * c + ch];
-        s3 += sp[(t + 3) * c + ch];
-      }
-      for (; t < tiles; ++t) s0 += sp[t * c + ch];
-      g[ch] = ((s0 + s1) + (s2 + s3)) * inv_count;
-    }
-    __syncthreads();
-    // hidden unit j: 8 threads, strided channel slices, shuffle-reduced
-    for (int j0 = 0; j0 < hid; j0 += 32) {
-      const int j = j0 + (tid >> 3), part = tid & 7;
-      float acc = 0.f;
-      if (j < hid)
-        for (int ch = part; ch < c; ch += 8) acc += sw1[j * c + ch] * g[ch];
-      acc += __shfl_xor(acc, 1);
-      acc += __shfl_xor(acc, 2);
-      acc += __shfl_xor(acc, 4);
-      if (j < hid && part == 0) hbuf[j] = fmaxf(acc + (b1 ? b1[j] : 0.f), 0.f);
-    }
-    __syncthreads();
-    for (int ch = tid; ch < c; ch += 256) {
-      float acc = b2 ? b2[ch] : 0.f;
-      for (int j = 0; j < hid; ++j) acc += sw2[j * c + ch] * hbuf[j];
-      att[(int64_t)n * c + ch] = sigmoidf_(acc);
-    }
-    return;
-  }
-  for (int ch = tid; ch < c; ch += 256) {
-    float acc = 0.f;
-#pragma unroll 8
-    for (int t = 0; t < tiles; ++t) acc += pn[(int64_t)t * c + ch];
-    g[ch] = acc * inv_count;
   }
   __syncthreads();
-  for (int j = tid; j < hid; j += 256) {
-    float acc = b1 ? b1[j] : 0.f;
-    const float* wr = w1 + (int64_t)j * c;
-#pragma unroll 8
-    for (int ch = 0; ch < c; ++ch) acc += wr[ch] * g[ch];
-    hbuf[j] = fmaxf(acc, 0.f);
+  for (int e = tid; e < nsl * c; e += SE_ST) {
+    const int ch = e % c, s = e / c;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int t = s;
+    for (; t + 3 * nsl < tiles; t += 4 * nsl) {
+      s0 += sp[t * c + ch];
+      s1 += sp[(t + nsl) * c + ch];
+      s2 += sp[(t + 2 * nsl) * c + ch];
+      s3 += sp[(t + 3 * nsl) * c + ch];
+    }
+    for (; t < tiles; t += nsl) s0 += sp[t * c + ch];
+    red[s * c + ch] = (s0 + s1) + (s2 + s3);
   }
   __syncthreads();
-  for (int ch = tid; ch < c; ch += 256) {
-    float acc = b2 ? b2[ch] : 0.f;
+  for (int ch = tid; ch < c; ch += SE_ST) {
+    float v = 0.f;
+    for (int s = 0; s < nsl; ++s) v += red[s * c + ch];
+    g[ch] = v * inv_count;
+  }
+  __syncthreads();
+  // hidden unit j: 8 threads, strided channel slices, shuffle-reduced
+  for (int j0 = 0; j0 < hid; j0 += SE_ST / 8) {
+    const int j = j0 + (tid >> 3), part = tid & 7;
+    float a0 = 0.f, a1 = 0.f;
+    if (j < hid) {
+      int ch = part;
+      for (; ch + 8 < c; ch += 16) {
+        a0 += sw1[j * c + ch] * g[ch];
+        a1 += sw1[j * c + ch + 8] * g[ch + 8];
+      }
+      for (; ch < c; ch += 8) a0 += sw1[j * c + ch] * g[ch];
+    }
+    float acc = a0 + a1;
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    acc += __shfl_xor(acc, 4);
+    if (j < hid && part == 0) hbuf[j] = fmaxf(acc + (b1 ? b1[j] : 0.f), 0.f);
+  }
+  __syncthreads();
+  for (int ch = tid; ch < c; ch += SE_ST) {
+    const float* wr = sw2 + ch * (hid + 1);
+    float a[4] = {b2 ? b2[ch] : 0.f, 0.f, 0.f, 0.f};
+    int j = 0;
+    for (; j + 4 <= hid; j += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] += wr[j + u] * hbuf[j + u];
+    }
+    for (; j < hid; ++j) a[0] += wr[j] * hbuf[j];
+    att[(int64_t)n * c + ch] = sigmoidf_((a[0] + a[1]) + (a[2] + a[3]));
+  }
+}
+
+// Large C (the staged copy would not fit): NT threads (256 for C <= 256, 1024
+// above: a small block starts sooner next to concurrent kernels, a large one
+// keeps more weight loads in flight); three phases, each issuing its loads back to back so that a phase costs a few
+// memory round trips, not one per element:
+//  1. g[c] = inv_count * (sum over tiles): nsl = NT / C tile slices per
+//     channel when C < NT, 8 independent chains each, slices combined in a
+//     fixed order (deterministic);
+//  2. h[j] = relu(b1[j] + W1[j] . g): each wave takes 8 hidden units at a
+//     time, lanes along channels (coalesced W1 rows, 4 channel steps unrolled:
+//     32 loads in flight per lane), shuffle-reduced;
+//  3. att[c] = sigmoid(b2[c] + W2[c] . h): one thread per channel, its W2 row
+//     in 16-byte pieces (rows 16-byte aligned) issued before the products.
+constexpr int SE_UJ = 8;  // hidden units per wave per round
+
+template <int NT>
+__global__ __launch_bounds__(NT) void se_mlp_kernel(const float* partial, int tiles, float inv_count,
+                                                   const float* w1, const float* b1, const float* w2,
+                                                   const float* b2, float* att, int c, int hid) {
+  extern __shared__ float lds[];
+  float* g = lds;           // [C]
+  float* hbuf = g + c;      // [hid]
+  float* red = hbuf + hid;  // [nsl][C] slice sums
+  const int n = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NWV = NT / 64;
+  const float* pn = partial + (int64_t)n * tiles * c;
+  const int nsl = c < NT ? NT / c : 1;
+  // ---- 1. channel means ----
+  for (int base = 0; base < c * nsl; base += NT) {
+    const int e = base + tid;
+    if (e < c * nsl) {
+      const int ch = e % c, s = e / c;
+      float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      int t = s;
+      for (; t + 7 * nsl < tiles; t += 8 * nsl) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] += pn[(int64_t)(t + u * nsl) * c + ch];
+      }
+      for (int u = 0; t < tiles; t += nsl, ++u) a[u & 7] += pn[(int64_t)t * c + ch];
+      red[s * c + ch] = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+    }
+  }
+  __syncthreads();
+  for (int ch = tid; ch < c; ch += NT) {
+    float v = 0.f;
+    for (int s = 0; s < nsl; ++s) v += red[s * c + ch];
+    g[ch] = v * inv_count;
+  }
+  __syncthreads();
+  // ---- 2. hidden layer ----
+  for (int j0 = wave * SE_UJ; j0 < hid; j0 += NWV * SE_UJ) {
+    float acc[SE_UJ];
+#pragma unroll
+    for (int u = 0; u < SE_UJ; ++u) acc[u] = 0.f;
+    int ch = lane;
+    for (; ch + 192 < c; ch += 256) {  // 4 channel steps: 32 loads in flight
+      float wv[4][SE_UJ];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int u = 0; u < SE_UJ; ++u) wv[q][u] = j0 + u < hid ? w1[(int64_t)(j0 + u) * c + ch + 64 * q] : 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float gv = g[ch + 64 * q];
+#pragma unroll
+        for (int u = 0; u < SE_UJ; ++u) acc[u] += wv[q][u] * gv;
+      }
+    }
+    for (; ch < c; ch += 64) {
+      const float gv = g[ch];
+#pragma unroll
+      for (int u = 0; u < SE_UJ; ++u)
+        if (j0 + u < hid) acc[u] += w1[(int64_t)(j0 + u) * c + ch] * gv;
+    }
+#pragma unroll
+    for (int u = 0; u < SE_UJ; ++u) {
+      float v = acc[u];
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      if (lane == 0 && j0 + u < hid) hbuf[j0 + u] = fmaxf(v + (b1 ? b1[j0 + u] : 0.f), 0.f);
+    }
+  }
+  __syncthreads();
+  // ---- 3. output layer ----
+  const bool vec = (hid & 3) == 0 && ((uintptr_t)w2 & 15) == 0;
+  for (int ch = tid; ch < c; ch += NT) {
     const float* wr = w2 + (int64_t)ch * hid;
-#pragma unroll 8
-    for (int j = 0; j < hid; ++j) acc += wr[j] * hbuf[j];
-    att[(int64_t)n * c + ch] = sigmoidf_(acc);
+    float a[4] = {b2 ? b2[ch] : 0.f, 0.f, 0.f, 0.f};
+    int j = 0;
+    if (vec) {
+      for (; j + 16 <= hid; j += 16) {  // four 16-byte pieces in flight
+        floatx4 wq[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) wq[q] = *(const floatx4*)(wr + j + 4 * q);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) a[u] += wq[q][u] * hbuf[j + 4 * q + u];
+      }
+    }
+    for (; j < hid; ++j) a[j & 3] += wr[j] * hbuf[j];
+    att[(int64_t)n * c + ch] = sigmoidf_((a[0] + a[1]) + (a[2] + a[3]));
   }
 }
 
 // ---- channel scale: out[n, c, :] = x[n, c, :] * att[n, c] (NCHW) or per pixel (NHWC) -------
+// NCHW over the flat tensor in 16-byte pieces (hw >= 8): the plane of a piece's
+// first element gives its scale; a piece straddles at most one plane boundary.
+template <typename T>
+__global__ __launch_bounds__(256) void channel_scale_flat_kernel(const T* x, const float* att, T* out, int nvec,
+                                                                int hw) {
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += gridDim.x * 256) {
+    const int e0 = v * 8;
+    const int p0 = e0 / hw, nb = (p0 + 1) * hw - e0;  // elements of the piece in plane p0 (att index = plane)
+    const float s0 = att[p0], s1 = nb < 8 ? att[p0 + 1] : s0;
+    const t8 xv = *(const t8*)(x + e0);
+    t8 o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = from_f32<T>(to_f32(xv[k]) * (k < nb ? s0 : s1));
+    *(t8*)(out + e0) = o;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void channel_scale_kernel(const T* x, const float* att, T* out, int64_t total,
                                                            int c, int hw, int layout, int cs) {
@@ -485,6 +648,17 @@ extern "C" int kad_se_pool(const void* x, float* partial, int n, int c, int h, i
   if (layout == KAD_NCHW) {
     const int planes = n * c;
     dim3 grid(ceil_div(planes, 4));
+    const int64_t total = (int64_t)planes * P;
+    if (P >= 8 && total % 8 == 0 && total < (1ll << 31) && (uintptr_t)x % (8 * dtype_size(dtype)) == 0) {
+      dim3 gridf(ceil_div(planes, 16));  // 4 waves x 4 planes per block
+      switch (dtype) {
+        case KAD_F32: hipLaunchKernelGGL(se_pool_flat_kernel<float>, gridf, dim3(256), 0, st, (const float*)x, partial, planes, P); break;
+        case KAD_F16: hipLaunchKernelGGL(se_pool_flat_kernel<half_t>, gridf, dim3(256), 0, st, (const half_t*)x, partial, planes, P); break;
+        case KAD_BF16: hipLaunchKernelGGL(se_pool_flat_kernel<bf16_t>, gridf, dim3(256), 0, st, (const bf16_t*)x, partial, planes, P); break;
+        default: return fail(KAD_EINVAL, "kad_se_pool: unknown dtype %d", dtype);
+      }
+      return check_launch("kad_se_pool");
+    }
     switch (dtype) {
       case KAD_F32: hipLaunchKernelGGL(se_pool_nchw_kernel<float>, grid, dim3(256), 0, st, (const float*)x, partial, planes, P); break;
       case KAD_F16: hipLaunchKernelGGL(se_pool_nchw_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, partial, planes, P); break;
@@ -515,12 +689,25 @@ extern "C" int kad_se_mlp(const float* partial, int tiles, float inv_count, cons
                           const float* w2, const float* b2, float* att, int n, int c, int hid, void* stream) {
   KAD_CHECK_ARG(partial && w1 && w2 && att, "kad_se_mlp: null pointer");
   KAD_CHECK_ARG(n > 0 && c > 0 && hid > 0 && tiles > 0, "kad_se_mlp: bad shape");
-  const size_t lds_small = (size_t)(c + hid) * sizeof(float);
-  KAD_CHECK_ARG(lds_small <= 64 * 1024, "kad_se_mlp: C + hidden too large");
-  const size_t lds_staged = lds_small + ((size_t)tiles * c + 2 * (size_t)hid * c) * sizeof(float);
-  const int staged = lds_staged <= 64 * 1024 ? 1 : 0;
-  hipLaunchKernelGGL(se_mlp_kernel, dim3(n), dim3(256), staged ? lds_staged : lds_small, (hipStream_t)stream,
-                     partial, tiles, inv_count, w1, b1, w2, b2, att, c, hid, staged);
+  const int nsl_s = c < SE_ST ? SE_ST / c : 1;
+  const size_t lds_staged =
+      (size_t)(c + hid + (size_t)(nsl_s + tiles) * c + (size_t)hid * c + (size_t)c * (hid + 1)) * sizeof(float);
+  if (lds_staged <= 160 * 1024) {  // gfx950: 160 KB of LDS per CU (KADConv's C -> C -> C SE at 100 x 100: 89 KB)
+    allow_lds(se_mlp_staged_kernel, lds_staged);
+    hipLaunchKernelGGL(se_mlp_staged_kernel, dim3(n), dim3(SE_ST), lds_staged, (hipStream_t)stream, partial, tiles,
+                       inv_count, w1, b1, w2, b2, att, c, hid);
+    return check_launch("kad_se_mlp");
+  }
+  const int nt = c <= 256 ? 256 : 1024;
+  const int nsl = c < nt ? nt / c : 1;
+  const size_t lds = (size_t)(c + hid + (size_t)nsl * c) * sizeof(float);
+  KAD_CHECK_ARG(lds <= 64 * 1024, "kad_se_mlp: C + hidden too large");
+  if (nt == 256)
+    hipLaunchKernelGGL(se_mlp_kernel<256>, dim3(n), dim3(256), lds, (hipStream_t)stream, partial, tiles, inv_count, w1,
+                       b1, w2, b2, att, c, hid);
+  else
+    hipLaunchKernelGGL(se_mlp_kernel<1024>, dim3(n), dim3(1024), lds, (hipStream_t)stream, partial, tiles, inv_count,
+                       w1, b1, w2, b2, att, c, hid);
   return check_launch("kad_se_mlp");
 }
 
@@ -532,6 +719,19 @@ extern "C" int kad_channel_scale(const void* x, const float* att, void* out, int
   KAD_CHECK_ARG(cs >= c, "kad_channel_scale: channel stride < C");
   const int64_t total = (int64_t)n * h * w * cs;
   hipStream_t st = (hipStream_t)stream;
+  const int vb = 8 * dtype_size(dtype);
+  if (layout == KAD_NCHW && h * w >= 8 && total % 8 == 0 && total < (1ll << 31) && (uintptr_t)x % vb == 0 &&
+      (uintptr_t)out % vb == 0) {
+    const int nvec = (int)(total / 8);
+    const dim3 grid(grid_for(nvec));
+    switch (dtype) {
+      case KAD_F32: hipLaunchKernelGGL(channel_scale_flat_kernel<float>, grid, dim3(256), 0, st, (const float*)x, att, (float*)out, nvec, h * w); break;
+      case KAD_F16: hipLaunchKernelGGL(channel_scale_flat_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, att, (half_t*)out, nvec, h * w); break;
+      case KAD_BF16: hipLaunchKernelGGL(channel_scale_flat_kernel<bf16_t>, grid, dim3(256), 0, st, (const bf16_t*)x, att, (bf16_t*)out, nvec, h * w); break;
+      default: return fail(KAD_EINVAL, "kad_channel_scale: unknown dtype %d", dtype);
+    }
+    return check_launch("kad_channel_scale");
+  }
   switch (dtype) {
     case KAD_F32: hipLaunchKernelGGL(channel_scale_kernel<float>, dim3(grid_for(total)), dim3(256), 0, st, (const float*)x, att, (float*)out, total, c, h * w, layout, cs); break;
     case KAD_F16: hipLaunchKernelGGL(channel_scale_kernel<half_t>, dim3(grid_for(total)), dim3(256), 0, st, (const half_t*)x, att, (half_t*)out, total, c, h * w, layout, cs); break;

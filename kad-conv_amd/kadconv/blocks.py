@@ -64,12 +64,17 @@ class SqueezeExcitation(nn.Module):
         super().__init__()
         hid = max(min_hidden, c // reduction)
         self.fc = nn.Sequential(nn.Linear(c, hid), nn.ReLU(), nn.Linear(hid, c), nn.Sigmoid())
+        self._f32 = {}
 
     def forward(self, x):
         if _use_hip(self, x):
+            # fp32 copies of the MLP parameters, cached per parameter version
+            ps = (self.fc[0].weight, self.fc[0].bias, self.fc[2].weight, self.fc[2].bias)
+            key = tuple((p._version, p.data_ptr()) for p in ps)
+            if key not in self._f32:
+                self._f32 = {key: tuple(p.detach().float().contiguous() for p in ps)}
             with torch.no_grad():
-                return ops.squeeze_excitation(x, self.fc[0].weight, self.fc[0].bias, self.fc[2].weight,
-                                              self.fc[2].bias)
+                return ops.squeeze_excitation(x, *self._f32[key])
         return x * self.fc(x.mean(dim=(2, 3))).view(x.shape[0], -1, 1, 1)
 
 

@@ -105,7 +105,9 @@ def squeeze_excitation(x, w1, b1, w2, b2):
         raise ValueError('kadconv.ops.squeeze_excitation needs a GPU tensor')
     N, C, H, W = x.shape
     hid = w1.shape[0]
-    f32 = lambda t: t.detach().to(torch.float32).contiguous()  # noqa: E731
+    def f32(t):  # fp32 contiguous tensors are used as they are (no per-call copy)
+        return t if (t.dtype == torch.float32 and t.is_contiguous()) else t.detach().float().contiguous()
+
     nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
     layout = _ext.KAD_NHWC if nhwc else _ext.KAD_NCHW
     xv = x.permute(0, 2, 3, 1) if nhwc else x.contiguous()

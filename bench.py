@@ -1,6 +1,6 @@
 """Benchmark of the KAD-Conv inference hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--no-cpu] [--per-op-only]
 
 Step = one fused KADConv(256) forward on x [8, 256, 100, 100] fp16 (BASELINE
 config 2's metric shape), inputs resident in HBM, weights random from a seed
@@ -250,6 +250,8 @@ def main():
     ap.add_argument('--warmup', type=int, default=20)
     ap.add_argument('--no-ops', action='store_true', help='skip the per-op table of the other configs')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline')
+    ap.add_argument('--per-op-only', action='store_true',
+                    help='print only the per-op table (a short program for rocprofv3 kernel traces)')
     ap.add_argument('--traffic-probe', action='store_true', help='short program for the rocprofv3 --pmc passes')
     ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
                     help='compute profiles/dsc0_traffic.json from the two --pmc counter CSVs')
@@ -259,6 +261,10 @@ def main():
         return
     if args.traffic_probe:
         traffic_probe()
+        return
+    if args.per_op_only:
+        with torch.no_grad():
+            print(json.dumps(per_op(args.steps, args.warmup)))
         return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU: every GPU box of this build has one MI355X and the KAD-Conv forward '

@@ -53,6 +53,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
+// Buffer -> LDS loads of 16 / 4 bytes per lane: lane i's bytes land at
+// dst + size * i (dst wave-uniform); the global address is base + soffset
+// (wave-uniform) + voff (per lane).  They count in vmcnt like other loads.
+// __syncthreads() fences wait for all of them (vmcnt(0)); a software pipeline
+// waits for its own stage with an explicit s_waitcnt and a bare s_barrier, and
+// keeps each stage in a __shared__ object of its own so that the compiler's
+// wait counts for LDS reads stay per stage.
+#define KAD_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KAD_LDS(dst), 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KAD_LDS(dst), 4, voff, soff, 0, 0);
+}
+
 // Bilinear resize source index (PyTorch, align_corners=False, output size
 // given): s = max(scale * (dst + 0.5) - 0.5, 0) with scale = in / out; rows
 // i0 = floor(s) and i1 = min(i0 + 1, in - 1), weight of i1 = s - i0.

@@ -204,16 +204,6 @@ constexpr int GN_XB = 32 * GN_PX * 2;   // input tile bytes per stage
 template <typename T> struct Raw16 { typedef half8_t type; };
 template <> struct Raw16<bf16_t> { typedef bf16x8_t type; };
 
-#define KAD_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-// Buffer -> LDS loads of 16 / 4 bytes per lane: lane i's bytes land at dst + size * i.
-// The address is base + soffset (wave-uniform) + voff (per lane).
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KAD_LDS(dst), 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, char* dst, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KAD_LDS(dst), 4, voff, soff, 0, 0);
-}
 
 template <typename T, bool V16, int NW>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_args a, int P, int tiles_px,

@@ -199,18 +199,36 @@ __device__ __forceinline__ PyFrag<T> pooled_frag(const T* xs, int q0, int g8) {
 // The widest column tiles get the whole register file (1 block per CU) instead of spilling.
 template <typename T, int HB> struct PyOcc { static constexpr int v = HB <= (sizeof(T) == 4 ? 2 : 3) ? 2 : 1; };
 
+// Weight chunks per K step of the pipelined 16-bit path: 3 branches x 2 HB
+// fragments of 16 columns x 32 channels (1 KB each, MFMA lane order).
+template <int HB> struct PyW { static constexpr int NCH = 6 * HB, BYTES = NCH * 1024; };
+
+// dma = 1 (host-checked: 16-bit NCHW input, W % 4 == 0, offsets fit 31 bits):
+// the K loop pipelines through LDS (weights by buffer -> LDS loads into a
+// 3-stage ring, the x slice two steps ahead in registers); else the
+// register-staged loop with one step of prefetch.
 template <typename T, int HB>
-__global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(kad_pyramid_args a, int cin_pad) {
+__global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(kad_pyramid_args a, int cin_pad,
+                                                                                 int dma) {
   constexpr int LDA = PyLds<T>::lda;
   constexpr int NB = 32 * HB;              // output columns per branch per block
   constexpr int BTASKS = 3 * NB * 4;       // 16-byte weight pieces per K step (3 branches)
   constexpr int BPT = (BTASKS + PY_THREADS - 1) / PY_THREADS;
   constexpr int OBT = NB + 16 / (int)sizeof(T);   // epilogue staging row of y (T)
+  constexpr bool H16 = sizeof(T) == 2;
+  // 16-bit: the weight ring, one __shared__ object per stage (exact wait counts per stage)
+  __shared__ __align__(16) char pw0[H16 ? PyW<HB>::BYTES : 16];
+  __shared__ __align__(16) char pw1[H16 ? PyW<HB>::BYTES : 16];
+  __shared__ __align__(16) char pw2[H16 ? PyW<HB>::BYTES : 16];
+  // 16-bit pipelined path: the two x stages, a static object too (no wait on the weight loads to read it)
+  __shared__ __align__(16) T xsd[H16 ? 2 * PY_TILE * LDA : 8];
   extern __shared__ __align__(16) char smem[];
-  T* xs = (T*)smem;                   // [128][LDA]
-  T* bs = xs + PY_TILE * LDA;         // [3][NB][LDA]
-  T* obt = (T*)smem;                  // epilogue: [128][OBT] y values of one branch
-  float* colred = (float*)(smem + PY_TILE * OBT * sizeof(T));  // epilogue: [32][NB] column partials
+  T* xs = (T*)smem;                   // register-staged path: [128][LDA]
+  T* bs = xs + PY_TILE * LDA;         // register-staged path: [3][NB][LDA]
+  // epilogue: [64][OBT] y values of one branch (branch 0: one pixel half)
+  T* obt = (H16 && dma) ? xsd : (T*)smem;
+  // epilogue: column partials, [32][NB] fp32 (branch 2: [2][HB][16][16])
+  float* colred = H16 ? (float*)pw2 : (float*)(smem + 64 * OBT * sizeof(T));
 
   const int tx = blockIdx.x, ty = blockIdx.y % a.nty, cy = blockIdx.y / a.nty, n = blockIdx.z;
   const int r0 = ty * PY_TR, c0 = tx * PY_TC;
@@ -315,21 +333,17 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     }
   };
 
-  load_step(0);
-  for (int k0 = 0; k0 < cin_pad; k0 += 32) {
-    __syncthreads();  // the previous step's MFMAs are done with xs / bs
-    store_step();
-    if (k0 + 32 < cin_pad) load_step(k0 + 32);  // in flight while this step computes
-    __syncthreads();
+  // one K step of MFMAs from the staged x slice (x_stage) and weights (bfrag(b, bf))
+  auto mma_step = [&](const T* x_stage, auto bfrag) {
     // ---- A fragments: the slice (branch 0) and its 2x2 / 4x4 averages (branches 1, 2) ----------
     // wave (wa, wb) = pixel half x column half
     PyFrag<T> a0[4], a1, a2;
 #pragma unroll
-    for (int mm = 0; mm < 4; ++mm) a0[mm] = frag_ld(xs + ((wa * 4 + mm) * 16 + row16) * LDA + grp * 8);
-    if (nb > 1) a1 = pooled_frag<T, 2, LDA>(xs, (2 * wa) * PY_TC + 2 * row16, grp * 8);  // pooled (wa, row16)
+    for (int mm = 0; mm < 4; ++mm) a0[mm] = frag_ld(x_stage + ((wa * 4 + mm) * 16 + row16) * LDA + grp * 8);
+    if (nb > 1) a1 = pooled_frag<T, 2, LDA>(x_stage, (2 * wa) * PY_TC + 2 * row16, grp * 8);  // pooled (wa, row16)
     if (nb > 2) {  // pooled pixel row16 of the 1 x 8 tile (rows >= 8 are padding); this wave's two rows
       if (row16 < 8) {
-        a2 = pooled_frag<T, 4, LDA>(xs, (2 * wa) * PY_TC + 4 * row16, grp * 8);
+        a2 = pooled_frag<T, 4, LDA>(x_stage, (2 * wa) * PY_TC + 4 * row16, grp * 8);
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) a2.v[j] = from_f32<T>(0.f);
@@ -339,14 +353,133 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     for (int bb = 0; bb < HB; ++bb) {
       const int bf = wb * HB + bb;
       if (bf < nbf[0]) {
-        const PyFrag<T> bq = frag_ld(bs + (0 * NB + bf * 16 + row16) * LDA + grp * 8);
+        const PyFrag<T> bq = bfrag(0, bf);
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm) acc0[mm][bb] = py_mma_f<T>(a0[mm], bq, acc0[mm][bb]);
       }
-      if (bf < nbf[1]) acc1[bb] = py_mma_f<T>(a1, frag_ld(bs + (1 * NB + bf * 16 + row16) * LDA + grp * 8), acc1[bb]);
-      if (bf < nbf[2])
-        acc2[bb] = py_mma_f<T>(a2, frag_ld(bs + (2 * NB + bf * 16 + row16) * LDA + grp * 8), acc2[bb]);
+      if (bf < nbf[1]) acc1[bb] = py_mma_f<T>(a1, bfrag(1, bf), acc1[bb]);
+      if (bf < nbf[2]) acc2[bb] = py_mma_f<T>(a2, bfrag(2, bf), acc2[bb]);
     }
+  };
+  auto bfrag_lds = [&](int b, int bf) { return frag_ld(bs + (b * NB + bf * 16 + row16) * LDA + grp * 8); };
+
+  if constexpr (H16) {
+    if (dma) {
+      // ---- pipelined K loop (16-bit NCHW, W % 4 == 0) ---------------------------------------------
+      // Weights: chunk (b, f) of step ks is 1 KB (fragment f) of the fragment-ordered copy behind the
+      // row layout of branch b's packed buffer; wave w loads fragments w, w + 4, ... of every branch
+      // straight into LDS slot b FB + f of the step's stage.  x: this thread's two 8-pixel pieces as four
+      // 8-byte buffer loads (pieces past the image or channels past Cin read 0), two steps ahead.
+      // Step ks opens with "own loads of step ks landed" + barrier; loads for steps past the last
+      // read zeros, so every step issues the same loads and the wait count holds.
+      constexpr int FB = 2 * HB, UPB = (FB + 3) / 4, TWMIN = 3 * (FB / 4);  // loads per branch / per wave (min)
+      const int nk = cin_pad / 32;
+      const int wv = __builtin_amdgcn_readfirstlane(wave);
+      __amdgpu_buffer_rsrc_t rwb[3];
+#pragma unroll
+      for (int b = 0; b < 3; ++b) {
+        const int bb = b < nb ? b : 0;
+        const int cpk = round_up(round_up(a.cout[bb], 8), 128);
+        rwb[b] = make_rsrc((const T*)sel3(a.wpack, bb) + (int64_t)cpk * cin_pad, (uint32_t)((int64_t)cpk * cin_pad * 2));
+      }
+      uint32_t woff[3][UPB];
+#pragma unroll
+      for (int b = 0; b < 3; ++b)
+#pragma unroll
+        for (int u = 0; u < UPB; ++u) {
+          const int f = wv + 4 * u;
+          const bool ok = b < nb && f < nbf_sel(nbf, b);
+          woff[b][u] = ok ? (uint32_t)(((((col0 >> 4) + f) * nk) * 64 + lane) * 16) : KAD_OOB;
+        }
+      const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)a.n * a.cin * a.h * a.w * 2));
+      uint32_t xo[2];
+      int xv[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int e = tid + t * PY_THREADS;
+        const int ch = e & 31, rs = e >> 5, row = rs >> 2, seg = rs & 3;
+        const int gy = r0 + row, gx = c0 + seg * 8;
+        xo[t] = (uint32_t)(((((int64_t)n * a.cin + ch) * a.h + (gy < a.h ? gy : 0)) * a.w + gx) * 2);
+        xv[t] = xvalid[t];  // 0, 4 or 8 (W % 4 == 0)
+      }
+      const uint32_t xstep_b = (uint32_t)(32 * a.h * a.w * 2);
+      auto issue = [&](int ks, char* pw, uint4 (&xr2)[2]) {
+#pragma unroll
+        for (int b = 0; b < 3; ++b)
+#pragma unroll
+          for (int u = 0; u < UPB; ++u) {
+            const int f = wv + 4 * u;
+            if (f < FB) {  // wave-uniform: with FB % 4 != 0 the low waves take one fragment more
+              const uint32_t o = (woff[b][u] == KAD_OOB || ks >= nk) ? KAD_OOB : woff[b][u] + (uint32_t)ks * 1024u;
+              dma16(rwb[b], pw + (b * FB + f) * 1024, o, 0u);
+            }
+          }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const bool chok = ks < nk && ks * 32 + xch[t] < a.cin;
+          const uint32_t o = xo[t] + (uint32_t)ks * xstep_b;
+          typedef int intx2 __attribute__((ext_vector_type(2)));
+          const intx2 lo = __builtin_bit_cast(intx2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                         rx, (chok && xv[t] >= 4) ? o : KAD_OOB, 0, 0));
+          const intx2 hi = __builtin_bit_cast(intx2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                         rx, (chok && xv[t] == 8) ? o + 8 : KAD_OOB, 0, 0));
+          xr2[t] = uint4{(unsigned)lo[0], (unsigned)lo[1], (unsigned)hi[0], (unsigned)hi[1]};
+        }
+      };
+      auto store_x = [&](T* stage, const uint4 (&xr2)[2]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int e = tid + t * PY_THREADS;
+          const int ch = e & 31, rs = e >> 5, row = rs >> 2, seg = rs & 3;
+          Raw8 r;
+          r.lo = xr2[t];
+          r.hi = uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) stage[(row * PY_TC + seg * 8 + j) * LDA + ch] = raw_get<T>(r, j);
+        }
+      };
+      T* xs0 = xsd;
+      T* xs1 = xsd + PY_TILE * LDA;
+      uint4 xa[2], xb[2];
+      issue(0, pw0, xa);
+      issue(1, pw1, xb);
+      store_x(xs0, xa);
+      // step ks: stage ks % 3 for the weights, ks % 2 for x; x of step ks + 1 sits in registers
+      auto step = [&](int ks, const char* pwc, char* pwr, const T* xcur, T* xnext, uint4 (&xnow)[2],
+                      uint4 (&xload)[2]) {
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(TWMIN + 4) : "memory");
+        issue(ks + 2, pwr, xload);
+        mma_step(xcur, [&](int b, int bf) { return *(const PyFrag<T>*)(pwc + ((b * FB + bf) * 64 + lane) * 16); });
+        store_x(xnext, xnow);  // x of step ks + 1 into the stage read in step ks - 1
+      };
+      // rotation period 6 = lcm(3 weight stages, 2 x stages); x registers alternate xb (step ks + 1) / xa
+      const int nk6 = nk / 6 * 6;
+      for (int ks = 0; ks < nk6; ks += 6) {
+        step(ks, pw0, pw2, xs0, xs1, xb, xa);
+        step(ks + 1, pw1, pw0, xs1, xs0, xa, xb);
+        step(ks + 2, pw2, pw1, xs0, xs1, xb, xa);
+        step(ks + 3, pw0, pw2, xs1, xs0, xa, xb);
+        step(ks + 4, pw1, pw0, xs0, xs1, xb, xa);
+        step(ks + 5, pw2, pw1, xs1, xs0, xa, xb);
+      }
+      const int r6 = nk - nk6;
+      if (r6 > 0) step(nk6, pw0, pw2, xs0, xs1, xb, xa);
+      if (r6 > 1) step(nk6 + 1, pw1, pw0, xs1, xs0, xa, xb);
+      if (r6 > 2) step(nk6 + 2, pw2, pw1, xs0, xs1, xb, xa);
+      if (r6 > 3) step(nk6 + 3, pw0, pw2, xs1, xs0, xa, xb);
+      if (r6 > 4) step(nk6 + 4, pw1, pw0, xs0, xs1, xb, xa);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the loop
+    }
+  }
+  if (!H16 || !dma) {
+  load_step(0);
+  for (int k0 = 0; k0 < cin_pad; k0 += 32) {
+    __syncthreads();  // the previous step's MFMAs are done with xs / bs
+    store_step();
+    if (k0 + 32 < cin_pad) load_step(k0 + 32);  // in flight while this step computes
+    __syncthreads();
+    mma_step(xs, bfrag_lds);
+  }
   }
 
   // ---- epilogue, one branch at a time -------------------------------------------------------------
@@ -393,12 +526,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
       const int col = bf * 16 + row16, co = col0 + col;
       const bool real = co < cout;
       const float bv = (bias && real) ? bias[co] : 0.f;
-      if (b == 0) {
-#pragma unroll
-        for (int mm = 0; mm < 4; ++mm)
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            obt[((wa * 4 + mm) * 16 + grp * 4 + i) * OBT + col] = from_f32<T>(acc0[mm][bb][i] + bv);
+      if (b == 0) {  // y staged below, one pixel half at a time
         if (sums) {
 #pragma unroll
           for (int q = 0; q < 2; ++q) {  // tile rows 2 wa + q
@@ -487,36 +615,67 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
         }
       }
     }
-    // y_b: NHWC, 16-byte pieces of 8 channels straight from the staged rows (pad channels are 0)
+    // y_b: NHWC, 16-byte pieces of 8 channels straight from the staged rows (pad channels are 0);
+    // branch 0 in two passes of 64 pixels (the staging buffer holds 64 rows)
     T* y = (T*)a.out[b];
     const int g8 = ncols[b] >> 3;
     constexpr int G8 = NB / 8;
-    for (int e = tid; e < tr * tc * G8; e += PY_THREADS) {
-      const int px = e / G8, g = e - px * G8;
-      const int py_ = px / tc;  // tc is a power of two
-      const int gy = ty * tr + py_, gx = tx * tc + (px - py_ * tc);
-      if (g >= g8 || gy >= hbch || gx >= wbch) continue;
-      T* d = y + (((int64_t)n * hbch + gy) * wbch + gx) * a.out_cs[b] + col0 + g * 8;
-      const T* sp = obt + px * OBT + g * 8;
-      *(uint4*)d = *(const uint4*)sp;
-      if constexpr (sizeof(T) == 4) *(uint4*)(d + 4) = *(const uint4*)(sp + 4);
+    const int npass = b == 0 ? 2 : 1;
+    for (int h = 0; h < npass; ++h) {
+      if (b == 0) {
+        __syncthreads();  // the staging rows are free
+        if (wa == h) {
+#pragma unroll
+          for (int bb = 0; bb < HB; ++bb) {
+            const int bf = wb * HB + bb;
+            if (bf >= nbf[0]) continue;
+            const int col = bf * 16 + row16, co = col0 + col;
+            const float bv = (bias && co < cout) ? bias[co] : 0.f;
+#pragma unroll
+            for (int mm = 0; mm < 4; ++mm)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) obt[(mm * 16 + grp * 4 + i) * OBT + col] = from_f32<T>(acc0[mm][bb][i] + bv);
+          }
+        }
+        __syncthreads();
+      }
+      const int npx = b == 0 ? 64 : tr * tc;
+      for (int e = tid; e < npx * G8; e += PY_THREADS) {
+        const int pl = e / G8, g = e - pl * G8;
+        const int px = 64 * h + pl;
+        const int py_ = px / tc;  // tc is a power of two
+        const int gy = ty * tr + py_, gx = tx * tc + (px - py_ * tc);
+        if (g >= g8 || gy >= hbch || gx >= wbch) continue;
+        T* d = y + (((int64_t)n * hbch + gy) * wbch + gx) * a.out_cs[b] + col0 + g * 8;
+        const T* sp = obt + pl * OBT + g * 8;
+        *(uint4*)d = *(const uint4*)sp;
+        if constexpr (sizeof(T) == 4) *(uint4*)(d + 4) = *(const uint4*)(sp + 4);
+      }
     }
   }
 }
 
+// Dynamic LDS (register-staged path): the K loop's x and weight stages or the
+// epilogue's 64-row y staging (+ column partials on the fp32 path; the 16-bit
+// paths keep those in the static weight ring).
 template <typename T, int HB>
-static size_t pyramid_lds() {
-  const size_t stage = (size_t)(PY_TILE + 3 * 32 * HB) * PyLds<T>::lda * sizeof(T);
-  const size_t epi = (size_t)PY_TILE * (32 * HB + 16 / sizeof(T)) * sizeof(T) + (size_t)32 * 32 * HB * sizeof(float);
+static size_t pyramid_lds(int dma) {
+  if (dma) return 0;  // pipelined path: static weight ring and x stages (the epilogue reuses them)
+  const size_t lda = PyLds<T>::lda;
+  const size_t stage = (size_t)(PY_TILE + 3 * 32 * HB) * lda * sizeof(T);
+  size_t epi = (size_t)64 * (32 * HB + 16 / sizeof(T)) * sizeof(T);
+  if (sizeof(T) == 4) epi += (size_t)32 * 32 * HB * sizeof(float);
   return stage > epi ? stage : epi;
 }
 
 template <typename T, int HB>
 static void launch_pyramid(const kad_pyramid_args& a, int cin_pad, int maxcols, hipStream_t st) {
   dim3 grid(a.ntx, a.nty * ceil_div(maxcols, 32 * HB), a.n);
-  const size_t lds = pyramid_lds<T, HB>();
+  const int dma = sizeof(T) == 2 && a.in_layout == KAD_NCHW && a.w % 4 == 0 &&
+                  (int64_t)a.n * a.cin * a.h * a.w * 2 < (1ll << 31) && (uint32_t)(32 * a.h * a.w * 2) > 0;
+  const size_t lds = pyramid_lds<T, HB>(dma);
   allow_lds(pyramid_kernel<T, HB>, lds);
-  hipLaunchKernelGGL((pyramid_kernel<T, HB>), grid, dim3(PY_THREADS), lds, st, a, cin_pad);
+  hipLaunchKernelGGL((pyramid_kernel<T, HB>), grid, dim3(PY_THREADS), lds, st, a, cin_pad, dma);
 }
 
 template <typename T>

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KAD_ABI_VERSION 1
+#define KAD_ABI_VERSION 2
 
 /* element types */
 #define KAD_F32 0
@@ -93,6 +93,21 @@ typedef struct kad_dcn_args {
                              (both >= Cout: a channel slice of a wider tensor can be written) */
   int dtype;              /* KAD_F32 / KAD_F16 / KAD_BF16 (x, wpack, out) */
   int relu;               /* nonzero: ReLU between post_add and post_scale */
+  /* Squeeze-excitation of the output, fused (needs gap_partial).  When se_att is
+   * not NULL, the last block of each image to finish sums that image's GAP
+   * partials in a fixed order and writes
+   *   se_att[n][c] = sigmoid(W2 relu(W1 g + b1) + b2)[c],  g = se_inv_count * sum of partials,
+   * i.e. kad_se_mlp over the partials, without a launch of its own.
+   * se_count: [N] counters, zero before the first call; every call that
+   * completes leaves them zero again.  Calls that overlap on one se_count race. */
+  const float *se_w1;     /* [se_hid][Cout] */
+  const float *se_b1;     /* [se_hid] or NULL */
+  const float *se_w2;     /* [Cout][se_hid] */
+  const float *se_b2;     /* [Cout] or NULL */
+  float *se_att;          /* [N][Cout], or NULL: no SE */
+  unsigned *se_count;     /* [N] */
+  int se_hid;
+  float se_inv_count;     /* 1 / (Ho * Wo) */
 } kad_dcn_args;
 
 /* out = post_scale * act((deform_conv3x3(x, offset, mask, W) + bias) * post_mul + post_add).

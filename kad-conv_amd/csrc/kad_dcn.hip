@@ -74,6 +74,7 @@ constexpr int DCN_LDS = 160 * 1024;                // gfx950 LDS per CU
 constexpr int DCN_SLOT = DCN_THREADS / 4;          // region pixels staged per round (4 threads per pixel)
 constexpr int DCN_FCAP = 704;                      // footprint pixels (enough for stride <= 2)
 static_assert(DCN_TILE == 128 && DCN_SLOT % 64 == 0, "tile / staging geometry");
+constexpr int DCN_SE_LDS = 48 * 1024;              // fused SE scratch (floats in the region buffer) limit
 
 enum { MODE_EXT = 0, MODE_FUSED = 1, MODE_PLAIN = 2 };
 
@@ -287,6 +288,7 @@ template <typename T, typename OutT, int NBF, int MODE> struct DcnLds {
   static_assert(RCAP >= DCN_FCAP, "footprint must fit the region buffer");
   static_assert(MODE == MODE_PLAIN || sizeof(T) == 4 || RCAP * PXB <= 65536, "16-bit corner offsets");
   static_assert(RCAP * PXB >= STAGE_BYTES + DCN_WAVES * NB * 4, "epilogue tile must fit the region buffer");
+  static_assert(MODE == MODE_PLAIN || RCAP * PXB >= DCN_SE_LDS, "fused SE scratch must fit the region buffer");
 };
 
 // ---- buffer loads ------------------------------------------------------------------------------
@@ -576,6 +578,100 @@ __device__ __forceinline__ void offset_conv16(floatx4 (&oacc)[DCN_WM][2], __amdg
     __syncthreads();  // footprint / filters consumed before the next group (or the caller) reuses them
     c0 += G;
   }
+}
+
+// ---- fused squeeze-excitation of one image ------------------------------------------------------
+// Cross-block exchange without fences.  A device-scope release fence writes
+// back the whole L2 of the XCD (8 XCDs, each with its own L2), which costs
+// microseconds per block; atomic read-modify-writes, by contrast, are
+// performed at the memory-side coherence point for every XCD.  So every step
+// of the exchange is a relaxed device-scope RMW whose returned value the
+// thread waits for (the RMW has then been performed):
+//  - each block stores its GAP partials with atomic exchanges and waits;
+//  - after a barrier, thread 0 increments the image's arrival counter;
+//  - the block that completes the count resets it (exchange with 0) and reads
+//    every partial of the image with device-scope atomic loads (coherent across
+//    XCDs: they do not return a stale line of the reader's L2).
+// se_tail then forms g = se_inv_count * column sums of the [tiles][Cout]
+// partials in a fixed order (thread (slice s, channel c) takes tiles s,
+// s + nsl, ...; the slices are then added in order), so the result does not
+// depend on which block came last; then att = sigmoid(W2 relu(W1 g + b1) + b2)
+// with 8 lanes per output and a shuffle reduction.  lds: Cout + hid + 512 floats.
+__device__ __forceinline__ float dev_load(const float* p) {
+  return __uint_as_float(__hip_atomic_load((const unsigned*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void rmw_store(float* p, float v) {
+  const unsigned old = __hip_atomic_exchange((unsigned*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(old));  // the returning form: the thread's wait covers it
+}
+
+__device__ __forceinline__ void se_tail(const float* __restrict__ partial, const float* __restrict__ w1,
+                                        const float* __restrict__ b1, const float* __restrict__ w2,
+                                        const float* __restrict__ b2, float* __restrict__ att, float inv_count, int C,
+                                        int hid, int n, int tiles, float* lds) {
+  constexpr int PB = 16;   // loads in flight per thread per batch
+  constexpr int LPO = 4;   // lanes per MLP output (shuffle-reduced)
+  constexpr int OPP = DCN_THREADS / LPO;  // outputs per pass
+  const int tid = threadIdx.x;
+  float* g = lds;          // [C]
+  float* hb = g + C;       // [hid]
+  float* red = hb + hid;   // [nsl][C]
+  const float* pn = partial + (int64_t)n * tiles * C;
+  const int nsl = C < DCN_THREADS ? DCN_THREADS / C : 1;
+  for (int e = tid; e < nsl * C; e += DCN_THREADS) {
+    const int s = e / C, ch = e - s * C;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int t0 = s; t0 < tiles; t0 += PB * nsl) {
+      float v[PB];
+#pragma unroll
+      for (int u = 0; u < PB; ++u) {
+        const int t = t0 + u * nsl;
+        v[u] = t < tiles ? dev_load(pn + (int64_t)t * C + ch) : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < PB; ++u) acc[u & 3] += v[u];
+    }
+    red[e] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+  __syncthreads();
+  for (int ch = tid; ch < C; ch += DCN_THREADS) {
+    float v = 0.f;
+    for (int s = 0; s < nsl; ++s) v += red[s * C + ch];
+    g[ch] = v * inv_count;
+  }
+  __syncthreads();
+  const int part = tid & (LPO - 1);
+  // out[o] = act(sum_k w[o][k] in[k] + b[o]): LPO lanes per output, each taking k = part, part + LPO, ...
+  auto layer = [&](const float* __restrict__ w, const float* __restrict__ b, const float* in, int nin, int nout,
+                   bool relu, float* dst) {
+    for (int o0 = 0; o0 < nout; o0 += OPP) {
+      const int o = o0 + tid / LPO;
+      const float* wr = w + (int64_t)(o < nout ? o : 0) * nin;
+      float acc = 0.f;
+      for (int k0 = part; k0 < nin; k0 += PB * LPO) {
+        float wv[PB];
+#pragma unroll
+        for (int u = 0; u < PB; ++u) {
+          const int k = k0 + u * LPO;
+          wv[u] = (o < nout && k < nin) ? wr[k] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < PB; ++u) {
+          const int k = k0 + u * LPO;
+          acc += wv[u] * in[k < nin ? k : 0];
+        }
+      }
+      acc += __shfl_xor(acc, 1);
+      acc += __shfl_xor(acc, 2);
+      if (o < nout && part == 0) {
+        const float v = acc + (b ? b[o] : 0.f);
+        dst[o] = relu ? fmaxf(v, 0.f) : sigmoidf_(v);
+      }
+    }
+  };
+  layer(w1, b1, g, C, hid, true, hb);
+  __syncthreads();
+  layer(w2, b2, hb, hid, C, false, att + (int64_t)n * C);
 }
 
 // ---- kernel ------------------------------------------------------------------------------------
@@ -1067,7 +1163,35 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       float v = 0.f;
 #pragma unroll
       for (int i = 0; i < DCN_WAVES; ++i) v += gap_red[i][tid];
-      a.gap_partial[((int64_t)n * g.tiles + tile) * a.cout + co] = v;
+      float* dst = a.gap_partial + ((int64_t)n * g.tiles + tile) * a.cout + co;
+      if (MODE != MODE_PLAIN && a.se_att)
+        rmw_store(dst, v);  // read by another block of this launch (fused SE)
+      else
+        *dst = v;
+    }
+  }
+
+  // ---- 5. fused squeeze-excitation: the image's last block runs the MLP -------------------------------
+  // (exchange protocol at se_tail)
+  if constexpr (MODE != MODE_PLAIN) {
+    if (a.se_att && a.gap_partial) {
+      __shared__ int s_last;
+      __syncthreads();  // this block's partial exchanges are performed; the epilogue's LDS tile is free
+      if (tid == 0) {
+        const unsigned total = (unsigned)g.tiles * gridDim.y;
+        const unsigned prev = __hip_atomic_fetch_add(a.se_count + n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = prev + 1u == total;
+        if (last) {
+          const unsigned z = __hip_atomic_exchange(a.se_count + n, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          asm volatile("" ::"v"(z));
+        }
+        s_last = last;
+      }
+      __syncthreads();
+      if (s_last) {
+        se_tail(a.gap_partial, a.se_w1, a.se_b1, a.se_w2, a.se_b2, a.se_att, a.se_inv_count, a.cout, a.se_hid, n,
+                g.tiles, (float*)region);
+      }
     }
   }
 }
@@ -1146,6 +1270,14 @@ static int validate_dcn(const kad_dcn_args* a, int mode, DcnGeom* g_out) {
   const int ho = (a->h + 2 * a->pad - 3) / a->stride + 1;
   const int wo = (a->w + 2 * a->pad - 3) / a->stride + 1;
   KAD_CHECK_ARG(ho > 0 && wo > 0, "empty output");
+  if (a->se_att) {
+    KAD_CHECK_ARG(mode != MODE_PLAIN, "the fused squeeze-excitation needs a DCN / DSC output");
+    KAD_CHECK_ARG(a->gap_partial && a->se_w1 && a->se_w2 && a->se_count && a->se_hid > 0,
+                  "fused squeeze-excitation: gap_partial, se_w1, se_w2, se_count and se_hid > 0 are required");
+    KAD_CHECK_ARG((a->cout + a->se_hid + DCN_THREADS) * 4 <= DCN_SE_LDS,
+                  "fused squeeze-excitation: Cout + hidden = %d exceeds %d", a->cout + a->se_hid,
+                  DCN_SE_LDS / 4 - DCN_THREADS);
+  }
   const uintptr_t align = (uintptr_t)a->x | (uintptr_t)a->wpack | (uintptr_t)a->off_wpack;
   KAD_CHECK_ARG(align % 16 == 0, "x and packed weights must be 16-byte aligned");
   *g_out = make_geom(*a, ho, wo);

@@ -19,7 +19,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libkadconv
 
 KAD_F32, KAD_F16, KAD_BF16 = 0, 1, 2
 KAD_NHWC, KAD_NCHW = 0, 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _DTYPES = {torch.float32: KAD_F32, torch.float16: KAD_F16, torch.bfloat16: KAD_BF16}
 
@@ -40,6 +40,8 @@ class DcnArgs(ctypes.Structure):
         ('mask_sn', c_i64), ('mask_sp', c_i64), ('mask_sc', c_i64),
         ('n', c_int), ('cin', c_int), ('cout', c_int), ('h', c_int), ('w', c_int), ('stride', c_int), ('pad', c_int),
         ('x_cs', c_int), ('out_layout', c_int), ('out_cs', c_int), ('dtype', c_int), ('relu', c_int),
+        ('se_w1', c_vp), ('se_b1', c_vp), ('se_w2', c_vp), ('se_b2', c_vp), ('se_att', c_vp), ('se_count', c_vp),
+        ('se_hid', c_int), ('se_inv_count', ctypes.c_float),
     ]
 
 
@@ -198,9 +200,29 @@ def dcn_pack_weights(weight, dtype):
     return out
 
 
+def _set_se(a, se, gap_partial, n, cout, ho, wo):
+    """Fused squeeze-excitation fields of kad_dcn_args: se = (w1 [hid, C], b1, w2 [C, hid], b2, att [N, C],
+    count [N] int32, zero before the first call)."""
+    if se is None:
+        return
+    w1, b1, w2, b2, att, count = se
+    if gap_partial is None:
+        raise ValueError('the fused squeeze-excitation reads the GAP partials: pass gap_partial')
+    for t in (w1, b1, w2, b2, att):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise TypeError('SE weights and att must be contiguous float32')
+    hid = w1.shape[0]
+    if tuple(w1.shape) != (hid, cout) or tuple(w2.shape) != (cout, hid) or tuple(att.shape) != (n, cout):
+        raise ValueError('SE shapes: w1 [hid, C], w2 [C, hid], att [N, C]')
+    if count.dtype != torch.int32 or count.numel() < n:
+        raise ValueError('SE counters: int32 [N]')
+    a.se_w1, a.se_b1, a.se_w2, a.se_b2 = _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2)
+    a.se_att, a.se_count, a.se_hid, a.se_inv_count = _ptr(att), _ptr(count), hid, 1.0 / (ho * wo)
+
+
 def dcn_fwd(x_nhwc, cin, offset, offset_strides, mask, mask_strides, wpack, cout, out, *, stride=1, pad=1,
             bias=None, post_mul=None, post_add=None, post_scale=None, relu=False, out_layout=KAD_NHWC,
-            gap_partial=None, h=None, w=None):
+            gap_partial=None, h=None, w=None, se=None):
     """Low-level launcher: x_nhwc is [N, H, W, x_cs] (x_cs % 8 == 0, zero-padded channels)."""
     _need_gpu(x_nhwc, offset, mask, wpack, out)
     N, H, W, cs = x_nhwc.shape
@@ -222,14 +244,16 @@ def dcn_fwd(x_nhwc, cin, offset, offset_strides, mask, mask_strides, wpack, cout
             raise TypeError('offset/mask/epilogue/gap tensors must be float32')
     if wpack.dtype != x_nhwc.dtype or out.dtype != x_nhwc.dtype:
         raise TypeError('x, packed weights and out must share a dtype')
+    _set_se(a, se, gap_partial, N, cout, (H + 2 * pad - 3) // stride + 1, (W + 2 * pad - 3) // stride + 1)
     _check(load().kad_dcn_fwd(ctypes.byref(a), _stream()), 'kad_dcn_fwd')
     return out
 
 
 def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, out, *, stride=1, pad=1,
             bias=None, post_mul=None, post_add=None, post_scale=None, relu=False, out_layout=KAD_NHWC,
-            gap_partial=None):
-    """conv_offset + deformable conv in one launch (offsets never leave the chip)."""
+            gap_partial=None, se=None):
+    """conv_offset + deformable conv in one launch (offsets never leave the chip); with `se`,
+    also the squeeze-excitation MLP of the output (see _set_se)."""
     _need_gpu(x_nhwc, off_wpack, wpack, out)
     N, H, W, cs = x_nhwc.shape
     a = DcnArgs()
@@ -250,6 +274,7 @@ def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, o
             raise TypeError('offset bias/mask/epilogue/gap tensors must be float32')
     if wpack.dtype != x_nhwc.dtype or off_wpack.dtype != x_nhwc.dtype or out.dtype != x_nhwc.dtype:
         raise TypeError('x, packed weights and out must share a dtype')
+    _set_se(a, se, gap_partial, N, cout, (H + 2 * pad - 3) // stride + 1, (W + 2 * pad - 3) // stride + 1)
     _check(load().kad_dsc_fwd(ctypes.byref(a), _stream()), 'kad_dsc_fwd')
     return out
 

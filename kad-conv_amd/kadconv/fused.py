@@ -90,7 +90,7 @@ class DSCPlan:
                 and x.shape[1] == self.cin and self.stride == 1 and self.pad == 1 and x.numel() > 0)
 
     def stages(self, y, n, h, w, out, out_layout, bias=None, post_mul=None, post_add=None, post_scale=None,
-               relu=False, gap=None, tag='', sums=None):
+               relu=False, gap=None, tag='', sums=None, se=None):
         """DSC on an NHWC map y [N, h, w, cs] (cin channels) as a list of
         (name, launch) pairs with every buffer allocated up front.  `sums` =
         (rows, nrp, cols, ncp) axial partial sums of y if already computed."""
@@ -117,7 +117,7 @@ class DSCPlan:
         # conv_offset + deformable conv in one kernel: the offsets stay on chip
         st.append(('dsc' + tag, lambda: _ext.dsc_fwd(
             y, self.cin, owp, self.off_b, mask, (P * 9, 9, 1), wp, self.cout, out, bias=b, post_mul=post_mul,
-            post_add=post_add, post_scale=post_scale, relu=relu, out_layout=out_layout, gap_partial=gap)))
+            post_add=post_add, post_scale=post_scale, relu=relu, out_layout=out_layout, gap_partial=gap, se=se)))
         return st
 
     def run(self, *args, **kw):
@@ -149,8 +149,8 @@ class _Branch:
         self.dsc = DSCPlan(dsc)
         self.bn_a, self.bn_b = _fold_bn(bn)
         self.scale = _f32(scale.weight.reshape(-1))
-        self.w1, self.b1 = _f32(fc[0].weight), _f32(fc[0].bias)
-        self.w2, self.b2 = _f32(fc[2].weight), _f32(fc[2].bias)
+        self.w1, self.b1 = _f32(fc[0].weight.reshape(fc[0].weight.shape[0], -1)), _f32(fc[0].bias)
+        self.w2, self.b2 = _f32(fc[2].weight.reshape(fc[2].weight.shape[0], -1)), _f32(fc[2].bias)
         self.hid = self.w1.shape[0]
         self._packed = {}
 
@@ -235,11 +235,11 @@ class KADConvPlan:
             else:
                 z = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
                 z_layout = _ext.KAD_NHWC
-            ch = br.dsc.stages(ys[i], N, h, w, z, z_layout, post_mul=br.bn_a, post_add=br.bn_b,
-                               post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i])
+            # the SE MLP runs in the DSC kernel's last block per image (att from the GAP partials)
             att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
-            ch.append((f'se{i}', lambda gap=gap, tiles=tiles, P=P, br=br, att=att: _ext.se_mlp(
-                gap, tiles, 1.0 / P, br.w1, br.b1, br.w2, br.b2, att, N, br.c, br.hid)))
+            se = (br.w1, br.b1, br.w2, br.b2, att, self._se_counters(dev, i, N))
+            ch = br.dsc.stages(ys[i], N, h, w, z, z_layout, post_mul=br.bn_a, post_add=br.bn_b,
+                               post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i], se=se)
             if full:
                 ch.append((f'merge{i}', lambda br=br, att=att: _ext.scale_residual(
                     out_v, att, xin, br.c_off, br.c, out_layout)))
@@ -250,6 +250,17 @@ class KADConvPlan:
                     out_v, out_layout, mb, residual=xin, channels=(br.c_off, br.c_off + br.c))))
             chains.append(ch)
         return st, chains, [], out
+
+    def _se_counters(self, dev, i, n):
+        """Per-image arrival counters of branch i's fused SE (zero between calls), kept per device."""
+        key = (torch.device(dev).index, i)
+        counters = getattr(self, '_se_count', {})
+        c = counters.get(key)
+        if c is None or c.numel() < n:
+            c = torch.zeros(max(n, 1), dtype=torch.int32, device=dev)
+            counters[key] = c
+            self._se_count = counters
+        return c
 
     def _side_streams(self, dev):
         """One side stream per branch chain (default priority), created once per device."""

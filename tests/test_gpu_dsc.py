@@ -163,3 +163,45 @@ def test_dsc_rejects_stride3():
     out = torch.empty(1, 22, 22, 8, dtype=torch.float16, device='cuda')
     with pytest.raises(RuntimeError, match='stride 3'):
         _ext.dsc_fwd(x, 8, owp, None, None, (0, 0, 0), wp, 8, out, stride=3)
+
+
+@pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
+@pytest.mark.parametrize('C,Co,hid,H,W', [(86, 86, 86, 23, 31), (24, 130, 16, 17, 40), (40, 40, 32, 9, 9)])
+def test_dsc_fused_squeeze_excitation(dt, C, Co, hid, H, W):
+    """kad_dsc_fwd with the SE fields set: the last block of each image turns the
+    GAP partials into att = sigmoid(W2 relu(W1 mean(out) + b1) + b2)
+    (KADConv.forward, kad_conv.py:125).  Reference: that MLP in float64 over the
+    kernel's own output (so only the reduction and the MLP are under test).
+    Several calls in a row with changing batch sizes share one counter buffer,
+    which every completed call must leave at zero; Co = 130 spans two column
+    blocks, whose partials the last block must both see.  att tolerance: 2e-5
+    absolute (fp32 sums of at most H*W values, sigmoid slope <= 1/4)."""
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(C * 7 + Co)
+    w1 = (torch.randn(hid, Co, generator=g) / Co ** 0.5).to(dev)
+    b1 = (torch.randn(hid, generator=g) * 0.1).to(dev)
+    w2 = (torch.randn(Co, hid, generator=g) / hid ** 0.5).to(dev)
+    b2 = (torch.randn(Co, generator=g) * 0.1).to(dev)
+    count = torch.zeros(4, dtype=torch.int32, device=dev)
+    for call, N in enumerate([3, 1, 4, 2]):
+        x, ow, ob, w, b = _inputs(N, C, Co, H, W, seed=call + 11)
+        mask = _mask(N, H, W, seed=call)
+        xq = nhwc_padded(x.to(dtype).to(dev))
+        md = mask.permute(0, 2, 3, 1).contiguous().to(dev)
+        wp = _ext.dcn_pack_weights(w.to(dtype).to(dev), dtype)
+        owp = _ext.dcn_pack_weights(ow.to(dtype).to(dev), dtype)
+        out = torch.empty(N, Co, H, W, dtype=dtype, device=dev)
+        gap = torch.full((N, _ext.dcn_tiles(H, W), Co), float('nan'), device=dev)
+        att = torch.full((N, Co), float('nan'), device=dev)
+        print(f'fused SE {dt} C={C} Co={Co} hid={hid} {H}x{W} call {call} N={N}', flush=True)
+        _ext.dsc_fwd(xq, C, owp, ob.to(dev), md, (H * W * 9, 9, 1), wp, Co, out, bias=b.to(dev),
+                     out_layout=_ext.KAD_NCHW, gap_partial=gap, se=(w1, b1, w2, b2, att, count))
+        torch.cuda.synchronize()
+        assert int(count.abs().sum().item()) == 0, 'arrival counters not reset'
+        m = out.double().mean(dim=(2, 3))
+        h = torch.relu(m @ w1.double().t() + b1.double())
+        ref = torch.sigmoid(h @ w2.double().t() + b2.double())
+        err = (att.double() - ref).abs().max().item()
+        assert err <= 2e-5, f'call {call}: att max|d| = {err:.3e}'
+        check_close(out, _ref(x, ow, ob, w, b, mask, dtype), dtype, 'output')

@@ -574,6 +574,97 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(kad_merge_args a) {
   }
 }
 
+// NCHW output, branches with disjoint channel ranges, planes of a multiple of 8
+// pixels, 16-byte aligned tensors.  Block = (8-channel group of one branch, run
+// of MB_E consecutive pixels of the plane, image): the residual reads and the
+// output writes are 16-byte vectors over contiguous 2 KB runs of each of the 8
+// planes.  The branch-map rows that the run's output rows sample (NHWC, one
+// 16-byte piece = the group's 8 channels of a pixel) are staged first, as
+// planar fp32 [8][rows][bw], so the interpolation reads consecutive addresses.
+constexpr int MB_E = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(256) void merge_band_kernel(kad_merge_args a, int srows_cap, int bw_cap) {
+  extern __shared__ float zsm[];  // [8][srows_cap][bw_cap]
+  __shared__ float s_att[8], s_gate[8];
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  const int run = blockIdx.x, n = blockIdx.z, tid = threadIdx.x;
+  int b = 0, k = blockIdx.y;
+#pragma unroll
+  for (int i = 0; i < KAD_MAX_BRANCHES; ++i) {
+    if (i == b && i < a.nbranch - 1) {
+      const int ng = ceil_div(a.br_c[i], 8);
+      if (k >= ng) {
+        k -= ng;
+        b = i + 1;
+      }
+    }
+  }
+  const int cb0 = k * 8;
+  const int nch = a.br_c[b] - cb0 < 8 ? a.br_c[b] - cb0 : 8;
+  const int cbase = a.br_c_off[b] + cb0;
+  const int H = a.h, W = a.w, P = H * W;
+  const int bh = a.br_h[b], bw = a.br_w[b], cs = a.br_cs[b];
+  const int f0 = run * MB_E, f1 = P - f0 < MB_E ? P : f0 + MB_E;
+  const float inv_w = 1.f / (float)W;
+  const int ya = (int)(((float)f0 + 0.5f) * inv_w), yb = (int)(((float)(f1 - 1) + 0.5f) * inv_w);
+  const RowSrc ra = row_src(a, b, ya), rb = row_src(a, b, yb);
+  const int sy_lo = ra.y0;
+  int srows = rb.y1 - sy_lo + 1;
+  srows = srows < srows_cap ? srows : srows_cap;  // the host sizes srows_cap for the longest run
+  const T* z = (const T*)a.br_z[b] + (int64_t)n * bh * bw * cs + cb0;
+  for (int e = tid; e < srows * bw; e += 256) {
+    const int r = e / bw, sx = e - r * bw;
+    const v8 v = *(const v8*)(z + ((int64_t)(sy_lo + r) * bw + sx) * cs);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) zsm[(j * srows_cap + r) * bw_cap + sx] = to_f32(v[j]);
+  }
+  if (tid < 8) {
+    s_att[tid] = tid < nch ? a.br_coeff[b] * (a.br_att[b] ? a.br_att[b][(int64_t)n * a.br_c[b] + cb0 + tid] : 1.f)
+                           : 0.f;
+    s_gate[tid] = (a.gate && tid < nch) ? a.gate[cbase + tid] : 1.f;
+  }
+  __syncthreads();
+  const float sh = (float)bh / (float)H, sw = (float)bw / (float)W;
+  const T* res = (const T*)a.residual;
+  T* out = (T*)a.out;
+  constexpr int VPP = MB_E / 8;  // vectors per plane and run
+  for (int q = tid; q < 8 * VPP; q += 256) {
+    const int cl = q / VPP, f = f0 + (q - cl * VPP) * 8;
+    if (cl >= nch || f >= f1) continue;
+    const int64_t pb = ((int64_t)n * a.c + cbase + cl) * P + f;
+    v8 rv;
+    if (res) rv = *(const v8*)(res + pb);
+    const float at = s_att[cl], gt = s_gate[cl];
+    const float* zp = zsm + cl * srows_cap * bw_cap;
+    int y = (int)(((float)f + 0.5f) * inv_w), x = f - y * W;
+    int y0, y1;
+    float ly;
+    src_index(y, bh, H, sh, y0, y1, ly);
+    v8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (x == W) {  // next output row
+        x = 0;
+        ++y;
+        src_index(y, bh, H, sh, y0, y1, ly);
+      }
+      int x0, x1;
+      float lx;
+      src_index(x, bw, W, sw, x0, x1, lx);
+      const float* r0 = zp + (y0 - sy_lo) * bw_cap;
+      const float* r1 = zp + (y1 - sy_lo) * bw_cap;
+      const float top = r0[x0] + lx * (r0[x1] - r0[x0]);
+      const float bot = r1[x0] + lx * (r1[x1] - r1[x0]);
+      float v = at * (top + ly * (bot - top));
+      if (res) v += to_f32(rv[j]);
+      o[j] = from_f32<T>(v * gt);
+      ++x;
+    }
+    *(v8*)(out + pb) = o;
+  }
+}
+
 // NHWC output: block = (one row, image); threads run along channels, so every
 // read (branch maps, residual) and the write are contiguous.
 template <typename T>
@@ -857,7 +948,29 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
   disjoint = disjoint && cover == a->c_end;
   const int tsz = a->dtype == KAD_F32 ? 4 : 2;
   const size_t row_lds = (size_t)2 * maxbw * 40 * tsz + (size_t)32 * ceil_div(a->w, 4) * 4 * tsz;
-  if (a->layout == KAD_NCHW && disjoint && row_lds <= 64 * 1024) {
+  // band kernel: rows of the longest run of MB_E pixels, and the source rows they sample
+  const int64_t P = (int64_t)a->h * a->w;
+  const int run_rows = ceil_div(MB_E, a->w) + 1;
+  int srows_cap = 0, ngroups = 0;
+  bool band = a->layout == KAD_NCHW && disjoint && P % 8 == 0 && P < (1ll << 23) &&  // float pixel -> row exact
+              ((uintptr_t)a->out % 16) == 0 && ((uintptr_t)a->residual % 16) == 0;
+  for (int b = 0; b < a->nbranch; ++b) {
+    const int r = (int)((double)(run_rows - 1) * a->br_h[b] / a->h) + 3;
+    srows_cap = r > srows_cap ? r : srows_cap;
+    ngroups += ceil_div(a->br_c[b], 8);
+    band = band && a->br_cs[b] % 8 == 0 && a->br_cs[b] >= round_up(a->br_c[b], 8) &&
+           ((uintptr_t)a->br_z[b] % (8 * tsz)) == 0;
+  }
+  const size_t band_lds = (size_t)8 * srows_cap * maxbw * sizeof(float);
+  if (band && band_lds <= 64 * 1024) {
+    dim3 grid((unsigned)ceil_div(P, (int64_t)MB_E), ngroups, a->n);
+    switch (a->dtype) {
+      case KAD_F32: hipLaunchKernelGGL(merge_band_kernel<float>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw); break;
+      case KAD_F16: hipLaunchKernelGGL(merge_band_kernel<half_t>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw); break;
+      case KAD_BF16: hipLaunchKernelGGL(merge_band_kernel<bf16_t>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw); break;
+      default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
+    }
+  } else if (a->layout == KAD_NCHW && disjoint && row_lds <= 64 * 1024) {
     dim3 grid(a->h, nchunks, a->n);
     switch (a->dtype) {
       case KAD_F32: hipLaunchKernelGGL(merge_rows_kernel<float>, grid, dim3(256), row_lds, st, *a); break;

@@ -244,6 +244,19 @@ int kad_lcsa_prep(const float *rows, int nrp, const float *cols, int ncp, float 
 int kad_lcsa_mask(const float *arow, const float *colm, const float *params, const void *emat, const float *ebias,
                   float *mask, int n, int c, int h, int w, int emat_dtype, void *stream);
 
+/* kad_lcsa_mask with the channel contraction split over ksplit blocks per
+ * 16x16 tile (for small images, whose few tiles would leave most CUs idle):
+ * each split writes its raw logits to work[ksplit][N][H][W][9] (fp32,
+ * kad_lcsa_mask_work_elems elements; NULL for ksplit = 1), a second launch adds
+ * the splits in order, then ebias and the sigmoid (deterministic).
+ * kad_lcsa_mask_splits gives the split count used by the fused forwards (1 for
+ * shapes with enough tiles).  No reference counterpart (scheduling only). */
+int kad_lcsa_mask_splits(int n, int c, int h, int w);
+int64_t kad_lcsa_mask_work_elems(int n, int h, int w, int ksplit);
+int kad_lcsa_mask_split(const float *arow, const float *colm, const float *params, const void *emat,
+                        const float *ebias, float *mask, int n, int c, int h, int w, int emat_dtype, int ksplit,
+                        float *work, void *stream);
+
 /* ------------------------------------------------------------------------ */
 /* Squeeze-excitation                                                        */
 /* ------------------------------------------------------------------------ */

@@ -150,7 +150,7 @@ template <typename ET>
 __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* arow, const float* colm,
                                                                  const float* params, const ET* emat,
                                                                  const float* ebias, float* mask, int c, int h,
-                                                                 int w, int cp) {
+                                                                 int w, int cp, int ksplit, float* part) {
   constexpr int LDU = LmCfg<ET>::ldu;
   __shared__ __align__(16) ET us[LM_UR * LM_TW * LDU];
   __shared__ __align__(16) float s_col[LM_UR][LM_SCS];   // column means, columns w0 - 5 .. w0 + 20
@@ -161,7 +161,8 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
   const float* b1 = params + 11 * c;
   const float* bna = params + 12 * c;
   const float* bnb = params + 13 * c;
-  const int n = blockIdx.z;
+  // grid.z = N x ksplit: split sp takes the chunks [kc0, kc1) of the channel contraction
+  const int n = blockIdx.z / ksplit, sp = blockIdx.z - n * ksplit;
   const int h0 = blockIdx.y * LM_TH, w0 = blockIdx.x * LM_TW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, grp = lane >> 4;
@@ -171,118 +172,136 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  for (int cs = 0; cs < cp; cs += LM_SC) {
-    const int nsc = cp - cs < LM_SC ? cp - cs : LM_SC;   // multiple of 32
-    // ---- 1. one round of loads: column / row means and parameters of this group ----------------
-    // Index space uses the fixed group width LM_SC (constant divisors); channels past
-    // c or past the group read 0.
-    constexpr int NW = (LM_UR * LM_SC + LM_THREADS - 1) / LM_THREADS;    // per window
-    constexpr int NP = (LM_SC * BAND + LM_THREADS - 1) / LM_THREADS;     // w1
-    constexpr int NQ = (3 * LM_SC + LM_THREADS - 1) / LM_THREADS;        // b1 | bn_a | bn_b
-    __syncthreads();  // the previous group's LDS data is consumed
-    float vc_[NW], va_[NW], vw_[NP], vq_[NQ];
-#pragma unroll
-    for (int u = 0; u < NW; ++u) {
-      const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC, gc = cs + ch;
-      const int gx = w0 - HALF_BAND + r, gy = h0 - HALF_BAND + r;
-      const bool ok = r < LM_UR && ch < nsc && gc < c;
-      vc_[u] = (ok && gx >= 0 && gx < w) ? colm_n[(int64_t)gx * c + gc] : 0.f;
-      va_[u] = (ok && gy >= 0 && gy < h) ? arow_n[(int64_t)gy * c + gc] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < NP; ++u) {
-      const int e = tid + u * LM_THREADS;
-      vw_[u] = (e < nsc * BAND && cs * BAND + e < c * BAND) ? w1[cs * BAND + e] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < NQ; ++u) {
-      const int e = tid + u * LM_THREADS, which = e / LM_SC, ch = e - which * LM_SC, gc = cs + ch;
-      vq_[u] = (which < 3 && ch < nsc && gc < c) ? (which == 0 ? b1 : which == 1 ? bna : bnb)[gc] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < NW; ++u) {
-      const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC;
-      if (r < LM_UR) {
-        s_col[r][ch] = vc_[u];
-        s_a[r][ch] = va_[u];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < NP; ++u) {
-      const int e = tid + u * LM_THREADS;
-      if (e < LM_SC * BAND) s_w1[e] = vw_[u];
-    }
-#pragma unroll
-    for (int u = 0; u < NQ; ++u) {
-      const int e = tid + u * LM_THREADS, which = e / LM_SC, ch = e - which * LM_SC;
-      if (which < 3) (which == 0 ? s_b1 : which == 1 ? s_bna : s_bnb)[ch] = vq_[u];
-    }
-    __syncthreads();
-    // ---- 2. strip-conv coefficients of the 16 columns (separable 1x11 conv + folded BN) ----------
-    for (int e = tid; e < LM_TW * LM_SC; e += LM_THREADS) {
-      const int col = e / LM_SC, ch = e - col * LM_SC, gx = w0 + col;
-      float S = 0.f, B = 0.f;
-#pragma unroll
-      for (int k = 0; k < BAND; ++k) {
-        const int xx = gx + k - HALF_BAND;
-        const float wk = s_w1[ch * BAND + k];
-        if (xx >= 0 && xx < w) {
-          S += wk;
-          B += wk * s_col[col + k][ch];
-        }
-      }
-      const bool ok = gx < w && ch < nsc && cs + ch < c;
-      s_alpha[col][ch] = ok ? s_bna[ch] * S : 0.f;
-      s_beta[col][ch] = ok ? s_bna[ch] * (B + s_b1[ch]) + s_bnb[ch] : 0.f;
-    }
-    // ---- 3. per 32-channel chunk: E in flight while u is formed, then the GEMM ---------------------
-    for (int c0 = 0; c0 < nsc; c0 += 32) {
-      // this lane's E fragments: logit row l16, taps 0..10, channels cs + c0 + grp * 8 .. + 8
-      typedef typename LmFrag<ET>::frag EF;
-      EF ef[BAND];
-#pragma unroll
-      for (int k = 0; k < BAND; ++k) ef[k] = LmFrag<ET>::ld(emat + (int64_t)(l16 * BAND + k) * cp + cs + c0 + grp * 8);
-      __syncthreads();  // alpha / beta ready; the previous chunk's MFMAs are done with us
-      // u = relu(alpha * a + beta), 8 channels per task, one 16-byte LDS store
-      for (int e = tid; e < LM_UR * LM_TW * 4; e += LM_THREADS) {
-        const int g = e & 3, q = e >> 2, col = q & (LM_TW - 1), r = q >> 4;
-        const int gy = h0 - HALF_BAND + r;
-        const bool rv = gy >= 0 && gy < h;
-        const int ch = c0 + g * 8;
-        const floatx4 al0 = *(const floatx4*)&s_alpha[col][ch], al1 = *(const floatx4*)&s_alpha[col][ch + 4];
-        const floatx4 be0 = *(const floatx4*)&s_beta[col][ch], be1 = *(const floatx4*)&s_beta[col][ch + 4];
-        const floatx4 a0 = *(const floatx4*)&s_a[r][ch], a1 = *(const floatx4*)&s_a[r][ch + 4];
-        ET* dst = us + (r * LM_TW + col) * LDU + g * 8;
-        if constexpr (sizeof(ET) == 2) {
-          half8_t v;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            v[j] = (half_t)(rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f);
-            v[j + 4] = (half_t)(rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f);
-          }
-          *(half8_t*)dst = v;
-        } else {
-          floatx4 v0, v1;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            v0[j] = rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f;
-            v1[j] = rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f;
-          }
-          ((floatx4*)dst)[0] = v0;
-          ((floatx4*)dst)[1] = v1;
-        }
-      }
-      __syncthreads();
-#pragma unroll
-      for (int k = 0; k < BAND; ++k) {
-#pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          const int r = wave * 4 + f;  // tile row of this fragment
-          acc[f] = LmFrag<ET>::mma(ef[k], &us[((r + k) * LM_TW + l16) * LDU + grp * 8], acc[f]);
-        }
-      }
-    }
+  // Flat loop over 32-channel chunks kc; groups of LM_SC / 32 = 3 chunks share the
+  // staged means / parameters.  Loads run ahead: the next group's means and
+  // parameters are requested as soon as the current group is in LDS, the next
+  // chunk's E fragments as soon as the current chunk's MFMAs are issued.  The
+  // barriers inside the loop wait for LDS traffic only (a workgroup barrier
+  // would also drain those loads).
+  constexpr int NW = (LM_UR * LM_SC + LM_THREADS - 1) / LM_THREADS;    // per window
+  constexpr int NP = (LM_SC * BAND + LM_THREADS - 1) / LM_THREADS;     // w1
+  constexpr int NQ = (3 * LM_SC + LM_THREADS - 1) / LM_THREADS;        // b1 | bn_a | bn_b
+  constexpr int CPG = LM_SC / 32;                                      // chunks per group
+  const int nk = cp / 32;
+  const int kc0 = sp * nk / ksplit, kc1 = (sp + 1) * nk / ksplit;
+  float vc_[NW], va_[NW], vw_[NP], vq_[NQ];
+  typedef typename LmFrag<ET>::frag EF;
+  EF ef[BAND];
+  // Index space uses the fixed group width LM_SC (constant divisors); channels past
+  // c or past the group read 0.
+#define LM_LOAD_GROUP(CS)                                                                                      \
+  {                                                                                                            \
+    const int cs_ = (CS), nsc_ = cp - cs_ < LM_SC ? cp - cs_ : LM_SC;                                          \
+    _Pragma("unroll") for (int u = 0; u < NW; ++u) {                                                           \
+      const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC, gc = cs_ + ch;                    \
+      const int gx = w0 - HALF_BAND + r, gy = h0 - HALF_BAND + r;                                              \
+      const bool ok = r < LM_UR && ch < nsc_ && gc < c;                                                        \
+      vc_[u] = (ok && gx >= 0 && gx < w) ? colm_n[(int64_t)gx * c + gc] : 0.f;                                 \
+      va_[u] = (ok && gy >= 0 && gy < h) ? arow_n[(int64_t)gy * c + gc] : 0.f;                                 \
+    }                                                                                                          \
+    _Pragma("unroll") for (int u = 0; u < NP; ++u) {                                                           \
+      const int e = tid + u * LM_THREADS;                                                                      \
+      vw_[u] = (e < nsc_ * BAND && cs_ * BAND + e < c * BAND) ? w1[cs_ * BAND + e] : 0.f;                      \
+    }                                                                                                          \
+    _Pragma("unroll") for (int u = 0; u < NQ; ++u) {                                                           \
+      const int e = tid + u * LM_THREADS, which = e / LM_SC, ch = e - which * LM_SC, gc = cs_ + ch;            \
+      vq_[u] = (which < 3 && ch < nsc_ && gc < c) ? (which == 0 ? b1 : which == 1 ? bna : bnb)[gc] : 0.f;      \
+    }                                                                                                          \
   }
+  // this lane's E fragments of chunk KC: logit row l16, taps 0..10, channels 32 KC + grp * 8 .. + 8
+#define LM_LOAD_E(KC)                                                                                          \
+  _Pragma("unroll") for (int k = 0; k < BAND; ++k) ef[k] =                                                     \
+      LmFrag<ET>::ld(emat + (int64_t)(l16 * BAND + k) * cp + (KC) * 32 + grp * 8);
+#define LM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+  LM_LOAD_GROUP((kc0 / CPG) * LM_SC);
+  LM_LOAD_E(kc0);
+  for (int kc = kc0; kc < kc1; ++kc) {
+    const int g = kc / CPG, c0 = (kc - g * CPG) * 32, cs = g * LM_SC;
+    if (c0 == 0 || kc == kc0) {  // first chunk of a group (or of the split): stage it, request the next one
+      const int nsc = cp - cs < LM_SC ? cp - cs : LM_SC;
+      LM_LDS_BARRIER();  // the previous group's LDS data is consumed
+#pragma unroll
+      for (int u = 0; u < NW; ++u) {
+        const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC;
+        if (r < LM_UR) {
+          s_col[r][ch] = vc_[u];
+          s_a[r][ch] = va_[u];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < NP; ++u) {
+        const int e = tid + u * LM_THREADS;
+        if (e < LM_SC * BAND) s_w1[e] = vw_[u];
+      }
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) {
+        const int e = tid + u * LM_THREADS, which = e / LM_SC, ch = e - which * LM_SC;
+        if (which < 3) (which == 0 ? s_b1 : which == 1 ? s_bna : s_bnb)[ch] = vq_[u];
+      }
+      LM_LDS_BARRIER();
+      if ((g + 1) * CPG < kc1) LM_LOAD_GROUP(cs + LM_SC);
+      // strip-conv coefficients of the 16 columns (separable 1x11 conv + folded BN)
+      for (int e = tid; e < LM_TW * LM_SC; e += LM_THREADS) {
+        const int col = e / LM_SC, ch = e - col * LM_SC, gx = w0 + col;
+        float S = 0.f, B = 0.f;
+#pragma unroll
+        for (int k = 0; k < BAND; ++k) {
+          const int xx = gx + k - HALF_BAND;
+          const float wk = s_w1[ch * BAND + k];
+          if (xx >= 0 && xx < w) {
+            S += wk;
+            B += wk * s_col[col + k][ch];
+          }
+        }
+        const bool ok = gx < w && ch < nsc && cs + ch < c;
+        s_alpha[col][ch] = ok ? s_bna[ch] * S : 0.f;
+        s_beta[col][ch] = ok ? s_bna[ch] * (B + s_b1[ch]) + s_bnb[ch] : 0.f;
+      }
+    }
+    LM_LDS_BARRIER();  // alpha / beta ready; the previous chunk's MFMAs are done with us
+    // u = relu(alpha * a + beta), 8 channels per task, one 16-byte LDS store
+    for (int e = tid; e < LM_UR * LM_TW * 4; e += LM_THREADS) {
+      const int gq = e & 3, q = e >> 2, col = q & (LM_TW - 1), r = q >> 4;
+      const int gy = h0 - HALF_BAND + r;
+      const bool rv = gy >= 0 && gy < h;
+      const int ch = c0 + gq * 8;
+      const floatx4 al0 = *(const floatx4*)&s_alpha[col][ch], al1 = *(const floatx4*)&s_alpha[col][ch + 4];
+      const floatx4 be0 = *(const floatx4*)&s_beta[col][ch], be1 = *(const floatx4*)&s_beta[col][ch + 4];
+      const floatx4 a0 = *(const floatx4*)&s_a[r][ch], a1 = *(const floatx4*)&s_a[r][ch + 4];
+      ET* dst = us + (r * LM_TW + col) * LDU + gq * 8;
+      if constexpr (sizeof(ET) == 2) {
+        half8_t v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = (half_t)(rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f);
+          v[j + 4] = (half_t)(rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f);
+        }
+        *(half8_t*)dst = v;
+      } else {
+        floatx4 v0, v1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v0[j] = rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f;
+          v1[j] = rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f;
+        }
+        ((floatx4*)dst)[0] = v0;
+        ((floatx4*)dst)[1] = v1;
+      }
+    }
+    LM_LDS_BARRIER();
+#pragma unroll
+    for (int k = 0; k < BAND; ++k) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        const int r = wave * 4 + f;  // tile row of this fragment
+        acc[f] = LmFrag<ET>::mma(ef[k], &us[((r + k) * LM_TW + l16) * LDU + grp * 8], acc[f]);
+      }
+    }
+    if (kc + 1 < kc1) LM_LOAD_E(kc + 1);
+  }
+#undef LM_LOAD_GROUP
+#undef LM_LOAD_E
+#undef LM_LDS_BARRIER
   // acc[f][i]: logit j = 4 * grp + i of pixel (row 4 * wave + f, col l16)
 #pragma unroll
   for (int f = 0; f < 4; ++f) {
@@ -291,9 +310,23 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = grp * 4 + i;
-      if (j < 9) mask[(((int64_t)n * h + gy) * w + gx) * 9 + j] = sigmoidf_(acc[f][i] + ebias[j]);
+      if (j >= 9) continue;
+      if (ksplit == 1)
+        mask[(((int64_t)n * h + gy) * w + gx) * 9 + j] = sigmoidf_(acc[f][i] + ebias[j]);
+      else  // raw logits of this split; lcsa_mask_reduce_kernel adds the splits up
+        part[((((int64_t)sp * gridDim.z / ksplit + n) * h + gy) * w + gx) * 9 + j] = acc[f][i];
     }
   }
+}
+
+// mask = sigmoid(sum over the splits, in split order, + ebias): one thread per (pixel, logit).
+__global__ __launch_bounds__(256) void lcsa_mask_reduce_kernel(const float* part, const float* ebias, float* mask,
+                                                               int64_t total, int ksplit) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float v = 0.f;
+  for (int s = 0; s < ksplit; ++s) v += part[s * total + i];
+  mask[i] = sigmoidf_(v + ebias[i % 9]);
 }
 
 }  // namespace kad
@@ -341,22 +374,64 @@ extern "C" int kad_lcsa_prep(const float* rows, int nrp, const float* cols, int 
   return check_launch("kad_lcsa_prep");
 }
 
+namespace kad {
+
+static int launch_lcsa_mask(const float* arow, const float* colm, const float* params, const void* emat,
+                            const float* ebias, float* mask, int n, int c, int h, int w, int emat_dtype, int ksplit,
+                            float* work, hipStream_t st) {
+  const int cp = round_up(c, 32);
+  dim3 grid(ceil_div(w, LM_TW), ceil_div(h, LM_TH), n * ksplit);
+  if (emat_dtype == KAD_F32)
+    hipLaunchKernelGGL(lcsa_mask_kernel<float>, grid, dim3(LM_THREADS), 0, st, arow, colm, params,
+                       (const float*)emat, ebias, mask, c, h, w, cp, ksplit, work);
+  else if (emat_dtype == KAD_F16)
+    hipLaunchKernelGGL(lcsa_mask_kernel<half_t>, grid, dim3(LM_THREADS), 0, st, arow, colm, params,
+                       (const half_t*)emat, ebias, mask, c, h, w, cp, ksplit, work);
+  else
+    return fail(KAD_EINVAL, "kad_lcsa_mask: emat dtype must be KAD_F32 or KAD_F16");
+  int rc = check_launch("kad_lcsa_mask");
+  if (rc || ksplit == 1) return rc;
+  const int64_t total = (int64_t)n * h * w * 9;
+  hipLaunchKernelGGL(lcsa_mask_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, work, ebias,
+                     mask, total, ksplit);
+  return check_launch("kad_lcsa_mask (split reduction)");
+}
+
+}  // namespace kad
+
 extern "C" int kad_lcsa_mask(const float* arow, const float* colm, const float* params, const void* emat,
                              const float* ebias, float* mask, int n, int c, int h, int w, int emat_dtype,
                              void* stream) {
   KAD_CHECK_ARG(arow && colm && params && emat && ebias && mask, "kad_lcsa_mask: null pointer");
   KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0, "kad_lcsa_mask: bad shape");
   KAD_CHECK_ARG(((uintptr_t)emat) % 16 == 0, "kad_lcsa_mask: emat must be 16-byte aligned");
-  const int cp = round_up(c, 32);
-  dim3 grid(ceil_div(w, LM_TW), ceil_div(h, LM_TH), n);
-  hipStream_t st = (hipStream_t)stream;
-  if (emat_dtype == KAD_F32)
-    hipLaunchKernelGGL(lcsa_mask_kernel<float>, grid, dim3(LM_THREADS), 0, st, arow, colm, params,
-                       (const float*)emat, ebias, mask, c, h, w, cp);
-  else if (emat_dtype == KAD_F16)
-    hipLaunchKernelGGL(lcsa_mask_kernel<half_t>, grid, dim3(LM_THREADS), 0, st, arow, colm, params,
-                       (const half_t*)emat, ebias, mask, c, h, w, cp);
-  else
-    return fail(KAD_EINVAL, "kad_lcsa_mask: emat dtype must be KAD_F32 or KAD_F16");
-  return check_launch("kad_lcsa_mask");
+  return kad::launch_lcsa_mask(arow, colm, params, emat, ebias, mask, n, c, h, w, emat_dtype, 1, nullptr,
+                               (hipStream_t)stream);
+}
+
+extern "C" int kad_lcsa_mask_splits(int n, int c, int h, int w) {
+  if (n <= 0 || c <= 0 || h <= 0 || w <= 0) return 0;
+  // two blocks fit a CU; split the channel chunks until about 512 blocks are in flight
+  const int blocks = ceil_div(w, kad::LM_TW) * ceil_div(h, kad::LM_TH) * n;
+  const int nk = round_up(c, 32) / 32;
+  const int want = 512 / blocks;
+  return want <= 1 ? 1 : (want < nk ? want : nk);
+}
+
+extern "C" int64_t kad_lcsa_mask_work_elems(int n, int h, int w, int ksplit) {
+  return (n > 0 && h > 0 && w > 0 && ksplit > 1) ? (int64_t)ksplit * n * h * w * 9 : 0;
+}
+
+extern "C" int kad_lcsa_mask_split(const float* arow, const float* colm, const float* params, const void* emat,
+                                   const float* ebias, float* mask, int n, int c, int h, int w, int emat_dtype,
+                                   int ksplit, float* work, void* stream) {
+  KAD_CHECK_ARG(arow && colm && params && emat && ebias && mask, "kad_lcsa_mask_split: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0, "kad_lcsa_mask_split: bad shape");
+  KAD_CHECK_ARG(((uintptr_t)emat) % 16 == 0, "kad_lcsa_mask_split: emat must be 16-byte aligned");
+  KAD_CHECK_ARG(ksplit >= 1 && ksplit <= round_up(c, 32) / 32, "kad_lcsa_mask_split: ksplit %d outside [1, %d]",
+                ksplit, round_up(c, 32) / 32);
+  KAD_CHECK_ARG(ksplit == 1 || work, "kad_lcsa_mask_split: ksplit > 1 needs a work buffer");
+  KAD_CHECK_ARG((int64_t)n * ksplit < 65536, "kad_lcsa_mask_split: N x ksplit too large");
+  return kad::launch_lcsa_mask(arow, colm, params, emat, ebias, mask, n, c, h, w, emat_dtype, ksplit, work,
+                               (hipStream_t)stream);
 }

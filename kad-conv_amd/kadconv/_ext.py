@@ -102,6 +102,10 @@ SIGNATURES = {
     'kad_lcsa_pack': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_vp]),
     'kad_lcsa_prep': (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
     'kad_lcsa_mask': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_lcsa_mask_splits': (c_int, [c_int, c_int, c_int, c_int]),
+    'kad_lcsa_mask_work_elems': (c_i64, [c_int, c_int, c_int, c_int]),
+    'kad_lcsa_mask_split': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int,
+                                    c_vp, c_vp]),
     'kad_se_pool_tiles': (c_int, [c_int, c_int, c_int]),
     'kad_se_pool': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_se_mlp': (c_int, [c_vp, c_int, ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
@@ -412,10 +416,27 @@ def lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, c, h, w):
            'kad_lcsa_prep')
 
 
-def lcsa_mask(arow, colm, params, emat, ebias, mask, n, c, h, w):
-    _need_gpu(arow, colm, params, emat, ebias, mask)
-    _check(load().kad_lcsa_mask(_ptr(arow), _ptr(colm), _ptr(params), _ptr(emat), _ptr(ebias), _ptr(mask), n, c,
-                                h, w, kad_dtype(emat.dtype), _stream()), 'kad_lcsa_mask')
+def lcsa_mask_splits(n, c, h, w):
+    return load().kad_lcsa_mask_splits(n, c, h, w)
+
+
+def lcsa_mask_work_elems(n, h, w, ksplit):
+    return load().kad_lcsa_mask_work_elems(n, h, w, ksplit)
+
+
+def lcsa_mask(arow, colm, params, emat, ebias, mask, n, c, h, w, ksplit=1, work=None):
+    """ksplit > 1: the channel contraction split over blocks, partial logits in `work`
+    (fp32, lcsa_mask_work_elems(n, h, w, ksplit) elements)."""
+    _need_gpu(arow, colm, params, emat, ebias, mask, work)
+    if ksplit == 1:
+        _check(load().kad_lcsa_mask(_ptr(arow), _ptr(colm), _ptr(params), _ptr(emat), _ptr(ebias), _ptr(mask), n,
+                                    c, h, w, kad_dtype(emat.dtype), _stream()), 'kad_lcsa_mask')
+        return
+    if work is None or work.dtype != torch.float32 or work.numel() < lcsa_mask_work_elems(n, h, w, ksplit):
+        raise ValueError('lcsa_mask: ksplit > 1 needs a float32 work buffer of lcsa_mask_work_elems elements')
+    _check(load().kad_lcsa_mask_split(_ptr(arow), _ptr(colm), _ptr(params), _ptr(emat), _ptr(ebias), _ptr(mask), n,
+                                      c, h, w, kad_dtype(emat.dtype), ksplit, _ptr(work), _stream()),
+           'kad_lcsa_mask_split')
 
 
 # ---------------------------------------------------------------------------- SE

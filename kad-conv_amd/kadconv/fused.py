@@ -90,7 +90,7 @@ class DSCPlan:
                 and x.shape[1] == self.cin and self.stride == 1 and self.pad == 1 and x.numel() > 0)
 
     def stages(self, y, n, h, w, out, out_layout, bias=None, post_mul=None, post_add=None, post_scale=None,
-               relu=False, gap=None, tag='', sums=None, se=None):
+               relu=False, gap=None, tag='', sums=None, se=None, mask_split=True):
         """DSC on an NHWC map y [N, h, w, cs] (cin channels) as a list of
         (name, launch) pairs with every buffer allocated up front.  `sums` =
         (rows, nrp, cols, ncp) axial partial sums of y if already computed."""
@@ -110,9 +110,14 @@ class DSCPlan:
             arow = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
             colm = torch.empty(n, w, self.cin, dtype=torch.float32, device=dev)
             mask = torch.empty(n, h, w, 9, dtype=torch.float32, device=dev)
+            # split the mask's channel contraction over blocks when the image has few tiles (standalone
+            # DSC); KADConv's coarse branches run beside the full-resolution chain and stay unsplit
+            ks = _ext.lcsa_mask_splits(n, self.cin, h, w) if mask_split else 1
+            work = torch.empty(_ext.lcsa_mask_work_elems(n, h, w, ks), dtype=torch.float32, device=dev) \
+                if ks > 1 else None
             st.append(('lcsa_prep' + tag, lambda: _ext.lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, self.cin, h, w)))
             st.append(('lcsa_mask' + tag, lambda: _ext.lcsa_mask(arow, colm, self.lcsa, emat, ebias, mask, n,
-                                                                 self.cin, h, w)))
+                                                                 self.cin, h, w, ks, work)))
         b = self.bias if bias is None else bias
         # conv_offset + deformable conv in one kernel: the offsets stay on chip
         st.append(('dsc' + tag, lambda: _ext.dsc_fwd(
@@ -239,7 +244,8 @@ class KADConvPlan:
             att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
             se = (br.w1, br.b1, br.w2, br.b2, att, self._se_counters(dev, i, N))
             ch = br.dsc.stages(ys[i], N, h, w, z, z_layout, post_mul=br.bn_a, post_add=br.bn_b,
-                               post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i], se=se)
+                               post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i], se=se,
+                               mask_split=False)
             if full:
                 ch.append((f'merge{i}', lambda br=br, att=att: _ext.scale_residual(
                     out_v, att, xin, br.c_off, br.c, out_layout)))

@@ -223,6 +223,11 @@ int64_t kad_lcsa_emat_elems(int c);
 int kad_axial_sums(const void *x, float *rows, float *cols, int n, int c, int h, int w, int x_cs, int dtype,
                    void *stream);
 
+/* The same sums of a contiguous NCHW map [N][C][H][W] (x aligned to 4
+ * elements), one block per channel plane of at most 12288 pixels: the
+ * standalone DSC reads its NCHW input here instead of the NHWC copy. */
+int kad_axial_sums_nchw(const void *x, float *rows, float *cols, int n, int c, int h, int w, int dtype, void *stream);
+
 /* E[j][k][c] = w4[j][c] * w3[c][k] (j < 9, else 0) and ebias[16] = b4 + w4 . b3:
  * the 11x1 depthwise conv and the 1x1 projection of LCSA (kad_conv.py:33-35)
  * fused into one matrix.  emat_dtype KAD_F16 (fp16/bf16 runs) or KAD_F32. */

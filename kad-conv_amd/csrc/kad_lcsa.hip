@@ -55,6 +55,62 @@ __global__ __launch_bounds__(256) void axial_sums_kernel(const T* x, float* rows
   }
 }
 
+// ---- axial sums of an NCHW map ---------------------------------------------------------------
+// One block per (image, channel) plane: the plane is read once (8-byte pieces
+// when its size is a multiple of 4 elements) into LDS as fp32 (rows padded by
+// one float), then thread y sums row y and thread x sums column x, each in
+// index order (deterministic).  Plane of at most AX_MAX_PX pixels.
+constexpr int AX_MAX_PX = 12288;
+
+template <typename T>
+__global__ __launch_bounds__(256) void axial_sums_nchw_kernel(const T* x, float* rows, float* cols, int c, int h,
+                                                             int w) {
+  extern __shared__ float pl[];  // [h][w + 1]
+  const int plane = blockIdx.x, n = plane / c, ch = plane - n * c;
+  const int P = h * w, ws = w + 1;
+  const T* xp = x + (int64_t)plane * P;
+  const float inv_w = 1.f / (float)w;
+  if (P % 4 == 0) {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    for (int e = threadIdx.x; e < P / 4; e += 256) {
+      const t4 v = *(const t4*)(xp + 4 * e);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int f = 4 * e + j, y = (int)(((float)f + 0.5f) * inv_w), xx = f - y * w;
+        pl[y * ws + xx] = to_f32(v[j]);
+      }
+    }
+  } else {
+    for (int f = threadIdx.x; f < P; f += 256) {
+      const int y = (int)(((float)f + 0.5f) * inv_w), xx = f - y * w;
+      pl[y * ws + xx] = to_f32(xp[f]);
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < h + w; i += 256) {
+    float a0 = 0.f, a1 = 0.f;
+    if (i < h) {
+      const float* r = pl + i * ws;
+      int j = 0;
+      for (; j + 1 < w; j += 2) {
+        a0 += r[j];
+        a1 += r[j + 1];
+      }
+      if (j < w) a0 += r[j];
+      rows[((int64_t)n * h + i) * c + ch] = a0 + a1;
+    } else {
+      const int xx = i - h;
+      int j = 0;
+      for (; j + 1 < h; j += 2) {
+        a0 += pl[j * ws + xx];
+        a1 += pl[(j + 1) * ws + xx];
+      }
+      if (j < h) a0 += pl[j * ws + xx];
+      cols[((int64_t)n * w + xx) * c + ch] = a0 + a1;
+    }
+  }
+}
+
 // ---- E and b4' from the module weights -----------------------------------------------------------
 // params (fp32): w1[C][11] | b1[C] | bn_a[C] | bn_b[C] | w3[C][11] | b3[C] | w4[9][C] | b4[9]
 template <typename ET>
@@ -350,6 +406,25 @@ extern "C" int kad_axial_sums(const void* x, float* rows, float* cols, int n, in
     default: return fail(KAD_EINVAL, "kad_axial_sums: unknown dtype %d", dtype);
   }
   return check_launch("kad_axial_sums");
+}
+
+extern "C" int kad_axial_sums_nchw(const void* x, float* rows, float* cols, int n, int c, int h, int w, int dtype,
+                                   void* stream) {
+  KAD_CHECK_ARG(x && rows && cols, "kad_axial_sums_nchw: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0, "kad_axial_sums_nchw: bad shape");
+  KAD_CHECK_ARG((int64_t)h * w <= AX_MAX_PX, "kad_axial_sums_nchw: %dx%d plane exceeds %d pixels", h, w, AX_MAX_PX);
+  KAD_CHECK_ARG((int64_t)n * c < (1ll << 31), "kad_axial_sums_nchw: too many planes");
+  KAD_CHECK_ARG(((uintptr_t)x) % (4 * dtype_size(dtype)) == 0, "kad_axial_sums_nchw: x must be aligned to 4 elements");
+  const size_t lds = (size_t)h * (w + 1) * sizeof(float);
+  const dim3 grid(n * c);
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case KAD_F32: allow_lds(axial_sums_nchw_kernel<float>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<float>, grid, dim3(256), lds, st, (const float*)x, rows, cols, c, h, w); break;
+    case KAD_F16: allow_lds(axial_sums_nchw_kernel<half_t>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<half_t>, grid, dim3(256), lds, st, (const half_t*)x, rows, cols, c, h, w); break;
+    case KAD_BF16: allow_lds(axial_sums_nchw_kernel<bf16_t>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<bf16_t>, grid, dim3(256), lds, st, (const bf16_t*)x, rows, cols, c, h, w); break;
+    default: return fail(KAD_EINVAL, "kad_axial_sums_nchw: unknown dtype %d", dtype);
+  }
+  return check_launch("kad_axial_sums_nchw");
 }
 
 extern "C" int kad_lcsa_pack(const float* params, void* emat, float* ebias, int c, int emat_dtype, void* stream) {

@@ -99,6 +99,7 @@ SIGNATURES = {
     'kad_lcsa_params_elems': (c_i64, [c_int]),
     'kad_lcsa_emat_elems': (c_i64, [c_int]),
     'kad_axial_sums': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_axial_sums_nchw': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_lcsa_pack': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_vp]),
     'kad_lcsa_prep': (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
     'kad_lcsa_mask': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
@@ -408,6 +409,19 @@ def axial_sums(x_nhwc, c, rows, cols):
     N, H, W, cs = x_nhwc.shape
     _check(load().kad_axial_sums(_ptr(x_nhwc), _ptr(rows), _ptr(cols), N, c, H, W, cs, kad_dtype(x_nhwc.dtype),
                                  _stream()), 'kad_axial_sums')
+
+
+AXIAL_NCHW_MAX_PX = 12288
+
+
+def axial_sums_nchw(x, rows, cols):
+    """Row / column sums of a contiguous NCHW map (planes of at most AXIAL_NCHW_MAX_PX pixels)."""
+    _need_gpu(x, rows, cols)
+    N, C, H, W = x.shape
+    if not x.is_contiguous():
+        raise ValueError('axial_sums_nchw: x must be contiguous NCHW')
+    _check(load().kad_axial_sums_nchw(_ptr(x), _ptr(rows), _ptr(cols), N, C, H, W, kad_dtype(x.dtype), _stream()),
+           'kad_axial_sums_nchw')
 
 
 def lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, c, h, w):

@@ -90,7 +90,7 @@ class DSCPlan:
                 and x.shape[1] == self.cin and self.stride == 1 and self.pad == 1 and x.numel() > 0)
 
     def stages(self, y, n, h, w, out, out_layout, bias=None, post_mul=None, post_add=None, post_scale=None,
-               relu=False, gap=None, tag='', sums=None, se=None, mask_split=True):
+               relu=False, gap=None, tag='', sums=None, se=None, mask_split=True, x_nchw=None):
         """DSC on an NHWC map y [N, h, w, cs] (cin channels) as a list of
         (name, launch) pairs with every buffer allocated up front.  `sums` =
         (rows, nrp, cols, ncp) axial partial sums of y if already computed."""
@@ -104,7 +104,11 @@ class DSCPlan:
                 rows = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
                 cols = torch.empty(n, w, self.cin, dtype=torch.float32, device=dev)
                 nrp = ncp = 1
-                st.append(('axial_sums' + tag, lambda: _ext.axial_sums(y, self.cin, rows, cols)))
+                if x_nchw is not None and h * w <= _ext.AXIAL_NCHW_MAX_PX and x_nchw.data_ptr() % 16 == 0:
+                    # the NCHW input itself: contiguous planes, one block each
+                    st.append(('axial_sums' + tag, lambda: _ext.axial_sums_nchw(x_nchw, rows, cols)))
+                else:
+                    st.append(('axial_sums' + tag, lambda: _ext.axial_sums(y, self.cin, rows, cols)))
             else:
                 rows, nrp, cols, ncp = sums
             arow = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
@@ -140,7 +144,7 @@ class DSCPlan:
             self.run(y, n, h, w, out.permute(0, 2, 3, 1), _ext.KAD_NHWC)
             return out
         out = torch.empty(n, self.cout, h, w, dtype=x.dtype, device=x.device)
-        return self.run(y, n, h, w, out, _ext.KAD_NCHW)
+        return self.run(y, n, h, w, out, _ext.KAD_NCHW, x_nchw=x if x.is_contiguous() else None)
 
 
 class _Branch:

@@ -517,8 +517,11 @@ __device__ __forceinline__ void offset_conv16(floatx4 (&oacc)[DCN_WM][2], __amdg
     // one descriptor per pass (a buffer descriptor must be wave-uniform)
     for (int fb = 0, wb = 0; fb < np || wb < nw; fb += NTF * DCN_THREADS, wb += NTW * DCN_THREADS) {
       frag vf[NTF], vw[NTW];
+      // pieces past np / nw are skipped by block-uniform branches (no address work, no load)
 #pragma unroll
       for (int t = 0; t < NTF; ++t) {  // footprint piece: pixel q, 8 channels r of the group
+        vf[t] = zero8<T>();
+        if (fb + t * DCN_THREADS >= np) continue;
         const int e = fb + tid + t * DCN_THREADS;
         uint32_t o = DCN_OOB;
         if (e < np) {
@@ -532,6 +535,8 @@ __device__ __forceinline__ void offset_conv16(floatx4 (&oacc)[DCN_WM][2], __amdg
       }
 #pragma unroll
       for (int t = 0; t < NTW; ++t) {  // filter piece: tap k, filter col, 8 channels r
+        vw[t] = zero8<T>();
+        if (wb + t * DCN_THREADS >= nw) continue;
         const int f = wb + tid + t * DCN_THREADS;
         uint32_t o = DCN_OOB;
         if (f < nw) {

@@ -721,6 +721,40 @@ __global__ __launch_bounds__(256) void to_nhwc_kernel(const T* x, T* out, int c,
   }
 }
 
+// 16-bit, planes of a multiple of 8 pixels, 16-byte aligned, cs % 8 == 0: 8-pixel
+// (16-byte) loads along each plane, 8-channel (16-byte) stores along each
+// pixel.  LDS rows of 72 elements (144 bytes): the 16-byte row stores of 8
+// lanes hit distinct banks.
+template <typename T>
+__global__ __launch_bounds__(256) void to_nhwc_v8_kernel(const T* x, T* out, int c, int P, int cs) {
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  __shared__ __align__(16) T tile[64][72];
+  const int n = blockIdx.z;
+  const int p0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
+  const T* xb = x + (int64_t)n * c * P;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int v = tid & 7, cl = (tid >> 3) + 32 * u;
+    const int p = p0 + 8 * v, ch = c0 + cl;
+    v8 val = {};
+    if (p < P && ch < c) val = *(const v8*)(xb + (int64_t)ch * P + p);  // P % 8 == 0: the piece is whole
+    *(v8*)&tile[cl][8 * v] = val;
+  }
+  __syncthreads();
+  T* ob = out + (int64_t)n * P * cs;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int pl = tid & 63, g = (tid >> 6) + 4 * u;
+    const int p = p0 + pl, ch = c0 + 8 * g;
+    if (p >= P || ch >= cs) continue;
+    v8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = tile[8 * g + j][pl];
+    *(v8*)(ob + (int64_t)p * cs + ch) = o;
+  }
+}
+
 static int grid_for(int64_t total) {
   int64_t b = (total + 255) / 256;
   return (int)(b < 65536 ? (b > 0 ? b : 1) : 65536);
@@ -1005,6 +1039,15 @@ extern "C" int kad_to_nhwc(const void* x, void* out, int n, int c, int h, int w,
   const int P = h * w;
   dim3 grid(ceil_div(P, 64), ceil_div(out_cs, 64), n);
   hipStream_t st = (hipStream_t)stream;
+  if (dtype != KAD_F32 && P % 8 == 0 && out_cs % 8 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0) {
+    if (dtype == KAD_F16)
+      hipLaunchKernelGGL(to_nhwc_v8_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, (half_t*)out, c, P, out_cs);
+    else if (dtype == KAD_BF16)
+      hipLaunchKernelGGL(to_nhwc_v8_kernel<bf16_t>, grid, dim3(256), 0, st, (const bf16_t*)x, (bf16_t*)out, c, P, out_cs);
+    else
+      return fail(KAD_EINVAL, "kad_to_nhwc: unknown dtype %d", dtype);
+    return check_launch("kad_to_nhwc");
+  }
   switch (dtype) {
     case KAD_F32: hipLaunchKernelGGL(to_nhwc_kernel<float>, grid, dim3(256), 0, st, (const float*)x, (float*)out, c, P, out_cs); break;
     case KAD_F16: hipLaunchKernelGGL(to_nhwc_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, (half_t*)out, c, P, out_cs); break;

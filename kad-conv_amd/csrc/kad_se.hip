@@ -287,6 +287,79 @@ __global__ __launch_bounds__(NT) void se_mlp_kernel(const float* partial, int ti
   }
 }
 
+// Wide C (C <= 1024, C % 64 == 0, hid <= 64, hid % 4 == 0, 16-byte aligned
+// weights): every weight load of a layer in one batch.  1024 threads:
+//  - thread (j = tid / 16, part = tid % 16) requests its W1 row slice
+//    W1[j][64 i + 4 part .. + 4] (C / 64 16-byte pieces) first, so the W1
+//    round trip overlaps the channel means;
+//  - g[c] = inv_count * sum over tiles (thread c, tiles in index order);
+//  - h[j] = relu(b1[j] + W1[j] . g): 16 lanes per unit, shuffle-reduced;
+//  - thread c requests its W2 row (hid / 4 pieces) right after its W1 products,
+//    then att[c] = sigmoid(b2[c] + W2[c] . h).
+constexpr int SE_WIDE = 1024;
+
+__global__ __launch_bounds__(SE_WIDE) void se_mlp_wide_kernel(const float* partial, int tiles, float inv_count,
+                                                              const float* w1, const float* b1, const float* w2,
+                                                              const float* b2, float* att, int c, int hid) {
+  __shared__ __align__(16) float g[SE_WIDE];
+  __shared__ __align__(16) float hb[64];
+  const int n = blockIdx.x, tid = threadIdx.x;
+  const int j = tid >> 4, part = tid & 15, np = c / 64;
+  floatx4 wv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    wv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (i < np && j < hid) wv[i] = *(const floatx4*)(w1 + (int64_t)j * c + 64 * i + 4 * part);
+  }
+  if (tid < c) {
+    const float* pn = partial + (int64_t)n * tiles * c + tid;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int t = 0;
+    for (; t + 3 < tiles; t += 4) {
+      a0 += pn[(int64_t)t * c];
+      a1 += pn[(int64_t)(t + 1) * c];
+      a2 += pn[(int64_t)(t + 2) * c];
+      a3 += pn[(int64_t)(t + 3) * c];
+    }
+    for (; t < tiles; ++t) a0 += pn[(int64_t)t * c];
+    g[tid] = ((a0 + a1) + (a2 + a3)) * inv_count;
+  }
+  __syncthreads();
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if (i < np) {
+      const floatx4 gv = *(const floatx4*)&g[64 * i + 4 * part];
+      acc += (wv[i][0] * gv[0] + wv[i][1] * gv[1]) + (wv[i][2] * gv[2] + wv[i][3] * gv[3]);
+    }
+  }
+  // W2 row of channel tid (the W1 registers are free now)
+  const int nq = hid / 4;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    wv[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (i < nq && tid < c) wv[i] = *(const floatx4*)(w2 + (int64_t)tid * hid + 4 * i);
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  acc += __shfl_xor(acc, 8);
+  if (part == 0 && j < hid) hb[j] = fmaxf(acc + (b1 ? b1[j] : 0.f), 0.f);
+  __syncthreads();
+  if (tid < c) {
+    float o0 = b2 ? b2[tid] : 0.f, o1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i < nq) {
+        const floatx4 hv = *(const floatx4*)&hb[4 * i];
+        o0 += wv[i][0] * hv[0] + wv[i][1] * hv[1];
+        o1 += wv[i][2] * hv[2] + wv[i][3] * hv[3];
+      }
+    }
+    att[(int64_t)n * c + tid] = sigmoidf_(o0 + o1);
+  }
+}
+
 // ---- channel scale: out[n, c, :] = x[n, c, :] * att[n, c] (NCHW) or per pixel (NHWC) -------
 // NCHW over the flat tensor in 16-byte pieces (hw >= 8): the plane of a piece's
 // first element gives its scale; a piece straddles at most one plane boundary.
@@ -821,6 +894,11 @@ extern "C" int kad_se_mlp(const float* partial, int tiles, float inv_count, cons
     allow_lds(se_mlp_staged_kernel, lds_staged);
     hipLaunchKernelGGL(se_mlp_staged_kernel, dim3(n), dim3(SE_ST), lds_staged, (hipStream_t)stream, partial, tiles,
                        inv_count, w1, b1, w2, b2, att, c, hid);
+    return check_launch("kad_se_mlp");
+  }
+  if (c <= SE_WIDE && c % 64 == 0 && hid <= 64 && hid % 4 == 0 && ((uintptr_t)w1 | (uintptr_t)w2) % 16 == 0) {
+    hipLaunchKernelGGL(se_mlp_wide_kernel, dim3(n), dim3(SE_WIDE), 0, (hipStream_t)stream, partial, tiles, inv_count,
+                       w1, b1, w2, b2, att, c, hid);
     return check_launch("kad_se_mlp");
   }
   const int nt = c <= 256 ? 256 : 1024;

@@ -213,6 +213,7 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
   __shared__ __align__(16) float s_a[LM_UR][LM_SCS];     // row means, rows h0 - 5 .. h0 + 20
   __shared__ float s_w1[LM_SC * BAND], s_b1[LM_SC], s_bna[LM_SC], s_bnb[LM_SC];
   __shared__ __align__(16) float s_alpha[LM_TW][LM_SCS], s_beta[LM_TW][LM_SCS];
+  __shared__ float s_eb[16];  // logit biases, staged with the first group
   const float* w1 = params;
   const float* b1 = params + 11 * c;
   const float* bna = params + 12 * c;
@@ -271,6 +272,7 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
 #define LM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
   LM_LOAD_GROUP((kc0 / CPG) * LM_SC);
   LM_LOAD_E(kc0);
+  if (tid < 16) s_eb[tid] = tid < 9 ? ebias[tid] : 0.f;  // read in the epilogue, after many barriers
   for (int kc = kc0; kc < kc1; ++kc) {
     const int g = kc / CPG, c0 = (kc - g * CPG) * 32, cs = g * LM_SC;
     if (c0 == 0 || kc == kc0) {  // first chunk of a group (or of the split): stage it, request the next one
@@ -296,33 +298,42 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
       }
       LM_LDS_BARRIER();
       if ((g + 1) * CPG < kc1) LM_LOAD_GROUP(cs + LM_SC);
-      // strip-conv coefficients of the 16 columns (separable 1x11 conv + folded BN)
+      // strip-conv coefficients of the 16 columns (separable 1x11 conv + folded BN), branch-free:
+      // the staged column means are 0 outside the image, so only S needs the in-image mask, and
+      // every LDS read of a task is independent (a task is not a chain of dependent reads)
       for (int e = tid; e < LM_TW * LM_SC; e += LM_THREADS) {
         const int col = e / LM_SC, ch = e - col * LM_SC, gx = w0 + col;
-        float S = 0.f, B = 0.f;
+        float S0 = 0.f, S1 = 0.f, B0 = 0.f, B1 = 0.f;
 #pragma unroll
         for (int k = 0; k < BAND; ++k) {
           const int xx = gx + k - HALF_BAND;
-          const float wk = s_w1[ch * BAND + k];
-          if (xx >= 0 && xx < w) {
-            S += wk;
-            B += wk * s_col[col + k][ch];
+          const float wk = s_w1[ch * BAND + k], cm = s_col[col + k][ch];
+          const float m = (xx >= 0 && xx < w) ? wk : 0.f;
+          if (k & 1) {
+            S1 += m;
+            B1 += wk * cm;
+          } else {
+            S0 += m;
+            B0 += wk * cm;
           }
         }
+        const float S = S0 + S1, B = B0 + B1;
         const bool ok = gx < w && ch < nsc && cs + ch < c;
         s_alpha[col][ch] = ok ? s_bna[ch] * S : 0.f;
         s_beta[col][ch] = ok ? s_bna[ch] * (B + s_b1[ch]) + s_bnb[ch] : 0.f;
       }
     }
     LM_LDS_BARRIER();  // alpha / beta ready; the previous chunk's MFMAs are done with us
-    // u = relu(alpha * a + beta), 8 channels per task, one 16-byte LDS store
-    for (int e = tid; e < LM_UR * LM_TW * 4; e += LM_THREADS) {
-      const int gq = e & 3, q = e >> 2, col = q & (LM_TW - 1), r = q >> 4;
+    // u = relu(alpha * a + beta): thread (column, 8-channel group) fixed, rows r0, r0 + 4, ...;
+    // its alpha / beta are read once per chunk, one 16-byte LDS store per row
+    {
+    const int gq = tid & 3, col = (tid >> 2) & (LM_TW - 1), r0 = tid >> 6;
+    const int ch = c0 + gq * 8;
+    const floatx4 al0 = *(const floatx4*)&s_alpha[col][ch], al1 = *(const floatx4*)&s_alpha[col][ch + 4];
+    const floatx4 be0 = *(const floatx4*)&s_beta[col][ch], be1 = *(const floatx4*)&s_beta[col][ch + 4];
+    for (int r = r0; r < LM_UR; r += LM_THREADS / (4 * LM_TW)) {
       const int gy = h0 - HALF_BAND + r;
       const bool rv = gy >= 0 && gy < h;
-      const int ch = c0 + gq * 8;
-      const floatx4 al0 = *(const floatx4*)&s_alpha[col][ch], al1 = *(const floatx4*)&s_alpha[col][ch + 4];
-      const floatx4 be0 = *(const floatx4*)&s_beta[col][ch], be1 = *(const floatx4*)&s_beta[col][ch + 4];
       const floatx4 a0 = *(const floatx4*)&s_a[r][ch], a1 = *(const floatx4*)&s_a[r][ch + 4];
       ET* dst = us + (r * LM_TW + col) * LDU + gq * 8;
       if constexpr (sizeof(ET) == 2) {
@@ -344,6 +355,7 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
         ((floatx4*)dst)[1] = v1;
       }
     }
+    }
     LM_LDS_BARRIER();
 #pragma unroll
     for (int k = 0; k < BAND; ++k) {
@@ -358,6 +370,9 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
 #undef LM_LOAD_GROUP
 #undef LM_LOAD_E
 #undef LM_LDS_BARRIER
+  float eb[4];  // this lane's logit biases (logits 4 grp .. 4 grp + 3)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) eb[i] = s_eb[grp * 4 + i];
   // acc[f][i]: logit j = 4 * grp + i of pixel (row 4 * wave + f, col l16)
 #pragma unroll
   for (int f = 0; f < 4; ++f) {
@@ -368,7 +383,7 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
       const int j = grp * 4 + i;
       if (j >= 9) continue;
       if (ksplit == 1)
-        mask[(((int64_t)n * h + gy) * w + gx) * 9 + j] = sigmoidf_(acc[f][i] + ebias[j]);
+        mask[(((int64_t)n * h + gy) * w + gx) * 9 + j] = sigmoidf_(acc[f][i] + eb[i]);
       else  // raw logits of this split; lcsa_mask_reduce_kernel adds the splits up
         part[((((int64_t)sp * gridDim.z / ksplit + n) * h + gy) * w + gx) * 9 + j] = acc[f][i];
     }

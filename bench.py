@@ -131,11 +131,11 @@ def cpu_baseline(shape, runs=5, warmup=2):
                       f'(os.cpu_count={os.cpu_count()}, affinity={threads}, cpu="{cpu_model}")'}
 
 
-def per_op(steps, warmup):
-    """The other BASELINE configs, graph-timed (us per call) with their floors."""
+def per_op_workloads():
+    """The other BASELINE configs as (name, launch, floor_us) with seeded inputs and weights."""
     import kadconv
     from oracle import kadconv_oracle as O
-    res = {}
+    out = []
     g = torch.Generator().manual_seed(0)
     dt = torch.float16
     # config 2: DSC(C, C) at the neck scales
@@ -145,19 +145,15 @@ def per_op(steps, warmup):
         d = d.to('cuda', dt).eval()
         kadconv.enable_fast_inference(d)
         x = torch.randn(8, C, H, H, generator=g).to('cuda', dt)
-        us, _ = time_graph(lambda: d(x), steps, warmup)
         fl = 8 * H * H * (2 * 9 * C * C + 2 * 9 * 18 * C + 2 * 9 * C + 44 * C)
         by = 2 * 8 * C * H * H * 2 + 2 * (9 * C * C + 162 * C + 9 * C)
-        floor = max(fl / PEAK_MFMA_F16, by / PEAK_HBM) * 1e6
-        res[f'dsc_{C}x{H}'] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+        out.append((f'dsc_{C}x{H}', lambda d=d, x=x: d(x), max(fl / PEAK_MFMA_F16, by / PEAK_HBM) * 1e6))
     # config 3: KADDown [8,256,100,100] -> [8,512,50,50]
     m = kadconv.KADDown(256, 512)
     m.load_state_dict(O.make_kaddown_state(256, 512))
     m = m.to('cuda', dt).eval()
     x = torch.randn(8, 256, 100, 100, generator=g).to('cuda', dt)
-    us, _ = time_graph(lambda: m(x), steps, warmup)
-    floor = max(6.86e9 / PEAK_MFMA_F16, 61.44e6 / PEAK_HBM) * 1e6
-    res['kaddown_256to512_100'] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+    out.append(('kaddown_256to512_100', lambda m=m, x=x: m(x), max(6.86e9 / PEAK_MFMA_F16, 61.44e6 / PEAK_HBM) * 1e6))
     # config 4a: 1x1 conv + SiLU [16,512,50,50]
     m = kadconv.Conv1x1SiLU(512, 512)
     with torch.no_grad():
@@ -165,15 +161,20 @@ def per_op(steps, warmup):
         m.conv.bias.normal_(0, 0.02)
     m = m.to('cuda', dt).eval()
     x = torch.randn(16, 512, 50, 50, generator=g).to('cuda', dt)
-    us, _ = time_graph(lambda: m(x), steps, warmup)
-    floor = max(20.97e9 / PEAK_MFMA_F16, 82.44e6 / PEAK_HBM) * 1e6
-    res['conv1x1_silu_512_50'] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+    out.append(('conv1x1_silu_512_50', lambda m=m, x=x: m(x), max(20.97e9 / PEAK_MFMA_F16, 82.44e6 / PEAK_HBM) * 1e6))
     # config 4b: SE [16,1024,25,25], r=16
     m = kadconv.SqueezeExcitation(1024, reduction=16).to('cuda', dt).eval()
     x = torch.randn(16, 1024, 25, 25, generator=g).to('cuda', dt)
-    us, _ = time_graph(lambda: m(x), steps, warmup)
-    floor = 40.96e6 / PEAK_HBM * 1e6
-    res['se_1024_25'] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+    out.append(('se_1024_25', lambda m=m, x=x: m(x), 40.96e6 / PEAK_HBM * 1e6))
+    return out
+
+
+def per_op(steps, warmup):
+    """The other BASELINE configs, graph-timed (us per call) with their floors."""
+    res = {}
+    for name, fn, floor in per_op_workloads():
+        us, _ = time_graph(fn, steps, warmup)
+        res[name] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
     return res
 
 
@@ -202,6 +203,32 @@ def traffic_probe():
         torch.cuda.synchronize()
         for _ in range(5):
             dsc0()
+        torch.cuda.synchronize()
+    print(json.dumps({'probe': 'done', 'copy_bytes': PROBE_COPY_BYTES}), flush=True)
+
+
+def counters_probe():
+    """A short program for the per-kernel counter table (rocprofv3 --pmc passes and
+    a kernel trace): every stage of the metric's forward, eagerly, then each per-op
+    workload, 3 times each, then the 64 MiB copy that scales FETCH_SIZE / WRITE_SIZE."""
+    import kadconv
+    m = build_kadconv(256, torch.float16)
+    kadconv.enable_fast_inference(m)
+    x = torch.randn(8, 256, 100, 100, generator=torch.Generator().manual_seed(0)).to('cuda', torch.float16)
+    with torch.no_grad():
+        st, _ = m._kad_plan.stages(x)
+        for _ in range(3):
+            for _, fn in st:
+                fn()
+                torch.cuda.synchronize()
+        for _, fn, _ in per_op_workloads():
+            for _ in range(3):
+                fn()
+                torch.cuda.synchronize()
+        a = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device='cuda')
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
         torch.cuda.synchronize()
     print(json.dumps({'probe': 'done', 'copy_bytes': PROBE_COPY_BYTES}), flush=True)
 
@@ -243,6 +270,59 @@ def traffic_from(fetch_csv, write_csv):
     print(json.dumps(out))
 
 
+COUNTERS_FILE = os.path.join(ROOT, 'profiles', 'kernel_counters.md')
+
+
+def counters_from(trace_csv, fetch_csv, write_csv, sq_csv):
+    """Per-kernel table from one kernel trace and three --pmc runs of counters_probe().
+    HBM bytes: FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled by their reading for
+    the 64 MiB copy (true: 64 MiB read + 64 MiB written).  MFMA busy: summed
+    SQ_VALU_MFMA_BUSY_CYCLES over all 1024 SIMDs' cycles, the latter from
+    GRBM_GUI_ACTIVE (which reads one count per XCD, 8 per dispatch-cycle)."""
+    import collections
+    import csv
+    import statistics
+
+    def pmc(path):
+        d = collections.defaultdict(lambda: collections.defaultdict(list))
+        for r in csv.DictReader(open(path)):
+            d[(r['Kernel_Name'], int(r['Grid_Size']))][r['Counter_Name']].append(float(r['Counter_Value']))
+        return d
+    f, w, sq = pmc(fetch_csv), pmc(write_csv), pmc(sq_csv)
+    dur = collections.defaultdict(list)
+    for r in csv.DictReader(open(trace_csv)):
+        g = int(r['Grid_Size_X']) * int(r['Grid_Size_Y']) * int(r['Grid_Size_Z'])
+        dur[(r['Kernel_Name'], g)].append((int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3)
+    copy = [k for k in f if 'copyBuffer' in k[0]]
+    ck = max(copy, key=lambda k: k[1])
+    sf = PROBE_COPY_BYTES / (statistics.median(f[ck]['FETCH_SIZE']) * 1024.0)
+    sw = PROBE_COPY_BYTES / (statistics.median(w[ck]['WRITE_SIZE']) * 1024.0)
+    rows = []
+    for k in f:
+        name, grid = k
+        if not name.startswith(('_ZN3kad', 'kad::', 'void kad::')) or 'pack_kernel' in name or k not in dur:
+            continue
+        us = statistics.median(dur[k])
+        rd = statistics.median(f[k]['FETCH_SIZE']) * 1024.0 * sf
+        wr = statistics.median(w[k]['WRITE_SIZE']) * 1024.0 * sw if k in w else float('nan')
+        mf = statistics.median(sq[k]['SQ_VALU_MFMA_BUSY_CYCLES']) if k in sq else 0.0
+        gr = statistics.median(sq[k]['GRBM_GUI_ACTIVE']) if k in sq else float('nan')
+        busy = mf / (gr / 8.0 * 1024.0) if gr == gr and gr > 0 else float('nan')
+        gbs = (rd + wr) / (us * 1e-6) / 1e9
+        rows.append((us * len(dur[k]), name, grid, len(dur[k]), us, rd / 1e6, wr / 1e6, gbs, gbs / (PEAK_HBM / 1e9), busy))
+    rows.sort(key=lambda r: -r[0])
+    lines = ['| kernel | work-items | calls | median us | read MB | write MB | GB/s | of 8 TB/s | MFMA busy |',
+             '|---|---|---|---|---|---|---|---|---|']
+    for _, name, grid, n, us, rd, wr, gbs, frac, busy in rows:
+        short = name if len(name) < 70 else name[:67] + '...'
+        lines.append(f'| `{short}` | {grid} | {n} | {us:.2f} | {rd:.2f} | {wr:.2f} | {gbs:.0f} | {100 * frac:.1f}% | '
+                     f'{100 * busy:.1f}% |')
+    table = '\n'.join(lines)
+    print(table)
+    print(json.dumps({'fetch_scale': sf, 'write_scale': sw}))
+    return table, sf, sw
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -253,11 +333,21 @@ def main():
     ap.add_argument('--per-op-only', action='store_true',
                     help='print only the per-op table (a short program for rocprofv3 kernel traces)')
     ap.add_argument('--traffic-probe', action='store_true', help='short program for the rocprofv3 --pmc passes')
+    ap.add_argument('--counters-probe', action='store_true',
+                    help='short program for the per-kernel counter table (every forward stage and per-op workload)')
+    ap.add_argument('--counters-from', nargs=4, metavar=('TRACE_CSV', 'FETCH_CSV', 'WRITE_CSV', 'SQ_CSV'),
+                    help='print the per-kernel counter table from a kernel trace and three --pmc CSVs')
     ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
                     help='compute profiles/dsc0_traffic.json from the two --pmc counter CSVs')
     args = ap.parse_args()
     if args.traffic_from:
         traffic_from(*args.traffic_from)
+        return
+    if args.counters_from:
+        counters_from(*args.counters_from)
+        return
+    if args.counters_probe:
+        counters_probe()
         return
     if args.traffic_probe:
         traffic_probe()

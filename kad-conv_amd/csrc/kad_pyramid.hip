@@ -209,7 +209,7 @@ template <int HB> struct PyW { static constexpr int NCH = 6 * HB, BYTES = NCH * 
 // register-staged loop with one step of prefetch.
 template <typename T, int HB>
 __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(kad_pyramid_args a, int cin_pad,
-                                                                                 int dma) {
+                                                                                 int dma, int ncy, int grid8) {
   constexpr int LDA = PyLds<T>::lda;
   constexpr int NB = 32 * HB;              // output columns per branch per block
   constexpr int BTASKS = 3 * NB * 4;       // 16-byte weight pieces per K step (3 branches)
@@ -230,7 +230,11 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
   // epilogue: column partials, [32][NB] fp32 (branch 2: [2][HB][16][16])
   float* colred = H16 ? (float*)pw2 : (float*)(smem + 64 * OBT * sizeof(T));
 
-  const int tx = blockIdx.x, ty = blockIdx.y % a.nty, cy = blockIdx.y / a.nty, n = blockIdx.z;
+  // XCD-aware order: block b runs on XCD b % 8, which takes the contiguous run of tiles
+  // [(b % 8) grid8 / 8, ...): the tiles of a row band (which share input lines) stay in one L2.
+  const int bq = (int)(blockIdx.x & 7) * (grid8 >> 3) + (int)(blockIdx.x >> 3);
+  if (bq >= a.ntx * a.nty * ncy * a.n) return;  // whole block, before any barrier
+  const int tx = bq % a.ntx, r1 = bq / a.ntx, ty = r1 % a.nty, r2 = r1 / a.nty, cy = r2 % ncy, n = r2 / ncy;
   const int r0 = ty * PY_TR, c0 = tx * PY_TC;
   const int col0 = cy * NB;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -670,12 +674,14 @@ static size_t pyramid_lds(int dma) {
 
 template <typename T, int HB>
 static void launch_pyramid(const kad_pyramid_args& a, int cin_pad, int maxcols, hipStream_t st) {
-  dim3 grid(a.ntx, a.nty * ceil_div(maxcols, 32 * HB), a.n);
+  const int ncy = ceil_div(maxcols, 32 * HB);
+  const int grid8 = round_up(a.ntx * a.nty * ncy * a.n, 8);
+  dim3 grid(grid8);
   const int dma = sizeof(T) == 2 && a.in_layout == KAD_NCHW && a.w % 4 == 0 &&
                   (int64_t)a.n * a.cin * a.h * a.w * 2 < (1ll << 31) && (uint32_t)(32 * a.h * a.w * 2) > 0;
   const size_t lds = pyramid_lds<T, HB>(dma);
   allow_lds(pyramid_kernel<T, HB>, lds);
-  hipLaunchKernelGGL((pyramid_kernel<T, HB>), grid, dim3(PY_THREADS), lds, st, a, cin_pad, dma);
+  hipLaunchKernelGGL((pyramid_kernel<T, HB>), grid, dim3(PY_THREADS), lds, st, a, cin_pad, dma, ncy, grid8);
 }
 
 template <typename T>
@@ -708,6 +714,8 @@ extern "C" int kad_pyramid_proj(const kad_pyramid_args* a, void* stream) {
                 "kad_pyramid_proj: bad shape");
   KAD_CHECK_ARG(a->in_layout == KAD_NCHW || (a->in_layout == KAD_NHWC && a->x_cs >= a->cin),
                 "kad_pyramid_proj: bad input layout");
+  KAD_CHECK_ARG((int64_t)a->n * ceil_div(a->w, PY_TC) * ceil_div(a->h, PY_TR) * 8 < (1ll << 31),
+                "kad_pyramid_proj: too many tiles");
   KAD_CHECK_ARG(a->ntx == ceil_div(a->w, PY_TC) && a->nty == ceil_div(a->h, PY_TR),
                 "kad_pyramid_proj: ntx/nty must come from kad_pyramid_tiles");
   int maxcols = 0;

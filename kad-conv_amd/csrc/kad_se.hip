@@ -798,12 +798,18 @@ __global__ __launch_bounds__(256) void to_nhwc_kernel(const T* x, T* out, int c,
 // (16-byte) loads along each plane, 8-channel (16-byte) stores along each
 // pixel.  LDS rows of 72 elements (144 bytes): the 16-byte row stores of 8
 // lanes hit distinct banks.
+// Flat XCD-aware grid: block b runs on XCD b % 8, which takes a contiguous run of
+// (image, channel tile, pixel tile) tiles, so the 128-byte lines that two neighbouring
+// pixel tiles share (planes need not be line-aligned) are fetched into one L2.
 template <typename T>
-__global__ __launch_bounds__(256) void to_nhwc_v8_kernel(const T* x, T* out, int c, int P, int cs) {
+__global__ __launch_bounds__(256) void to_nhwc_v8_kernel(const T* x, T* out, int c, int P, int cs, int npt, int nct,
+                                                         int total, int grid8) {
   typedef T v8 __attribute__((ext_vector_type(8)));
   __shared__ __align__(16) T tile[64][72];
-  const int n = blockIdx.z;
-  const int p0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
+  const int bq = (int)(blockIdx.x & 7) * (grid8 >> 3) + (int)(blockIdx.x >> 3);
+  if (bq >= total) return;  // whole block, before the barrier
+  const int pt = bq % npt, r = bq / npt, ct = r % nct, n = r / nct;
+  const int p0 = pt * 64, c0 = ct * 64;
   const T* xb = x + (int64_t)n * c * P;
   const int tid = threadIdx.x;
 #pragma unroll
@@ -1117,11 +1123,16 @@ extern "C" int kad_to_nhwc(const void* x, void* out, int n, int c, int h, int w,
   const int P = h * w;
   dim3 grid(ceil_div(P, 64), ceil_div(out_cs, 64), n);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype != KAD_F32 && P % 8 == 0 && out_cs % 8 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0) {
+  const int64_t tiles = (int64_t)ceil_div(P, 64) * ceil_div(out_cs, 64) * n;
+  if (dtype != KAD_F32 && P % 8 == 0 && out_cs % 8 == 0 && (uintptr_t)x % 16 == 0 && (uintptr_t)out % 16 == 0 &&
+      tiles * 8 < (1ll << 31)) {
+    const int npt = ceil_div(P, 64), nct = ceil_div(out_cs, 64), total = (int)tiles, grid8 = round_up(total, 8);
     if (dtype == KAD_F16)
-      hipLaunchKernelGGL(to_nhwc_v8_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, (half_t*)out, c, P, out_cs);
+      hipLaunchKernelGGL(to_nhwc_v8_kernel<half_t>, dim3(grid8), dim3(256), 0, st, (const half_t*)x, (half_t*)out, c,
+                         P, out_cs, npt, nct, total, grid8);
     else if (dtype == KAD_BF16)
-      hipLaunchKernelGGL(to_nhwc_v8_kernel<bf16_t>, grid, dim3(256), 0, st, (const bf16_t*)x, (bf16_t*)out, c, P, out_cs);
+      hipLaunchKernelGGL(to_nhwc_v8_kernel<bf16_t>, dim3(grid8), dim3(256), 0, st, (const bf16_t*)x, (bf16_t*)out, c,
+                         P, out_cs, npt, nct, total, grid8);
     else
       return fail(KAD_EINVAL, "kad_to_nhwc: unknown dtype %d", dtype);
     return check_launch("kad_to_nhwc");

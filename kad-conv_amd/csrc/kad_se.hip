@@ -657,12 +657,17 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(kad_merge_args a) {
 constexpr int MB_E = 1024;
 
 template <typename T>
-__global__ __launch_bounds__(256) void merge_band_kernel(kad_merge_args a, int srows_cap, int bw_cap) {
+__global__ __launch_bounds__(256) void merge_band_kernel(kad_merge_args a, int srows_cap, int bw_cap, int nruns,
+                                                         int ngroups, int grid8) {
   extern __shared__ float zsm[];  // [8][srows_cap][bw_cap]
   __shared__ float s_att[8], s_gate[8];
   typedef T v8 __attribute__((ext_vector_type(8)));
-  const int run = blockIdx.x, n = blockIdx.z, tid = threadIdx.x;
-  int b = 0, k = blockIdx.y;
+  // XCD-aware order: XCD b % 8 takes a contiguous run of (image, group, run) tiles, so the
+  // runs of one plane (which share boundary lines and source rows) stay in one L2
+  const int bq = (int)(blockIdx.x & 7) * (grid8 >> 3) + (int)(blockIdx.x >> 3);
+  if (bq >= nruns * ngroups * a.n) return;  // whole block, before the barrier
+  const int run = bq % nruns, rq = bq / nruns, n = rq / ngroups, tid = threadIdx.x;
+  int b = 0, k = rq % ngroups;
 #pragma unroll
   for (int i = 0; i < KAD_MAX_BRANCHES; ++i) {
     if (i == b && i < a.nbranch - 1) {
@@ -1080,12 +1085,14 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
            ((uintptr_t)a->br_z[b] % (8 * tsz)) == 0;
   }
   const size_t band_lds = (size_t)8 * srows_cap * maxbw * sizeof(float);
-  if (band && band_lds <= 64 * 1024) {
-    dim3 grid((unsigned)ceil_div(P, (int64_t)MB_E), ngroups, a->n);
+  const int nruns = ceil_div((int)P, MB_E);
+  if (band && band_lds <= 64 * 1024 && (int64_t)nruns * ngroups * a->n * 8 < (1ll << 31)) {
+    const int grid8 = round_up(nruns * ngroups * a->n, 8);
+    dim3 grid(grid8);
     switch (a->dtype) {
-      case KAD_F32: hipLaunchKernelGGL(merge_band_kernel<float>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw); break;
-      case KAD_F16: hipLaunchKernelGGL(merge_band_kernel<half_t>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw); break;
-      case KAD_BF16: hipLaunchKernelGGL(merge_band_kernel<bf16_t>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw); break;
+      case KAD_F32: hipLaunchKernelGGL(merge_band_kernel<float>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw, nruns, ngroups, grid8); break;
+      case KAD_F16: hipLaunchKernelGGL(merge_band_kernel<half_t>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw, nruns, ngroups, grid8); break;
+      case KAD_BF16: hipLaunchKernelGGL(merge_band_kernel<bf16_t>, grid, dim3(256), band_lds, st, *a, srows_cap, maxbw, nruns, ngroups, grid8); break;
       default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
     }
   } else if (a->layout == KAD_NCHW && disjoint && row_lds <= 64 * 1024) {

@@ -697,12 +697,14 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   __shared__ int s_box[4];       // ymin, ymax, xmin, xmax (clamped corners of live samples)
   __shared__ int s_reg[5];       // region y0, x0, rows, cols, capped flag
 
-  // XCD-aware tile order: block b runs on XCD b % 8; give each XCD a contiguous band.
+  // XCD-aware tile order over (image, tile) flattened: block b runs on XCD b % 8, which takes a
+  // contiguous run of it (8 images: one image per XCD), so neighbouring tiles share their halos
+  // through one L2; the column blocks of a tile (blockIdx.y) land on the same XCD.
   const int bx = blockIdx.x;
-  const int tile = (bx & 7) * (g.grid_x >> 3) + (bx >> 3);
-  if (tile >= g.tiles) return;  // whole block, before any barrier
+  const int q = (bx & 7) * (g.grid_x >> 3) + (bx >> 3);
+  if (q >= a.n * g.tiles) return;  // whole block, before any barrier
+  const int n = q / g.tiles, tile = q - n * g.tiles;
   const int co0 = blockIdx.y * NB;
-  const int n = blockIdx.z;
   const int tyi = tile / g.tiles_x;
   const int ty0 = tyi * g.th, tx0 = (tile - tyi * g.tiles_x) * g.tw;
   const int P = g.ho * g.wo;
@@ -1224,7 +1226,7 @@ static DcnGeom make_geom(const kad_dcn_args& a, int ho, int wo) {
   pick_tile(ho, wo, &g.th, &g.tw);
   g.tiles_x = ceil_div(wo, g.tw);
   g.tiles = ceil_div(ho, g.th) * g.tiles_x;
-  g.grid_x = round_up(g.tiles, 8);
+  g.grid_x = round_up(a.n * g.tiles, 8);  // flattened (image, tile), padded to whole XCD rounds
   g.nchunk = ceil_div(a.cin, 32);
   g.cout_pad = round_up(a.cout, 16);
   g.fh = (g.th - 1) * a.stride + 3;
@@ -1236,7 +1238,7 @@ static DcnGeom make_geom(const kad_dcn_args& a, int ho, int wo) {
 
 template <typename T, typename OutT, int NBF, int MODE>
 static int launch_dcn(const kad_dcn_args& a, hipStream_t st, const DcnGeom& g) {
-  dim3 grid(g.grid_x, ceil_div(a.cout, NBF * 16), a.n);
+  dim3 grid(g.grid_x, ceil_div(a.cout, NBF * 16), 1);
   hipLaunchKernelGGL((dcn_fwd_kernel<T, OutT, NBF, MODE>), grid, dim3(DCN_THREADS), 0, st, a, g);
   return check_launch(MODE == MODE_PLAIN ? "kad_conv3x3_fwd" : MODE == MODE_FUSED ? "kad_dsc_fwd" : "kad_dcn_fwd");
 }
@@ -1285,6 +1287,7 @@ static int validate_dcn(const kad_dcn_args* a, int mode, DcnGeom* g_out) {
   }
   const uintptr_t align = (uintptr_t)a->x | (uintptr_t)a->wpack | (uintptr_t)a->off_wpack;
   KAD_CHECK_ARG(align % 16 == 0, "x and packed weights must be 16-byte aligned");
+  KAD_CHECK_ARG((int64_t)a->n * ceil_div(ho, 1) * wo < (1ll << 30), "kad_dcn: N x output pixels too large");
   *g_out = make_geom(*a, ho, wo);
   if (mode != MODE_EXT)
     KAD_CHECK_ARG(g_out->fh * g_out->fw <= DCN_FCAP, "stride %d not supported here (3x3 footprint of a tile %dx%d > %d px)",

@@ -251,6 +251,16 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     nbf[b] = ceil_div(c, 16);
   }
 
+  // the branches' biases for this block's columns, staged once (the epilogue reads them from LDS)
+  __shared__ float s_bias[3][NB];
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    const float* bp = b == 0 ? a.bias[0] : b == 1 ? a.bias[1] : a.bias[2];
+    const int cb = b < nb ? a.cout[b] : 0;
+    for (int col = tid; col < NB; col += PY_THREADS)
+      s_bias[b][col] = (bp && col0 + col < cb) ? bp[col0 + col] : 0.f;
+  }
+
   floatx4 acc0[4][HB], acc1[HB], acc2[HB];
 #pragma unroll
   for (int j = 0; j < HB; ++j) {
@@ -501,7 +511,6 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     const int tr = PY_TR >> b, tc = PY_TC >> b;
     const int hbch = a.out_h[b], wbch = a.out_w[b];
     const int cout = a.cout[b];
-    const float* bias = a.bias[b];
     const int vc = (wbch - tx * tc) < tc ? (wbch - tx * tc) : tc;  // valid columns in this tile
     const int vr = (hbch - ty * tr) < tr ? (hbch - ty * tr) : tr;  // valid rows
     const bool sums = a.rowpart[b] != nullptr;
@@ -529,7 +538,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
       if (bf >= nbf[b]) continue;  // uniform per wave
       const int col = bf * 16 + row16, co = col0 + col;
       const bool real = co < cout;
-      const float bv = (bias && real) ? bias[co] : 0.f;
+      const float bv = s_bias[b][col];  // 0 past Cout
       if (b == 0) {  // y staged below, one pixel half at a time
         if (sums) {
 #pragma unroll
@@ -597,7 +606,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
         if (bf >= nbf[b]) continue;
         const int col = bf * 16 + row16, co = col0 + col;
         if (co >= cout) continue;
-        const float bv = bias ? bias[co] : 0.f;
+        const float bv = s_bias[b][col];
         if (b == 0) {
 #pragma unroll
           for (int h = 0; h < 2; ++h)
@@ -634,7 +643,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
             const int bf = wb * HB + bb;
             if (bf >= nbf[0]) continue;
             const int col = bf * 16 + row16, co = col0 + col;
-            const float bv = (bias && co < cout) ? bias[co] : 0.f;
+            const float bv = s_bias[0][col];
 #pragma unroll
             for (int mm = 0; mm < 4; ++mm)
 #pragma unroll

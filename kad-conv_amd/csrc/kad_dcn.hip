@@ -1183,7 +1183,10 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   if constexpr (MODE != MODE_PLAIN) {
     if (a.se_att && a.gap_partial) {
       __shared__ int s_last;
-      __syncthreads();  // this block's partial exchanges are performed; the epilogue's LDS tile is free
+      // This block's partial exchanges are performed (each thread waited for its exchange's
+      // return) and the epilogue's LDS tile is free.  The barrier waits for LDS traffic only,
+      // not for the acknowledgements of the output stores, which no one here reads.
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (tid == 0) {
         const unsigned total = (unsigned)g.tiles * gridDim.y;
         const unsigned prev = __hip_atomic_fetch_add(a.se_count + n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1194,7 +1197,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
         }
         s_last = last;
       }
-      __syncthreads();
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (s_last) {
         se_tail(a.gap_partial, a.se_w1, a.se_b1, a.se_w2, a.se_b2, a.se_att, a.se_inv_count, a.cout, a.se_hid, n,
                 g.tiles, (float*)region);

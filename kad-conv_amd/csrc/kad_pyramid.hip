@@ -163,6 +163,25 @@ __device__ __forceinline__ floatx4 py_mma_f(const PyFrag<T>& a, const PyFrag<T>&
   }
 }
 
+// fp16 pooling sums without separate conversions: v_fma_mix_f32 with f16 sources
+// (op_sel_hi 1; op_sel picks the high half), multiplier 1.0 and one f32 rounding,
+// so mix_add2(a, b) == (float)a + (float)b and mix_add1(a, c) == (float)a + c exactly.
+template <int HI>
+__device__ __forceinline__ float mix_add2(unsigned a, unsigned b) {
+  float r;
+  if constexpr (HI) asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,1] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+  else asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,1]" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+template <int HI>
+__device__ __forceinline__ float mix_add1(unsigned a, float c) {
+  float r;
+  if constexpr (HI) asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(a), "v"(c));
+  else asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(a), "v"(c));
+  return r;
+}
+__device__ __forceinline__ unsigned frag_word(const uint4& q, int w) { return w == 0 ? q.x : w == 1 ? q.y : w == 2 ? q.z : q.w; }
+
 // Pooled input of branches 1 and 2, built straight into an A fragment (8
 // channels from lane group offset g8, fp32 sums, one rounding to T): S = 2, the
 // 2 x 2 window with top-left staged pixel q0; S = 4, the upper or lower half (two
@@ -173,7 +192,37 @@ __device__ __forceinline__ PyFrag<T> pooled_frag(const T* xs, int q0, int g8) {
   float acc8[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc8[j] = 0.f;
-  if constexpr (S == 2) {  // (a + b) + (c + d), as a 2x2 average is usually formed
+  if constexpr (__is_same(T, half_t)) {  // same sums in the same order, conversions folded into the adds
+    if constexpr (S == 2) {
+      const uint4 s0 = *(const uint4*)(xs + q0 * LDA + g8), s1 = *(const uint4*)(xs + (q0 + 1) * LDA + g8);
+      const uint4 s2 = *(const uint4*)(xs + (q0 + PY_TC) * LDA + g8);
+      const uint4 s3 = *(const uint4*)(xs + (q0 + PY_TC + 1) * LDA + g8);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        acc8[2 * w] = mix_add2<0>(frag_word(s0, w), frag_word(s1, w)) + mix_add2<0>(frag_word(s2, w), frag_word(s3, w));
+        acc8[2 * w + 1] =
+            mix_add2<1>(frag_word(s0, w), frag_word(s1, w)) + mix_add2<1>(frag_word(s2, w), frag_word(s3, w));
+      }
+    } else {
+      uint4 sv[2 * S];
+#pragma unroll
+      for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+        for (int dx = 0; dx < S; ++dx) sv[dy * S + dx] = *(const uint4*)(xs + (q0 + dy * PY_TC + dx) * LDA + g8);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        float lo = mix_add2<0>(frag_word(sv[0], w), frag_word(sv[1], w));
+        float hi = mix_add2<1>(frag_word(sv[0], w), frag_word(sv[1], w));
+#pragma unroll
+        for (int k = 2; k < 2 * S; ++k) {
+          lo = mix_add1<0>(frag_word(sv[k], w), lo);
+          hi = mix_add1<1>(frag_word(sv[k], w), hi);
+        }
+        acc8[2 * w] = lo;
+        acc8[2 * w + 1] = hi;
+      }
+    }
+  } else if constexpr (S == 2) {  // (a + b) + (c + d), as a 2x2 average is usually formed
     const PyFrag<T> s0 = frag_ld(xs + q0 * LDA + g8), s1 = frag_ld(xs + (q0 + 1) * LDA + g8);
     const PyFrag<T> s2 = frag_ld(xs + (q0 + PY_TC) * LDA + g8), s3 = frag_ld(xs + (q0 + PY_TC + 1) * LDA + g8);
 #pragma unroll
@@ -505,6 +554,11 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
   // sums from registers + one LDS exchange between the two pixel-half waves.
   // Branch-0 pixels outside the image hold exact zeros (zero input); pooled
   // branches mask windows past the floor-mode output explicitly.
+  // The barriers here guard the LDS staging (colred, obt) only: they wait for LDS
+  // traffic, not for the global stores of the previous phase (a workgroup
+  // barrier would wait for their write acknowledgements each time).  No load
+  // into LDS is in flight past the K loop.
+#define PY_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 #pragma unroll
   for (int b = 0; b < 3; ++b) {
     if (ncols[b] == 0) continue;   // uniform across the block
@@ -516,7 +570,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     const bool sums = a.rowpart[b] != nullptr;
     float* rowp = a.rowpart[b];
     float* colp = a.colpart[b];
-    __syncthreads();  // the K loop (or the previous branch) is done with the LDS
+    PY_LDS_BARRIER();  // the K loop (or the previous branch) is done with the LDS
     if (b == 2) {  // the lower-half products (wa == 1) join the upper half (wa == 0)
       if (wa == 1) {
 #pragma unroll
@@ -524,7 +578,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) colred[((wb * HB + bb) * 16 + grp * 4 + i) * 16 + row16] = acc2[bb][i];
       }
-      __syncthreads();
+      PY_LDS_BARRIER();
       if (wa == 0) {
 #pragma unroll
         for (int bb = 0; bb < HB; ++bb)
@@ -597,7 +651,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
         }
       }
     }
-    __syncthreads();
+    PY_LDS_BARRIER();
     // column sums of branches 0 and 1: the wa == 0 waves add the wa == 1 partials
     if (sums && b < 2 && wa == 0) {
 #pragma unroll
@@ -636,7 +690,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     const int npass = b == 0 ? 2 : 1;
     for (int h = 0; h < npass; ++h) {
       if (b == 0) {
-        __syncthreads();  // the staging rows are free
+        PY_LDS_BARRIER();  // the staging rows are free
         if (wa == h) {
 #pragma unroll
           for (int bb = 0; bb < HB; ++bb) {
@@ -650,7 +704,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
               for (int i = 0; i < 4; ++i) obt[(mm * 16 + grp * 4 + i) * OBT + col] = from_f32<T>(acc0[mm][bb][i] + bv);
           }
         }
-        __syncthreads();
+        PY_LDS_BARRIER();
       }
       const int npx = b == 0 ? 64 : tr * tc;
       for (int e = tid; e < npx * G8; e += PY_THREADS) {
@@ -667,6 +721,7 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     }
   }
 }
+#undef PY_LDS_BARRIER
 
 // Dynamic LDS (register-staged path): the K loop's x and weight stages or the
 // epilogue's 64-row y staging (+ column partials on the fp32 path; the 16-bit

@@ -253,8 +253,8 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
       const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC, gc = cs_ + ch;                    \
       const int gx = w0 - HALF_BAND + r, gy = h0 - HALF_BAND + r;                                              \
       const bool ok = r < LM_UR && ch < nsc_ && gc < c;                                                        \
-      vc_[u] = (ok && gx >= 0 && gx < w) ? colm_n[(int64_t)gx * c + gc] : 0.f;                                 \
-      va_[u] = (ok && gy >= 0 && gy < h) ? arow_n[(int64_t)gy * c + gc] : 0.f;                                 \
+      vc_[u] = (ok && gx >= 0 && gx < w) ? colm_n[(uint32_t)(gx * c + gc)] : 0.f;                              \
+      va_[u] = (ok && gy >= 0 && gy < h) ? arow_n[(uint32_t)(gy * c + gc)] : 0.f;                              \
     }                                                                                                          \
     _Pragma("unroll") for (int u = 0; u < NP; ++u) {                                                           \
       const int e = tid + u * LM_THREADS;                                                                      \
@@ -297,31 +297,43 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
         if (which < 3) (which == 0 ? s_b1 : which == 1 ? s_bna : s_bnb)[ch] = vq_[u];
       }
       LM_LDS_BARRIER();
-      if ((g + 1) * CPG < kc1) LM_LOAD_GROUP(cs + LM_SC);
-      // strip-conv coefficients of the 16 columns (separable 1x11 conv + folded BN), branch-free:
-      // the staged column means are 0 outside the image, so only S needs the in-image mask, and
-      // every LDS read of a task is independent (a task is not a chain of dependent reads)
-      for (int e = tid; e < LM_TW * LM_SC; e += LM_THREADS) {
-        const int col = e / LM_SC, ch = e - col * LM_SC, gx = w0 + col;
-        float S0 = 0.f, S1 = 0.f, B0 = 0.f, B1 = 0.f;
+      // strip-conv coefficients of the 16 columns (separable 1x11 conv + folded BN): task
+      // (channel ch, quarter qc of the columns) holds the channel's 11 taps and the 14 column
+      // means its 4 columns need in registers and forms the 4 sliding sums.  The staged column
+      // means are 0 outside the image, so only S needs the in-image mask.
+      static_assert(LM_TW == 16, "four column quarters");
+      for (int e = tid; e < 4 * LM_SC; e += LM_THREADS) {
+        const int qc = e / LM_SC, ch = e - qc * LM_SC;
+        float wk[BAND], cm[4 + BAND - 1];
 #pragma unroll
-        for (int k = 0; k < BAND; ++k) {
-          const int xx = gx + k - HALF_BAND;
-          const float wk = s_w1[ch * BAND + k], cm = s_col[col + k][ch];
-          const float m = (xx >= 0 && xx < w) ? wk : 0.f;
-          if (k & 1) {
-            S1 += m;
-            B1 += wk * cm;
-          } else {
-            S0 += m;
-            B0 += wk * cm;
+        for (int k = 0; k < BAND; ++k) wk[k] = s_w1[ch * BAND + k];
+#pragma unroll
+        for (int j = 0; j < 4 + BAND - 1; ++j) cm[j] = s_col[qc * 4 + j][ch];
+        const bool chok = ch < nsc && cs + ch < c;
+        const float bna = s_bna[ch], bb = s_b1[ch], bnb = s_bnb[ch];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = qc * 4 + q, gx = w0 + col;
+          float S0 = 0.f, S1 = 0.f, B0 = 0.f, B1 = 0.f;  // even / odd taps, added last
+#pragma unroll
+          for (int k = 0; k < BAND; ++k) {
+            const int xx = gx + k - HALF_BAND;
+            const float m = (xx >= 0 && xx < w) ? wk[k] : 0.f;
+            if (k & 1) {
+              S1 += m;
+              B1 += wk[k] * cm[q + k];
+            } else {
+              S0 += m;
+              B0 += wk[k] * cm[q + k];
+            }
           }
+          const float S = S0 + S1, B = B0 + B1;
+          const bool ok = gx < w && chok;
+          s_alpha[col][ch] = ok ? bna * S : 0.f;
+          s_beta[col][ch] = ok ? bna * (B + bb) + bnb : 0.f;
         }
-        const float S = S0 + S1, B = B0 + B1;
-        const bool ok = gx < w && ch < nsc && cs + ch < c;
-        s_alpha[col][ch] = ok ? s_bna[ch] * S : 0.f;
-        s_beta[col][ch] = ok ? s_bna[ch] * (B + s_b1[ch]) + s_bnb[ch] : 0.f;
       }
+      if ((g + 1) * CPG < kc1) LM_LOAD_GROUP(cs + LM_SC);  // after the coefficients: fewer live registers there
     }
     LM_LDS_BARRIER();  // alpha / beta ready; the previous chunk's MFMAs are done with us
     // u = relu(alpha * a + beta): thread (column, 8-channel group) fixed, rows r0, r0 + 4, ...;
@@ -494,6 +506,7 @@ extern "C" int kad_lcsa_mask(const float* arow, const float* colm, const float* 
                              void* stream) {
   KAD_CHECK_ARG(arow && colm && params && emat && ebias && mask, "kad_lcsa_mask: null pointer");
   KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0, "kad_lcsa_mask: bad shape");
+  KAD_CHECK_ARG((int64_t)(h > w ? h : w) * c < (1ll << 31), "kad_lcsa_mask: H or W times C exceeds 2^31 (32-bit mean indices)");
   KAD_CHECK_ARG(((uintptr_t)emat) % 16 == 0, "kad_lcsa_mask: emat must be 16-byte aligned");
   return kad::launch_lcsa_mask(arow, colm, params, emat, ebias, mask, n, c, h, w, emat_dtype, 1, nullptr,
                                (hipStream_t)stream);
@@ -517,6 +530,7 @@ extern "C" int kad_lcsa_mask_split(const float* arow, const float* colm, const f
                                    int ksplit, float* work, void* stream) {
   KAD_CHECK_ARG(arow && colm && params && emat && ebias && mask, "kad_lcsa_mask_split: null pointer");
   KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0, "kad_lcsa_mask_split: bad shape");
+  KAD_CHECK_ARG((int64_t)(h > w ? h : w) * c < (1ll << 31), "kad_lcsa_mask_split: H or W times C exceeds 2^31 (32-bit mean indices)");
   KAD_CHECK_ARG(((uintptr_t)emat) % 16 == 0, "kad_lcsa_mask_split: emat must be 16-byte aligned");
   KAD_CHECK_ARG(ksplit >= 1 && ksplit <= round_up(c, 32) / 32, "kad_lcsa_mask_split: ksplit %d outside [1, %d]",
                 ksplit, round_up(c, 32) / 32);

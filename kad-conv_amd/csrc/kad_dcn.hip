@@ -1154,14 +1154,22 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       if (pl >= npx || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
       out[((int64_t)n * P + (int64_t)oy * g.wo + ox) * a.out_cs + co] = ost[pl * SROW + col];
     }
-  } else {  // NCHW: consecutive lanes along the tile's pixels
-    for (int j = tid; j < DCN_TILE * NB; j += DCN_THREADS) {
-      const int col = j / DCN_TILE, pl = j - col * DCN_TILE;
-      const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
-      const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
-      const int co = co0 + col;
-      if (pl >= npx || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
-      out[((int64_t)n * a.out_cs + co) * P + (int64_t)oy * g.wo + ox] = ost[pl * SROW + col];
+  } else {  // NCHW: consecutive lanes along the tile's pixels; a thread keeps its pixel for every channel
+    static_assert(DCN_THREADS % DCN_TILE == 0, "one pixel per thread across channel steps");
+    constexpr int CSTEP = DCN_THREADS / DCN_TILE;
+    const int pl = tid % DCN_TILE, col0 = tid / DCN_TILE;
+    const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+    const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
+    if (pl < npx && oy < g.ho && ox < g.wo) {
+      OutT* dst = out + ((int64_t)n * a.out_cs + co0 + col0) * P + (int64_t)oy * g.wo + ox;
+      const OutT* src = ost + pl * SROW + col0;
+      const int ncol = a.cout - co0 < NB ? a.cout - co0 : NB;
+#pragma unroll 4
+      for (int col = col0; col < ncol; col += CSTEP) {
+        *dst = *src;
+        dst += (int64_t)CSTEP * P;
+        src += CSTEP;
+      }
     }
   }
   if (a.gap_partial && tid < NB) {

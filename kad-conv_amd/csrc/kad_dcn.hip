@@ -751,11 +751,6 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       }
     }
   }
-  if (tid < NB) {  // v = acc * mul + (bias * mul + add)
-    s_par[0][tid] = par[0] * par[1] + par[2];
-    s_par[1][tid] = par[1];
-    s_par[3][tid] = par[3];
-  }
   if (tid == 0) {
     s_box[0] = 0x7fffffff;
     s_box[1] = -1;
@@ -1084,7 +1079,14 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   constexpr int SROW = L::SROW;
   OutT* ost = (OutT*)region;
   float(*gap_red)[NB] = (float(*)[NB])((char*)region + L::STAGE_BYTES);
-  __syncthreads();  // every wave is done reading the region
+  // the epilogue parameters, loaded at the start, are staged only now: storing them
+  // there would have held waves 0-1 for a global round trip before the offset conv
+  if (tid < NB) {  // v = acc * mul + (bias * mul + add)
+    s_par[0][tid] = par[0] * par[1] + par[2];
+    s_par[1][tid] = par[1];
+    s_par[3][tid] = par[3];
+  }
+  __syncthreads();  // every wave is done reading the region; s_par staged
   bool pix_ok[DCN_WM][4];
 #pragma unroll
   for (int m = 0; m < DCN_WM; ++m)

@@ -68,6 +68,19 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, char* dst, uint32
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, KAD_LDS(dst), 4, voff, soff, 0, 0);
 }
 
+// v summed over lanes l and l ^ 16 (sum_xor16) or l and l ^ 32 (sum_xor32) of the wave,
+// on the VALU: v_permlane16_swap / v_permlane32_swap of v with itself leaves every lane
+// holding its own value and its partner's, in one order or the other (a + b == b + a, so
+// the sum equals v + __shfl_xor(v, 16 / 32) bit for bit, without an LDS-path round trip).
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Bilinear resize source index (PyTorch, align_corners=False, output size
 // given): s = max(scale * (dst + 0.5) - 0.5, 0) with scale = in / out; rows
 // i0 = floor(s) and i1 = min(i0 + 1, in - 1), weight of i1 = s - i0.

@@ -1121,8 +1121,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
 #pragma unroll
     for (int b = 0; b < NBF; ++b) {
       float v = gsum[b];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      v = sum_xor32(sum_xor16(v));
       if (grp == 0) gap_red[wave][b * 16 + row] = v;
     }
   }

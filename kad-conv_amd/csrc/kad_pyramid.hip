@@ -61,6 +61,27 @@ __device__ __forceinline__ T raw_get(const Raw8& r, int j) {
   }
 }
 
+// Eight elements of T packed as raw bits (inverse of raw_get).
+template <typename T>
+__device__ __forceinline__ Raw8 raw_pack(const T (&t)[8]) {
+  Raw8 r;
+  if constexpr (sizeof(T) == 2) {
+    unsigned w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (unsigned)__builtin_bit_cast(unsigned short, t[2 * j]) |
+             ((unsigned)__builtin_bit_cast(unsigned short, t[2 * j + 1]) << 16);
+    r.lo = uint4{w[0], w[1], w[2], w[3]};
+    r.hi = uint4{0u, 0u, 0u, 0u};
+  } else {
+    r.lo = uint4{__builtin_bit_cast(unsigned, t[0]), __builtin_bit_cast(unsigned, t[1]),
+                 __builtin_bit_cast(unsigned, t[2]), __builtin_bit_cast(unsigned, t[3])};
+    r.hi = uint4{__builtin_bit_cast(unsigned, t[4]), __builtin_bit_cast(unsigned, t[5]),
+                 __builtin_bit_cast(unsigned, t[6]), __builtin_bit_cast(unsigned, t[7])};
+  }
+  return r;
+}
+
 // 8 consecutive elements at p, the first `valid` real, the rest 0.
 template <typename T>
 __device__ __forceinline__ Raw8 load8_raw(const T* p, int valid) {
@@ -274,10 +295,16 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
   extern __shared__ __align__(16) char smem[];
   T* xs = (T*)smem;                   // register-staged path: [128][LDA]
   T* bs = xs + PY_TILE * LDA;         // register-staged path: [3][NB][LDA]
-  // epilogue: [64][OBT] y values of one branch (branch 0: one pixel half)
-  T* obt = (H16 && dma) ? xsd : (T*)smem;
-  // epilogue: column partials, [32][NB] fp32 (branch 2: [2][HB][16][16])
-  float* colred = H16 ? (float*)pw2 : (float*)(smem + 64 * OBT * sizeof(T));
+  // epilogue staging: y of branch 0 as T rows [128][OBT] in two 64-row halves, y of branch 1
+  // [32][OBT], and the two fp32 half-window products of branch 2 [2][8][NB].  Pipelined path:
+  // the three weight-ring stages (free after the K loop); register-staged path: dynamic LDS.
+  constexpr int Y0H = 64 * OBT * (int)sizeof(T), Y1B = 32 * OBT * (int)sizeof(T);
+  static_assert(!H16 || (Y0H <= PyW<HB>::BYTES && Y1B + 2 * 8 * NB * 4 <= PyW<HB>::BYTES),
+                "epilogue staging must fit the weight ring stages");
+  T* const y0a = (H16 && dma) ? (T*)pw0 : (T*)smem;
+  T* const y0b = (H16 && dma) ? (T*)pw1 : (T*)(smem + Y0H);
+  T* const y1s = (H16 && dma) ? (T*)pw2 : (T*)(smem + 2 * Y0H);
+  float* const y2s = (float*)((char*)y1s + Y1B);
 
   // XCD-aware order: block b runs on XCD b % 8, which takes the contiguous run of tiles
   // [(b % 8) grid8 / 8, ...): the tiles of a row band (which share input lines) stay in one L2.
@@ -545,194 +572,177 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
   }
   }
 
-  // ---- epilogue, one branch at a time -------------------------------------------------------------
+  // ---- epilogue -------------------------------------------------------------------------------------
   // acc layout: lane (row16, grp) holds column bf * 16 + row16 and tile pixels
   //   branch 0: (wa * 4 + mm) * 16 + grp * 4 + i  (tile row 2 wa + mm / 2, column (mm & 1) * 16 + grp * 4 + i)
   //   branch 1: wa * 16 + grp * 4 + i             (pooled row wa, column grp * 4 + i)
-  //   branch 2: grp * 4 + i (< 8)                 (pooled row 0, column grp * 4 + i)
-  // Row sums come from registers (+ shuffles across the 4 lane groups); column
-  // sums from registers + one LDS exchange between the two pixel-half waves.
-  // Branch-0 pixels outside the image hold exact zeros (zero input); pooled
-  // branches mask windows past the floor-mode output explicitly.
-  // The barriers here guard the LDS staging (colred, obt) only: they wait for LDS
-  // traffic, not for the global stores of the previous phase (a workgroup
-  // barrier would wait for their write acknowledgements each time).  No load
-  // into LDS is in flight past the K loop.
+  //   branch 2: grp * 4 + i (< 8)                 (pooled row 0, column grp * 4 + i; wa = half of the window)
+  // 1. Each wave rounds its outputs (bias added) to T and stages them; the row sums of
+  //    branches 0 and 1 come from the same rounded values in registers (+ shuffles across
+  //    the 4 lane groups), masked to the tile's valid columns.
+  // 2. After one barrier all threads store y as 16-byte NHWC pieces and form the column
+  //    sums (and branch 2's row sums, whose window halves meet only here) from LDS.
+  // The partial sums are fp32 sums of the rounded outputs, as pooling y in T does.  A tile
+  // with no row of a pooled branch still writes zero column partials (the consumer reads
+  // every slice).  The barriers wait for LDS traffic only.  No load into LDS is in flight
+  // past the K loop.
 #define PY_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+  PY_LDS_BARRIER();  // every wave is done with the K loop's LDS
+  int vcs[3], vrs[3];
 #pragma unroll
   for (int b = 0; b < 3; ++b) {
-    if (ncols[b] == 0) continue;   // uniform across the block
     const int tr = PY_TR >> b, tc = PY_TC >> b;
-    const int hbch = a.out_h[b], wbch = a.out_w[b];
-    const int cout = a.cout[b];
-    const int vc = (wbch - tx * tc) < tc ? (wbch - tx * tc) : tc;  // valid columns in this tile
-    const int vr = (hbch - ty * tr) < tr ? (hbch - ty * tr) : tr;  // valid rows
-    const bool sums = a.rowpart[b] != nullptr;
-    float* rowp = a.rowpart[b];
-    float* colp = a.colpart[b];
-    PY_LDS_BARRIER();  // the K loop (or the previous branch) is done with the LDS
-    if (b == 2) {  // the lower-half products (wa == 1) join the upper half (wa == 0)
-      if (wa == 1) {
+    const int hbch = b < nb ? a.out_h[b] : 0, wbch = b < nb ? a.out_w[b] : 0;
+    vcs[b] = (wbch - tx * tc) < tc ? (wbch - tx * tc) : tc;  // valid columns in this tile (may be <= 0)
+    vrs[b] = (hbch - ty * tr) < tr ? (hbch - ty * tr) : tr;  // valid rows
+  }
 #pragma unroll
-        for (int bb = 0; bb < HB; ++bb)
+  for (int bb = 0; bb < HB; ++bb) {
+    const int bf = wb * HB + bb;
+    const int col = bf * 16 + row16, co = col0 + col;
+    if (bf < nbf[0]) {
+      const float bv = s_bias[0][col];
+      T* yh = wa == 0 ? y0a : y0b;
+      float sr[2] = {0.f, 0.f};
 #pragma unroll
-          for (int i = 0; i < 4; ++i) colred[((wb * HB + bb) * 16 + grp * 4 + i) * 16 + row16] = acc2[bb][i];
-      }
-      PY_LDS_BARRIER();
-      if (wa == 0) {
+      for (int mm = 0; mm < 4; ++mm)
 #pragma unroll
-        for (int bb = 0; bb < HB; ++bb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc2[bb][i] += colred[((wb * HB + bb) * 16 + grp * 4 + i) * 16 + row16];
-      }
-    }
-#pragma unroll
-    for (int bb = 0; bb < HB; ++bb) {
-      const int bf = wb * HB + bb;
-      if (bf >= nbf[b]) continue;  // uniform per wave
-      const int col = bf * 16 + row16, co = col0 + col;
-      const bool real = co < cout;
-      const float bv = s_bias[b][col];  // 0 past Cout
-      if (b == 0) {  // y staged below, one pixel half at a time
-        if (sums) {
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {  // tile rows 2 wa + q
-            float sr = 0.f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) sr += acc0[2 * q][bb][i] + acc0[2 * q + 1][bb][i];
-            sr += __shfl_xor(sr, 16);
-            sr += __shfl_xor(sr, 32);
-            const int r = 2 * wa + q;
-            if (grp == 0 && real && r < vr)
-              rowp[(((int64_t)n * a.ntx + tx) * hbch + ty * tr + r) * cout + co] = sr + vc * bv;
-          }
-          if (wa == 1) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-              for (int i = 0; i < 4; ++i)
-                colred[(h * 16 + grp * 4 + i) * NB + col] = acc0[h][bb][i] + acc0[2 + h][bb][i];
-          }
+        for (int i = 0; i < 4; ++i) {
+          const T v = from_f32<T>(acc0[mm][bb][i] + bv);
+          yh[(mm * 16 + grp * 4 + i) * OBT + col] = v;
+          sr[mm >> 1] += ((mm & 1) * 16 + grp * 4 + i < vcs[0]) ? to_f32(v) : 0.f;
         }
-      } else if (b == 1) {
+      if (a.rowpart[0]) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) obt[(wa * 16 + grp * 4 + i) * OBT + col] = from_f32<T>(acc1[bb][i] + bv);
-        if (sums) {
-          float sr = 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sr += (grp * 4 + i < vc) ? acc1[bb][i] : 0.f;
-          sr += __shfl_xor(sr, 16);
-          sr += __shfl_xor(sr, 32);
-          if (grp == 0 && real && wa < vr)
-            rowp[(((int64_t)n * a.ntx + tx) * hbch + ty * tr + wa) * cout + co] = sr + vc * bv;
-          if (wa == 1) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) colred[(grp * 4 + i) * NB + col] = (1 < vr) ? acc1[bb][i] : 0.f;
-          }
-        }
-      } else if (wa == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (grp * 4 + i < 8) obt[(grp * 4 + i) * OBT + col] = from_f32<T>(acc2[bb][i] + bv);
-        if (sums) {
-          float sr = 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sr += (grp * 4 + i < vc) ? acc2[bb][i] : 0.f;
-          sr += __shfl_xor(sr, 16);
-          sr += __shfl_xor(sr, 32);
-          if (grp == 0 && real && vr > 0)
-            rowp[(((int64_t)n * a.ntx + tx) * hbch + ty * tr) * cout + co] = sr + vc * bv;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {  // a tile with no row of this branch contributes 0 (the consumer reads every slice)
-            const int c = grp * 4 + i;
-            if (real && c < vc)
-              colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] = vr > 0 ? acc2[bb][i] + bv : 0.f;
-          }
+        for (int q = 0; q < 2; ++q) {  // tile rows 2 wa + q
+          float v = sr[q];
+          v = sum_xor32(sum_xor16(v));
+          const int r = 2 * wa + q;
+          if (grp == 0 && co < a.cout[0] && r < vrs[0])
+            a.rowpart[0][(((int64_t)n * a.ntx + tx) * a.out_h[0] + ty * PY_TR + r) * a.cout[0] + co] = v;
         }
       }
     }
-    PY_LDS_BARRIER();
-    // column sums of branches 0 and 1: the wa == 0 waves add the wa == 1 partials
-    if (sums && b < 2 && wa == 0) {
+    if (bf < nbf[1]) {
+      const float bv = s_bias[1][col];
+      float sr = 0.f;
 #pragma unroll
-      for (int bb = 0; bb < HB; ++bb) {
-        const int bf = wb * HB + bb;
-        if (bf >= nbf[b]) continue;
-        const int col = bf * 16 + row16, co = col0 + col;
-        if (co >= cout) continue;
-        const float bv = s_bias[b][col];
-        if (b == 0) {
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int c = h * 16 + grp * 4 + i;
-              if (c < vc)
-                colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] =
-                    (acc0[h][bb][i] + acc0[2 + h][bb][i]) + colred[c * NB + col] + vr * bv;
-            }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {  // a tile with no row of this branch contributes 0
-            const int c = grp * 4 + i;
-            if (c < vc)
-              colp[(((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + co] =
-                  vr > 0 ? acc1[bb][i] + colred[c * NB + col] + vr * bv : 0.f;
-          }
-        }
+      for (int i = 0; i < 4; ++i) {
+        const T v = from_f32<T>(acc1[bb][i] + bv);
+        y1s[(wa * 16 + grp * 4 + i) * OBT + col] = v;
+        sr += (grp * 4 + i < vcs[1]) ? to_f32(v) : 0.f;
+      }
+      if (a.rowpart[1]) {
+        sr = sum_xor32(sum_xor16(sr));
+        if (grp == 0 && co < a.cout[1] && wa < vrs[1])
+          a.rowpart[1][(((int64_t)n * a.ntx + tx) * a.out_h[1] + ty * (PY_TR >> 1) + wa) * a.cout[1] + co] = sr;
       }
     }
-    // y_b: NHWC, 16-byte pieces of 8 channels straight from the staged rows (pad channels are 0);
-    // branch 0 in two passes of 64 pixels (the staging buffer holds 64 rows)
+    if (bf < nbf[2]) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (grp * 4 + i < 8) y2s[(wa * 8 + grp * 4 + i) * NB + col] = acc2[bb][i];
+    }
+  }
+  PY_LDS_BARRIER();
+  // staged y of branch b, pixel p, columns c8 .. c8 + 7 (branch 2: the halves added, bias, rounding)
+#define PY_STAGED(B, P, C8, OUT)                                                                     \
+  {                                                                                                  \
+    if ((B) == 0) {                                                                                  \
+      const T* sp_ = ((P) < 64 ? y0a + (P) * OBT : y0b + ((P) - 64) * OBT) + (C8);                   \
+      OUT.lo = *(const uint4*)sp_;                                                                   \
+      if constexpr (sizeof(T) == 4) OUT.hi = *(const uint4*)(sp_ + 4);                               \
+    } else if ((B) == 1) {                                                                           \
+      const T* sp_ = y1s + (P) * OBT + (C8);                                                         \
+      OUT.lo = *(const uint4*)sp_;                                                                   \
+      if constexpr (sizeof(T) == 4) OUT.hi = *(const uint4*)(sp_ + 4);                               \
+    } else {                                                                                         \
+      const floatx4* h0_ = (const floatx4*)(y2s + (P) * NB + (C8));                                  \
+      const floatx4* h1_ = (const floatx4*)(y2s + (8 + (P)) * NB + (C8));                            \
+      const floatx4 a0_ = h0_[0], a1_ = h0_[1], b0_ = h1_[0], b1_ = h1_[1];                          \
+      T t_[8];                                                                                       \
+      _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) {                                             \
+        t_[j_] = from_f32<T>(a0_[j_] + b0_[j_] + s_bias[2][(C8) + j_]);                              \
+        t_[4 + j_] = from_f32<T>(a1_[j_] + b1_[j_] + s_bias[2][(C8) + 4 + j_]);                      \
+      }                                                                                              \
+      OUT = raw_pack<T>(t_);                                                                         \
+    }                                                                                                \
+  }
+  constexpr int G8 = NB / 8;
+#pragma unroll
+  for (int b = 0; b < 3; ++b) {
+    if (ncols[b] == 0) continue;  // uniform across the block
+    const int tr = PY_TR >> b, tc = PY_TC >> b;
+    const int hbch = a.out_h[b], wbch = a.out_w[b], cout = a.cout[b], g8 = ncols[b] >> 3;
+    const int vc = vcs[b], vr = vrs[b];
+    // y_b: NHWC, 16-byte pieces of 8 channels (the pad channels come out zero)
     T* y = (T*)a.out[b];
-    const int g8 = ncols[b] >> 3;
-    constexpr int G8 = NB / 8;
-    const int npass = b == 0 ? 2 : 1;
-    for (int h = 0; h < npass; ++h) {
-      if (b == 0) {
-        PY_LDS_BARRIER();  // the staging rows are free
-        if (wa == h) {
+    for (int e = tid; e < tr * tc * G8; e += PY_THREADS) {
+      const int pl = e / G8, g = e - pl * G8;
+      const int py_ = pl / tc;  // tc is a power of two
+      const int gy = ty * tr + py_, gx = tx * tc + (pl - py_ * tc);
+      if (g >= g8 || gy >= hbch || gx >= wbch) continue;
+      Raw8 v;
+      PY_STAGED(b, pl, g * 8, v);
+      store8_raw(y + (((int64_t)n * hbch + gy) * wbch + gx) * a.out_cs[b] + col0 + g * 8, v);
+    }
+    if (!a.colpart[b]) continue;
+    // column sums over the tile's valid rows (0 if it has none), columns c < vc
+    float* colp = a.colpart[b];
+    for (int e = tid; e < tc * G8; e += PY_THREADS) {
+      const int c = e / G8, g = e - c * G8;
+      if (c >= vc || g * 8 >= cout - col0) continue;
+      float sc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < vr; ++r) {
+        Raw8 v;
+        PY_STAGED(b, r * tc + c, g * 8, v);
 #pragma unroll
-          for (int bb = 0; bb < HB; ++bb) {
-            const int bf = wb * HB + bb;
-            if (bf >= nbf[0]) continue;
-            const int col = bf * 16 + row16, co = col0 + col;
-            const float bv = s_bias[0][col];
-#pragma unroll
-            for (int mm = 0; mm < 4; ++mm)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) obt[(mm * 16 + grp * 4 + i) * OBT + col] = from_f32<T>(acc0[mm][bb][i] + bv);
-          }
-        }
-        PY_LDS_BARRIER();
+        for (int j = 0; j < 8; ++j) sc[j] += to_f32(raw_get<T>(v, j));
       }
-      const int npx = b == 0 ? 64 : tr * tc;
-      for (int e = tid; e < npx * G8; e += PY_THREADS) {
-        const int pl = e / G8, g = e - pl * G8;
-        const int px = 64 * h + pl;
-        const int py_ = px / tc;  // tc is a power of two
-        const int gy = ty * tr + py_, gx = tx * tc + (px - py_ * tc);
-        if (g >= g8 || gy >= hbch || gx >= wbch) continue;
-        T* d = y + (((int64_t)n * hbch + gy) * wbch + gx) * a.out_cs[b] + col0 + g * 8;
-        const T* sp = obt + pl * OBT + g * 8;
-        *(uint4*)d = *(const uint4*)sp;
-        if constexpr (sizeof(T) == 4) *(uint4*)(d + 4) = *(const uint4*)(sp + 4);
+      float* d = colp + (((int64_t)n * a.nty + ty) * wbch + tx * tc + c) * cout + col0 + g * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (col0 + g * 8 + j < cout) d[j] = sc[j];
+    }
+    if (b == 2 && a.rowpart[2]) {  // one pooled row per tile: its sum over the valid columns
+      static_assert(8 * G8 <= PY_THREADS && PY_TC >> 2 == 8, "thread (group g, column c) of the pooled row");
+      const int g = tid >> 3, c = tid & 7;  // the 8 lanes of a group stay together (all in or out)
+      if (g < G8) {
+        float sr[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (vr > 0 && c < vc) {
+          Raw8 v;
+          PY_STAGED(2, c, g * 8, v);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) sr[j] = to_f32(raw_get<T>(v, j));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          sr[j] += __shfl_xor(sr[j], 1);
+          sr[j] += __shfl_xor(sr[j], 2);
+          sr[j] += __shfl_xor(sr[j], 4);
+        }
+        if (c == 0 && vr > 0 && g * 8 < cout - col0) {
+          float* d = a.rowpart[2] + (((int64_t)n * a.ntx + tx) * hbch + ty) * cout + col0 + g * 8;
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (col0 + g * 8 + j < cout) d[j] = sr[j];
+        }
       }
     }
   }
+#undef PY_STAGED
 }
 #undef PY_LDS_BARRIER
 
 // Dynamic LDS (register-staged path): the K loop's x and weight stages or the
-// epilogue's 64-row y staging (+ column partials on the fp32 path; the 16-bit
-// paths keep those in the static weight ring).
+// epilogue staging (y of branches 0 and 1 as T rows, branch 2's fp32 window halves).
 template <typename T, int HB>
 static size_t pyramid_lds(int dma) {
-  if (dma) return 0;  // pipelined path: static weight ring and x stages (the epilogue reuses them)
+  if (dma) return 0;  // pipelined path: static weight ring and x stages (the epilogue reuses the ring)
   const size_t lda = PyLds<T>::lda;
   const size_t stage = (size_t)(PY_TILE + 3 * 32 * HB) * lda * sizeof(T);
-  size_t epi = (size_t)64 * (32 * HB + 16 / sizeof(T)) * sizeof(T);
-  if (sizeof(T) == 4) epi += (size_t)32 * 32 * HB * sizeof(float);
+  const size_t obt = (size_t)(32 * HB + 16 / sizeof(T)) * sizeof(T);
+  const size_t epi = (size_t)(128 + 32) * obt + (size_t)2 * 8 * 32 * HB * sizeof(float);
   return stage > epi ? stage : epi;
 }
 

@@ -327,14 +327,16 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     nbf[b] = ceil_div(c, 16);
   }
 
-  // the branches' biases for this block's columns, staged once (the epilogue reads them from LDS)
+  // The branches' biases for this block's columns: requested now, staged into LDS only at the
+  // epilogue (a store here would hold the loading waves for a round trip before the K loop).
+  static_assert(NB <= PY_THREADS, "one bias column per thread");
   __shared__ float s_bias[3][NB];
+  float bias_r[3];
 #pragma unroll
   for (int b = 0; b < 3; ++b) {
     const float* bp = b == 0 ? a.bias[0] : b == 1 ? a.bias[1] : a.bias[2];
     const int cb = b < nb ? a.cout[b] : 0;
-    for (int col = tid; col < NB; col += PY_THREADS)
-      s_bias[b][col] = (bp && col0 + col < cb) ? bp[col0 + col] : 0.f;
+    bias_r[b] = (tid < NB && bp && col0 + tid < cb) ? bp[col0 + tid] : 0.f;
   }
 
   floatx4 acc0[4][HB], acc1[HB], acc2[HB];
@@ -587,7 +589,11 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
   // every slice).  The barriers wait for LDS traffic only.  No load into LDS is in flight
   // past the K loop.
 #define PY_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
-  PY_LDS_BARRIER();  // every wave is done with the K loop's LDS
+  if (tid < NB) {
+#pragma unroll
+    for (int b = 0; b < 3; ++b) s_bias[b][tid] = bias_r[b];
+  }
+  PY_LDS_BARRIER();  // every wave is done with the K loop's LDS; the biases are staged
   int vcs[3], vrs[3];
 #pragma unroll
   for (int b = 0; b < 3; ++b) {

@@ -339,10 +339,13 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
     bias_r[b] = (tid < NB && bp && col0 + tid < cb) ? bp[col0 + tid] : 0.f;
   }
 
-  floatx4 acc0[4][HB], acc1[HB], acc2[HB];
+  // acc0: branch 0, this wave's pixel half x column half.  accp: the wave's pooled branch
+  // (wb = 0: branch 1, wb = 1: branch 2), this wave's pixel half x all 2 HB column fragments,
+  // so each pooled A fragment is formed by one wave instead of both column-half waves.
+  floatx4 acc0[4][HB], accp[2 * HB];
 #pragma unroll
   for (int j = 0; j < HB; ++j) {
-    acc1[j] = acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    accp[j] = accp[HB + j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc0[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
@@ -429,16 +432,17 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
   auto mma_step = [&](const T* x_stage, auto bfrag) {
     // ---- A fragments: the slice (branch 0) and its 2x2 / 4x4 averages (branches 1, 2) ----------
     // wave (wa, wb) = pixel half x column half
-    PyFrag<T> a0[4], a1, a2;
+    PyFrag<T> a0[4], ap;
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) a0[mm] = frag_ld(x_stage + ((wa * 4 + mm) * 16 + row16) * LDA + grp * 8);
-    if (nb > 1) a1 = pooled_frag<T, 2, LDA>(x_stage, (2 * wa) * PY_TC + 2 * row16, grp * 8);  // pooled (wa, row16)
-    if (nb > 2) {  // pooled pixel row16 of the 1 x 8 tile (rows >= 8 are padding); this wave's two rows
+    if (wb == 0) {  // branch 1: pooled (wa, row16)
+      if (nb > 1) ap = pooled_frag<T, 2, LDA>(x_stage, (2 * wa) * PY_TC + 2 * row16, grp * 8);
+    } else if (nb > 2) {  // branch 2: pooled pixel row16 of the 1 x 8 tile (rows >= 8 are padding), rows 2 wa, 2 wa + 1
       if (row16 < 8) {
-        a2 = pooled_frag<T, 4, LDA>(x_stage, (2 * wa) * PY_TC + 4 * row16, grp * 8);
+        ap = pooled_frag<T, 4, LDA>(x_stage, (2 * wa) * PY_TC + 4 * row16, grp * 8);
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a2.v[j] = from_f32<T>(0.f);
+        for (int j = 0; j < 8; ++j) ap.v[j] = from_f32<T>(0.f);
       }
     }
 #pragma unroll
@@ -449,9 +453,11 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
 #pragma unroll
         for (int mm = 0; mm < 4; ++mm) acc0[mm][bb] = py_mma_f<T>(a0[mm], bq, acc0[mm][bb]);
       }
-      if (bf < nbf[1]) acc1[bb] = py_mma_f<T>(a1, bfrag(1, bf), acc1[bb]);
-      if (bf < nbf[2]) acc2[bb] = py_mma_f<T>(a2, bfrag(2, bf), acc2[bb]);
     }
+    const int pbr = 1 + wb, nbp = wb == 0 ? nbf[1] : nbf[2];  // wave-uniform
+#pragma unroll
+    for (int bp = 0; bp < 2 * HB; ++bp)
+      if (bp < nbp) accp[bp] = py_mma_f<T>(ap, bfrag(pbr, bp), accp[bp]);
   };
   auto bfrag_lds = [&](int b, int bf) { return frag_ld(bs + (b * NB + bf * 16 + row16) * LDA + grp * 8); };
 
@@ -577,8 +583,8 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
   // ---- epilogue -------------------------------------------------------------------------------------
   // acc layout: lane (row16, grp) holds column bf * 16 + row16 and tile pixels
   //   branch 0: (wa * 4 + mm) * 16 + grp * 4 + i  (tile row 2 wa + mm / 2, column (mm & 1) * 16 + grp * 4 + i)
-  //   branch 1: wa * 16 + grp * 4 + i             (pooled row wa, column grp * 4 + i)
-  //   branch 2: grp * 4 + i (< 8)                 (pooled row 0, column grp * 4 + i; wa = half of the window)
+  //   branch 1 (accp, wb = 0): wa * 16 + grp * 4 + i  (pooled row wa, column grp * 4 + i)
+  //   branch 2 (accp, wb = 1): grp * 4 + i (< 8)      (pooled row 0, column grp * 4 + i; wa = half of the window)
   // 1. Each wave rounds its outputs (bias added) to T and stages them; the row sums of
   //    branches 0 and 1 come from the same rounded values in registers (+ shuffles across
   //    the 4 lane groups), masked to the tile's valid columns.
@@ -629,12 +635,17 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
         }
       }
     }
-    if (bf < nbf[1]) {
+  }
+  // pooled branches: wave (wa, wb) holds branch 1 + wb over the column fragments bp < 2 HB
+#pragma unroll
+  for (int bp = 0; bp < 2 * HB; ++bp) {
+    const int col = bp * 16 + row16, co = col0 + col;
+    if (wb == 0 && bp < nbf[1]) {
       const float bv = s_bias[1][col];
       float sr = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const T v = from_f32<T>(acc1[bb][i] + bv);
+        const T v = from_f32<T>(accp[bp][i] + bv);
         y1s[(wa * 16 + grp * 4 + i) * OBT + col] = v;
         sr += (grp * 4 + i < vcs[1]) ? to_f32(v) : 0.f;
       }
@@ -644,10 +655,10 @@ __global__ __launch_bounds__(PY_THREADS, (PyOcc<T, HB>::v)) void pyramid_kernel(
           a.rowpart[1][(((int64_t)n * a.ntx + tx) * a.out_h[1] + ty * (PY_TR >> 1) + wa) * a.cout[1] + co] = sr;
       }
     }
-    if (bf < nbf[2]) {
+    if (wb == 1 && bp < nbf[2]) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (grp * 4 + i < 8) y2s[(wa * 8 + grp * 4 + i) * NB + col] = acc2[bb][i];
+        if (grp * 4 + i < 8) y2s[(wa * 8 + grp * 4 + i) * NB + col] = accp[bp][i];
     }
   }
   PY_LDS_BARRIER();

@@ -323,6 +323,33 @@ def counters_from(trace_csv, fetch_csv, write_csv, sq_csv):
     return table, sf, sw
 
 
+def trace_md(trace_csv, title, cmd, desc=None):
+    """Markdown summary of a rocprofv3 --kernel-trace CSV: per (kernel, grid) the dispatch
+    count and the median / mean duration (the tables under profiles/)."""
+    import csv
+    import statistics
+    by_kg, meta = {}, {}
+    for r in csv.DictReader(open(trace_csv)):
+        d = (int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3
+        k = (r['Kernel_Name'], (int(r['Grid_Size_X']), int(r['Grid_Size_Y']), int(r['Grid_Size_Z'])))
+        by_kg.setdefault(k, []).append(d)
+        meta[k] = (r['Workgroup_Size_X'], r['VGPR_Count'], r['Accum_VGPR_Count'], r['LDS_Block_Size'])
+    tot = sum(sum(v) for v in by_kg.values())
+    out = [f'# {title}', '', 'Command (repo root, one MI355X):', '', '```', cmd, '```', '']
+    if desc:
+        out += [desc, '']
+    out += ['| kernel | grid (work-items x,y,z) | wg | vgpr | agpr | lds B | calls | median us | mean us | time % |',
+            '|---|---|---|---|---|---|---|---|---|---|']
+    for (k, g), v in sorted(by_kg.items(), key=lambda kv: -sum(kv[1])):
+        if sum(v) / tot < 0.002:
+            continue
+        wg, vg, ag, lds = meta[(k, g)]
+        name = k if len(k) < 90 else k[:87] + '...'
+        out.append(f'| `{name}` | {g} | {wg} | {vg} | {ag} | {lds} | {len(v)} | {statistics.median(v):.2f} | '
+                   f'{statistics.mean(v):.2f} | {100 * sum(v) / tot:.1f} |')
+    print('\n'.join(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -339,7 +366,12 @@ def main():
                     help='print the per-kernel counter table from a kernel trace and three --pmc CSVs')
     ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
                     help='compute profiles/dsc0_traffic.json from the two --pmc counter CSVs')
+    ap.add_argument('--trace-md', nargs='+', metavar='ARG',
+                    help='TRACE_CSV TITLE COMMAND [DESCRIPTION]: print the markdown summary of a kernel trace')
     args = ap.parse_args()
+    if args.trace_md:
+        trace_md(*args.trace_md)
+        return
     if args.traffic_from:
         traffic_from(*args.traffic_from)
         return

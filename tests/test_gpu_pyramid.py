@@ -6,6 +6,9 @@ The partial-sum buffers are filled with NaN first: every slice the consumer
 reads (all ntx row slices of a pooled row, all nty column slices of a pooled
 column, including tiles that hold no row of a coarse branch) must be written,
 and the slices must add up to the branch output's row and column sums.
+Shapes cover ragged tiles: (21, 70) has a last tile row band with no pooled row of
+branch 1 (its column partials must be zeros); (13, 66) has a last tile column with no
+column of branch 2 (its row partial must be written, as zero).
 Tolerances: fp32 1e-4 relative; fp16/bf16 1e-2 (outputs) and 2e-2 relative
 (sums of up to W values)."""
 import pytest
@@ -20,7 +23,7 @@ DT = {'f32': torch.float32, 'f16': torch.float16, 'bf16': torch.bfloat16}
 
 
 @pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
-@pytest.mark.parametrize('shape', [(2, 48, 37, 29), (1, 40, 21, 70), (2, 24, 8, 8)])
+@pytest.mark.parametrize('shape', [(2, 48, 37, 29), (1, 40, 21, 70), (2, 24, 8, 8), (1, 24, 13, 66)])
 def test_pyramid_proj_and_partial_sums(dt, shape):
     from kadconv import _ext
     dtype = DT[dt]

@@ -46,18 +46,35 @@ __global__ __launch_bounds__(KD_THREADS) void kaddown_prep_kernel(const T* __res
   if constexpr (VEC) {  // two outputs per step from 4-element input pieces, 2-element output pairs
     typedef T t4 __attribute__((ext_vector_type(4)));
     typedef T t2 __attribute__((ext_vector_type(2)));
-    for (int t = tid; t < P / 2; t += KD_THREADS) {
-      const int i = 2 * t, y = i / Wo, xo = i - y * Wo;
-      const t4 r0 = *(const t4*)(xp + (2 * y) * W + 2 * xo);
-      const t4 r1 = *(const t4*)(xp + (2 * y + 1) * W + 2 * xo);
-      const float v0 = 0.25f * ((to_f32(r0[0]) + to_f32(r0[1])) + (to_f32(r1[0]) + to_f32(r1[1])));
-      const float v1 = 0.25f * ((to_f32(r0[2]) + to_f32(r0[3])) + (to_f32(r1[2]) + to_f32(r1[3])));
-      p2[i] = v0;
-      p2[i + 1] = v1;
-      t2 o;
-      o[0] = from_f32<T>(v0);
-      o[1] = from_f32<T>(v1);
-      *(t2*)(ub + i) = o;
+    // batches of KU steps per thread: every load of a batch is issued before the first use
+    // (one round trip per batch; a 100 x 100 plane is one batch)
+    constexpr int KU = 8;
+    for (int t0 = tid; t0 < P / 2; t0 += KU * KD_THREADS) {
+      t4 r0[KU], r1[KU];
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        const int t = t0 + u * KD_THREADS;
+        if (t < P / 2) {
+          const int i = 2 * t, y = i / Wo, xo = i - y * Wo;
+          r0[u] = *(const t4*)(xp + (2 * y) * W + 2 * xo);
+          r1[u] = *(const t4*)(xp + (2 * y + 1) * W + 2 * xo);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        const int t = t0 + u * KD_THREADS;
+        if (t < P / 2) {
+          const int i = 2 * t;
+          const float v0 = 0.25f * ((to_f32(r0[u][0]) + to_f32(r0[u][1])) + (to_f32(r1[u][0]) + to_f32(r1[u][1])));
+          const float v1 = 0.25f * ((to_f32(r0[u][2]) + to_f32(r0[u][3])) + (to_f32(r1[u][2]) + to_f32(r1[u][3])));
+          p2[i] = v0;
+          p2[i + 1] = v1;
+          t2 o;
+          o[0] = from_f32<T>(v0);
+          o[1] = from_f32<T>(v1);
+          *(t2*)(ub + i) = o;
+        }
+      }
     }
   } else {
     for (int i = tid; i < P; i += KD_THREADS) {

@@ -45,19 +45,29 @@ __global__ __launch_bounds__(256) void se_pool_flat_kernel(const T* x, float* g,
   const int pe = pb + 4 < planes ? pb + 4 : planes;
   const int v_lo = pb * hw / 8, v_hi = (pe * hw + 7) / 8;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int v = v_lo + lane; v < v_hi; v += 64) {
-    const int e0 = v * 8;
-    const t8 xv = *(const t8*)(x + e0);
-    const int p0 = e0 / hw, nb = (p0 + 1) * hw - e0;  // elements of the piece in plane p0
-    float s0 = 0.f, s1 = 0.f;
+  // batches of KU pieces per lane: every load of a batch is issued before the first use
+  constexpr int KU = 8;
+  for (int vb = v_lo + lane; vb < v_hi; vb += 64 * KU) {
+    t8 xv[KU];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float xk = to_f32(xv[k]);
-      if (k < nb) s0 += xk; else s1 += xk;
+    for (int u = 0; u < KU; ++u)
+      if (vb + 64 * u < v_hi) xv[u] = *(const t8*)(x + (vb + 64 * u) * 8);
+#pragma unroll
+    for (int u = 0; u < KU; ++u) {
+      const int v = vb + 64 * u;
+      if (v >= v_hi) continue;
+      const int e0 = v * 8;
+      const int p0 = e0 / hw, nb = (p0 + 1) * hw - e0;  // elements of the piece in plane p0
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float xk = to_f32(xv[u][k]);
+        if (k < nb) s0 += xk; else s1 += xk;
+      }
+      const int k0 = p0 - pb;  // -1 .. 3; parts of planes outside [pb, pe) belong to other waves
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[k] += (k == k0 ? s0 : 0.f) + (k == k0 + 1 ? s1 : 0.f);
     }
-    const int k0 = p0 - pb;  // -1 .. 3; parts of planes outside [pb, pe) belong to other waves
-#pragma unroll
-    for (int k = 0; k < 4; ++k) acc[k] += (k == k0 ? s0 : 0.f) + (k == k0 + 1 ? s1 : 0.f);
   }
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -961,7 +971,7 @@ extern "C" int kad_channel_scale(const void* x, const float* att, void* out, int
 template <typename T>
 __global__ __launch_bounds__(256) void scale_residual_nchw_kernel(T* out, const float* att, const T* res, int c,
                                                                   int hw, int img_c, int c_off) {
-  constexpr int V = 16 / (int)sizeof(T), UNR = 4;
+  constexpr int V = 16 / (int)sizeof(T), UNR = 8;  // a 10^4-pixel 16-bit plane is one batch per thread
   const int plane = blockIdx.x, n = plane / c, j = plane - n * c;
   const float at = att[plane];
   const int64_t base = ((int64_t)n * img_c + c_off + j) * hw;

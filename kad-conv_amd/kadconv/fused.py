@@ -29,6 +29,10 @@ import torch
 from . import _ext
 
 
+DCN_BLOCK_COLS = 128  # output channels per block of the DCN kernels (8 MFMA column fragments)
+SPLIT_MIN_TILES = 128  # tiles per launch from which a separate offset conv pays (half the CUs)
+
+
 def _f32(t):
     return None if t is None else t.detach().to(torch.float32).contiguous()
 
@@ -123,6 +127,19 @@ class DSCPlan:
             st.append(('lcsa_mask' + tag, lambda: _ext.lcsa_mask(arow, colm, self.lcsa, emat, ebias, mask, n,
                                                                  self.cin, h, w, ks, work)))
         b = self.bias if bias is None else bias
+        if self.cout > DCN_BLOCK_COLS and se is None and n * _ext.dcn_tiles(h, w) >= SPLIT_MIN_TILES:
+            # several 128-channel column blocks per tile: conv_offset once per tile (a plain 3x3 conv
+            # into an fp32 [N, h, w, 18] map), then the deformable conv reading those offsets, instead
+            # of every column block of the fused kernel recomputing the same offsets.  With few tiles
+            # the separate offset launch occupies few CUs and costs more than it saves (measured:
+            # [8,256,50,50] 166 -> 158 us split; [8,512,25,25], 40 tiles, 153 -> 156 us).
+            off = torch.empty(n, h, w, 18, dtype=torch.float32, device=dev)
+            st.append(('conv_offset' + tag, lambda: _ext.conv3x3_fwd(y, self.cin, owp, 18, off, bias=self.off_b)))
+            st.append(('dsc' + tag, lambda: _ext.dcn_fwd(
+                y, self.cin, off, (P * 18, 18, 1), mask, (P * 9, 9, 1), wp, self.cout, out, bias=b,
+                post_mul=post_mul, post_add=post_add, post_scale=post_scale, relu=relu, out_layout=out_layout,
+                gap_partial=gap)))
+            return st
         # conv_offset + deformable conv in one kernel: the offsets stay on chip
         st.append(('dsc' + tag, lambda: _ext.dsc_fwd(
             y, self.cin, owp, self.off_b, mask, (P * 9, 9, 1), wp, self.cout, out, bias=b, post_mul=post_mul,

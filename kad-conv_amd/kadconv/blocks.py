@@ -124,6 +124,8 @@ class KADDown(nn.Module):
             b = sum(a[i] * self.proj[i].bias.detach().float() for i in range(self.n))
             self._packed = {key: (_ext.gemm_pack_weights(w * g[:, None], dtype), (g * b).contiguous())}
         wpack, bias = self._packed[key]
+        if N == 0:  # nothing to compute: the empty result
+            return torch.empty(N, c2, H // 2, W // 2, dtype=dtype, device=x.device)
         u = torch.empty(N, self.n * C, H // 2, W // 2, dtype=dtype, device=x.device)
         _ext.kaddown_prep(x.contiguous(), u, self.n)
         out = torch.empty(N, c2, H // 2, W // 2, dtype=dtype, device=x.device)

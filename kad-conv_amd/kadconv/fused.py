@@ -205,7 +205,7 @@ class KADConvPlan:
     def eligible(self, x):
         if not (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float16, torch.bfloat16)):
             return False
-        if x.shape[1] != self.dim:
+        if x.shape[1] != self.dim or x.shape[0] == 0:  # an empty batch takes the module's own forward
             return False
         s = 2 ** (self.n - 1)
         return x.shape[2] >= s and x.shape[3] >= s

@@ -62,6 +62,8 @@ def deform_conv2d(input, offset, weight, bias=None, stride=1, padding=0, dilatio
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (input, offset, weight, bias, mask)):
         raise NotImplementedError('kadconv HIP kernels are inference-only (no backward)')
     dtype = input.dtype
+    if N == 0 or Ho <= 0 or Wo <= 0:  # nothing to compute: the empty result, as torchvision returns it
+        return input.new_empty(N, Co, max(Ho, 0), max(Wo, 0))
     x, _ = _nhwc_view(input)
     P = Ho * Wo
     off = offset.to(torch.float32).contiguous()
@@ -89,6 +91,9 @@ def conv1x1(x, weight, bias=None, act=None, pool=1, wpack=None):
     b = bias.detach().to(torch.float32).contiguous() if bias is not None else None
     a = {None: 0, 'silu': 1}[act]
     Hp, Wp = H // pool, W // pool
+    if N * Hp * Wp == 0:  # nothing to compute: the empty result
+        mf = torch.channels_last if x.is_contiguous(memory_format=torch.channels_last) else torch.contiguous_format
+        return torch.empty(N, Co, Hp, Wp, dtype=dtype, device=x.device, memory_format=mf)
     if x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous():
         out = torch.empty(N, Co, Hp, Wp, dtype=dtype, device=x.device, memory_format=torch.channels_last)
         _ext.gemm1x1_fwd(x.permute(0, 2, 3, 1), _ext.KAD_NHWC, C, wpack, Co, out.permute(0, 2, 3, 1),
@@ -104,6 +109,8 @@ def squeeze_excitation(x, w1, b1, w2, b2):
     if not x.is_cuda:
         raise ValueError('kadconv.ops.squeeze_excitation needs a GPU tensor')
     N, C, H, W = x.shape
+    if N == 0:  # nothing to compute: the empty result
+        return torch.empty_like(x)
     hid = w1.shape[0]
     def f32(t):  # fp32 contiguous tensors are used as they are (no per-call copy)
         return t if (t.dtype == torch.float32 and t.is_contiguous()) else t.detach().float().contiguous()

@@ -343,18 +343,21 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
     const int ch = c0 + gq * 8;
     const floatx4 al0 = *(const floatx4*)&s_alpha[col][ch], al1 = *(const floatx4*)&s_alpha[col][ch + 4];
     const floatx4 be0 = *(const floatx4*)&s_beta[col][ch], be1 = *(const floatx4*)&s_beta[col][ch + 4];
+    [[maybe_unused]] const half8_t alh =
+        __builtin_convertvector(__builtin_shufflevector(al0, al1, 0, 1, 2, 3, 4, 5, 6, 7), half8_t);
+    [[maybe_unused]] const half8_t beh =
+        __builtin_convertvector(__builtin_shufflevector(be0, be1, 0, 1, 2, 3, 4, 5, 6, 7), half8_t);
     for (int r = r0; r < LM_UR; r += LM_THREADS / (4 * LM_TW)) {
       const int gy = h0 - HALF_BAND + r;
       const bool rv = gy >= 0 && gy < h;
       const floatx4 a0 = *(const floatx4*)&s_a[r][ch], a1 = *(const floatx4*)&s_a[r][ch + 4];
       ET* dst = us + (r * LM_TW + col) * LDU + gq * 8;
       if constexpr (sizeof(ET) == 2) {
-        half8_t v;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[j] = (half_t)(rv ? fmaxf(al0[j] * a0[j] + be0[j], 0.f) : 0.f);
-          v[j + 4] = (half_t)(rv ? fmaxf(al1[j] * a1[j] + be1[j], 0.f) : 0.f);
-        }
+        // packed fp16 (two values per v_pk_fma_f16 / v_pk_max_f16): u is stored in fp16 anyway;
+        // alpha, a and beta rounded to fp16 first move it by a few fp16 ulps
+        const half8_t ah = __builtin_convertvector(__builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7), half8_t);
+        half8_t v = __builtin_elementwise_max(alh * ah + beh, (half8_t)(half_t)0);
+        if (!rv) v = (half8_t)(half_t)0;
         *(half8_t*)dst = v;
       } else {
         floatx4 v0, v1;

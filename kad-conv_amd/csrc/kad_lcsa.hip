@@ -311,19 +311,26 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
         for (int j = 0; j < 4 + BAND - 1; ++j) cm[j] = s_col[qc * 4 + j][ch];
         const bool chok = ch < nsc && cs + ch < c;
         const float bna = s_bna[ch], bb = s_b1[ch], bnb = s_bnb[ch];
+        // 1 / 0: window column j (image column w0 + 4 qc - 5 + j) inside / outside the image.
+        // S sums the in-image taps as fma(wk, ind, S): S + wk * 1 and S + wk * 0 round exactly
+        // like S + wk and S + 0 (finite weights), with one instruction per tap instead of three.
+        float ind[4 + BAND - 1];
+#pragma unroll
+        for (int j = 0; j < 4 + BAND - 1; ++j) {
+          const int xx = w0 + qc * 4 - HALF_BAND + j;
+          ind[j] = (xx >= 0 && xx < w) ? 1.f : 0.f;
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int col = qc * 4 + q, gx = w0 + col;
           float S0 = 0.f, S1 = 0.f, B0 = 0.f, B1 = 0.f;  // even / odd taps, added last
 #pragma unroll
           for (int k = 0; k < BAND; ++k) {
-            const int xx = gx + k - HALF_BAND;
-            const float m = (xx >= 0 && xx < w) ? wk[k] : 0.f;
             if (k & 1) {
-              S1 += m;
+              S1 = fmaf(wk[k], ind[q + k], S1);
               B1 += wk[k] * cm[q + k];
             } else {
-              S0 += m;
+              S0 = fmaf(wk[k], ind[q + k], S0);
               B0 += wk[k] * cm[q + k];
             }
           }

@@ -162,6 +162,10 @@ __global__ __launch_bounds__(256) void lcsa_prep_kernel(const float* rows, int n
 }
 
 // ---- mask GEMM ------------------------------------------------------------------------------------
+// The mask's sigmoid, shared by the single and split paths: v_rcp_f32 (1 ulp)
+// instead of the IEEE division sequence (about ten instructions per value).
+__device__ __forceinline__ float mask_sigmoid(float v) { return __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
 constexpr int LM_TH = 16, LM_TW = 16;                   // output tile
 constexpr int LM_UR = LM_TH + 2 * HALF_BAND;            // u rows staged
 constexpr int LM_THREADS = 256;
@@ -405,7 +409,7 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
       const int j = grp * 4 + i;
       if (j >= 9) continue;
       if (ksplit == 1)
-        mask[(((int64_t)n * h + gy) * w + gx) * 9 + j] = sigmoidf_(acc[f][i] + eb[i]);
+        mask[(((int64_t)n * h + gy) * w + gx) * 9 + j] = mask_sigmoid(acc[f][i] + eb[i]);
       else  // raw logits of this split; lcsa_mask_reduce_kernel adds the splits up
         part[((((int64_t)sp * gridDim.z / ksplit + n) * h + gy) * w + gx) * 9 + j] = acc[f][i];
     }
@@ -419,7 +423,7 @@ __global__ __launch_bounds__(256) void lcsa_mask_reduce_kernel(const float* part
   if (i >= total) return;
   float v = 0.f;
   for (int s = 0; s < ksplit; ++s) v += part[s * total + i];
-  mask[i] = sigmoidf_(v + ebias[i % 9]);
+  mask[i] = mask_sigmoid(v + ebias[i % 9]);
 }
 
 }  // namespace kad

@@ -274,9 +274,12 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
   _Pragma("unroll") for (int k = 0; k < BAND; ++k) ef[k] =                                                     \
       LmFrag<ET>::ld(emat + (int64_t)(l16 * BAND + k) * cp + (KC) * 32 + grp * 8);
 #define LM_LDS_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
+  // logit biases, read in the epilogue after many barriers; loaded first, so that their LDS
+  // store waits for this load only, not for the group's and the E fragments' loads behind it
+  const float ebv = tid < 9 ? ebias[tid] : 0.f;
   LM_LOAD_GROUP((kc0 / CPG) * LM_SC);
   LM_LOAD_E(kc0);
-  if (tid < 16) s_eb[tid] = tid < 9 ? ebias[tid] : 0.f;  // read in the epilogue, after many barriers
+  if (tid < 16) s_eb[tid] = ebv;
   for (int kc = kc0; kc < kc1; ++kc) {
     const int g = kc / CPG, c0 = (kc - g * CPG) * 32, cs = g * LM_SC;
     if (c0 == 0 || kc == kc0) {  // first chunk of a group (or of the split): stage it, request the next one

@@ -78,16 +78,9 @@ def time_eager(fn, steps, warmup=3):
 
 
 def metric_state(dim, seed=0):
-    """Synthetic weights of the metric's layer as the workload spec defines
-    them: kaiming-uniform convolutions and biases by state-dict name (seed 0),
-    conv_offset ~ N(0, 2 / sqrt(9 c)) with zero bias (offsets ~2 px per unit of
-    input scale), identity branch BatchNorm, branch scale 1."""
-    from oracle import kadconv_oracle as O
-    sd = O.make_kadconv_state(dim, seed=seed, offset_std_px=2.0, bn_random=False)
-    for k in list(sd):
-        if k.startswith('weight.'):
-            sd[k] = torch.ones_like(sd[k])
-    return sd
+    """Synthetic weights of the metric's layer (kadconv.synthetic.make_metric_kadconv_state)."""
+    from kadconv import synthetic as S
+    return S.make_metric_kadconv_state(dim, seed=seed)
 
 
 def build_kadconv(dim, dtype, seed=0):
@@ -134,14 +127,14 @@ def cpu_baseline(shape, runs=5, warmup=2):
 def per_op_workloads():
     """The other BASELINE configs as (name, launch, floor_us) with seeded inputs and weights."""
     import kadconv
-    from oracle import kadconv_oracle as O
+    from kadconv import synthetic as S
     out = []
     g = torch.Generator().manual_seed(0)
     dt = torch.float16
     # config 2: DSC(C, C) at the neck scales
     for C, H in [(128, 100), (256, 50), (512, 25)]:
         d = kadconv.DSC(C, C)
-        d.load_state_dict(O.make_dsc_state(C, C, seed=C, offset_std_px=2.0), strict=False)
+        d.load_state_dict(S.make_dsc_state(C, C, seed=C, offset_std_px=2.0), strict=False)
         d = d.to('cuda', dt).eval()
         kadconv.enable_fast_inference(d)
         x = torch.randn(8, C, H, H, generator=g).to('cuda', dt)
@@ -150,7 +143,7 @@ def per_op_workloads():
         out.append((f'dsc_{C}x{H}', lambda d=d, x=x: d(x), max(fl / PEAK_MFMA_F16, by / PEAK_HBM) * 1e6))
     # config 3: KADDown [8,256,100,100] -> [8,512,50,50]
     m = kadconv.KADDown(256, 512)
-    m.load_state_dict(O.make_kaddown_state(256, 512))
+    m.load_state_dict(S.make_kaddown_state(256, 512))
     m = m.to('cuda', dt).eval()
     x = torch.randn(8, 256, 100, 100, generator=g).to('cuda', dt)
     out.append(('kaddown_256to512_100', lambda m=m, x=x: m(x), max(6.86e9 / PEAK_MFMA_F16, 61.44e6 / PEAK_HBM) * 1e6))

@@ -98,8 +98,19 @@ class KADDown(nn.Module):
             z = z + a[i] * b
         return z * torch.sigmoid(self.gate).view(1, -1, 1, 1)
 
+    # kad_kaddown_prep keeps a plane's 2x2, 4x4 and 8x8 means in LDS as fp32 (160 KB per CU)
+    _PREP_LDS = 160 * 1024
+
+    def _hip_eligible(self, x):
+        H, W = x.shape[2:]
+        pools = (H // 2) * (W // 2) + (H // 4) * (W // 4) + (H // 8) * (W // 8)
+        return (_use_hip(self, x) and 1 <= self.n <= 3 and H >= 2 ** self.n and W >= 2 ** self.n
+                and 4 * pools <= self._PREP_LDS)
+
     def forward(self, x):
-        if not _use_hip(self, x):
+        # inputs the one-pass kernel does not cover (n > 3 branches, planes whose pools exceed
+        # its LDS staging, images smaller than the deepest pool) take the plain composition
+        if not self._hip_eligible(x):
             return self._plain(x)
         with torch.no_grad():
             return self._fast(x)

@@ -279,11 +279,16 @@ class KADConvPlan:
         return st, chains, [], out
 
     def _se_counters(self, dev, i, n):
-        """Per-image arrival counters of branch i's fused SE (zero between calls), kept per device."""
+        """Per-image arrival counters of branch i's fused SE (zero between calls), kept per device.
+        A larger batch gets a new buffer, but the old one stays alive with the plan: a HIP graph
+        captured earlier holds its address and its replays keep using it.  Forwards of one layer
+        that overlap on the GPU (several streams) share these counters and must not run concurrently."""
         key = (torch.device(dev).index, i)
         counters = getattr(self, '_se_count', {})
         c = counters.get(key)
         if c is None or c.numel() < n:
+            if c is not None:
+                self.__dict__.setdefault('_se_retired', []).append(c)
             c = torch.zeros(max(n, 1), dtype=torch.int32, device=dev)
             counters[key] = c
             self._se_count = counters

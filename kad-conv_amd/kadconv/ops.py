@@ -2,8 +2,8 @@
 
 * ``deform_conv2d`` -- drop-in for ``torchvision.ops.deform_conv2d`` (the call
   at KAD-Conv/kadconv/kad_conv.py:66-67) for 3x3 kernels, one offset group,
-  dilation 1.  GPU tensors run the gfx950 HIP kernel; CPU tensors are handed to
-  torchvision when it is importable (the reference's own CPU path).
+  dilation 1.  GPU tensors run the gfx950 HIP kernel; CPU tensors run a
+  plain-torch im2col restatement (any kernel size, stride, dilation).
 * ``conv1x1`` -- 1x1 conv + bias + optional SiLU, optional input avg-pool
   (north-star piece 3; KAD-CNet ``Conv`` after Conv-BN fusion).
 * ``squeeze_excitation`` -- SE block: GAP, FC-ReLU-FC-sigmoid, channel scale.
@@ -12,6 +12,7 @@ GPU entry points never fall back to another implementation: if the HIP library
 is missing they raise ``kadconv._ext.KadExtensionError``.
 """
 import torch
+import torch.nn.functional as F
 
 from . import _ext
 
@@ -33,17 +34,70 @@ def _pair(v):
     return (v, v) if isinstance(v, int) else tuple(v)
 
 
+def _deform_conv2d_cpu(x, offset, weight, bias, s, p, d, mask):
+    """Plain-torch modulated deformable convolution for CPU tensors (the
+    reference's CPU path is torchvision's operator, absent here).
+
+    Sampling rule of torchvision (restated at acceleration/kadc_dcn_direct.py:57-107):
+    a sample at (py, px) is 0 if py <= -1, py >= H, px <= -1 or px >= W;
+    otherwise the four corners around floor(p) are blended and corners
+    outside the image read 0.  Here the image is zero-padded by one pixel on
+    every side, so for every live sample all four corners (rows floor(py)
+    and floor(py) + 1 in [-1, H]) index the padded image and the outside
+    corners read the padding: one flat gather per corner, no per-corner
+    validity.  The columns [N, Cin * KH * KW, P] then meet the weights in one
+    batched matmul (im2col, the torchvision strategy)."""
+    N, C, H, W = x.shape
+    Co, Ci, KH, KW = weight.shape
+    Ho, Wo = offset.shape[2:]
+    K = KH * KW
+    dt = x.dtype
+    xp = F.pad(x, (1, 1, 1, 1)).reshape(N, C, (H + 2) * (W + 2))
+    base_y = (torch.arange(Ho, dtype=dt) * s[0] - p[0]).view(1, 1, Ho, 1)
+    base_x = (torch.arange(Wo, dtype=dt) * s[1] - p[1]).view(1, 1, 1, Wo)
+    ky = (torch.arange(K) // KW).to(dt).view(1, K, 1, 1) * d[0]
+    kx = (torch.arange(K) % KW).to(dt).view(1, K, 1, 1) * d[1]
+    off = offset.reshape(N, K, 2, Ho, Wo)
+    py = base_y + ky + off[:, :, 0]                     # [N, K, Ho, Wo]
+    px = base_x + kx + off[:, :, 1]
+    live = (py > -1) & (py < H) & (px > -1) & (px < W)
+    py = torch.where(live, py, torch.zeros_like(py))    # dead samples: any in-range position, weight 0
+    px = torch.where(live, px, torch.zeros_like(px))
+    fy, fx = torch.floor(py), torch.floor(px)
+    ly, lx = py - fy, px - fx
+    r0 = fy.long() + 1                                  # padded row of floor(py), in [0, H]
+    c0 = fx.long() + 1
+    gain = live.to(dt) if mask is None else live.to(dt) * mask.reshape(N, K, Ho, Wo)
+    cols = x.new_zeros(N, C, K * Ho * Wo)
+    for dy, dx, wgt in ((0, 0, (1 - ly) * (1 - lx)), (0, 1, (1 - ly) * lx), (1, 0, ly * (1 - lx)), (1, 1, ly * lx)):
+        idx = ((r0 + dy) * (W + 2) + (c0 + dx)).reshape(N, 1, -1).expand(N, C, -1)
+        cols += torch.gather(xp, 2, idx) * (wgt * gain).reshape(N, 1, -1)
+    cols = cols.reshape(N, C * K, Ho * Wo)               # row ci * K + k: weight's [Ci][KH][KW] order
+    out = torch.matmul(weight.reshape(Co, Ci * K), cols)
+    if bias is not None:
+        out = out + bias.view(1, Co, 1)
+    return out.reshape(N, Co, Ho, Wo)
+
+
 def deform_conv2d(input, offset, weight, bias=None, stride=1, padding=0, dilation=1, mask=None):
-    """Modulated deformable convolution with torchvision's signature and semantics."""
+    """Modulated deformable convolution with torchvision's signature and semantics.
+    GPU tensors run the gfx950 HIP kernel; CPU tensors run a plain-torch
+    restatement of the same sampling rule (the reference's CPU path is
+    torchvision's operator, which this image does not ship)."""
     if not input.is_cuda:
-        try:
-            import torchvision  # noqa: F401  (the reference's CPU operator)
-        except ImportError:
-            raise RuntimeError('kadconv.ops.deform_conv2d runs on the GPU (gfx950 HIP kernel); for CPU tensors '
-                               'it needs torchvision.ops.deform_conv2d, which is not installed') from None
-        import torchvision.ops
-        return torchvision.ops.deform_conv2d(input, offset, weight, bias, stride=stride, padding=padding,
-                                             dilation=dilation, mask=mask)
+        s, p, d = _pair(stride), _pair(padding), _pair(dilation)
+        if input.dim() != 4 or weight.dim() != 4 or weight.shape[1] != input.shape[1]:
+            raise ValueError('input [N, C, H, W] and weight [Cout, C, KH, KW] (one weight group) expected')
+        KH, KW = weight.shape[2:]
+        Ho = (input.shape[2] + 2 * p[0] - d[0] * (KH - 1) - 1) // s[0] + 1
+        Wo = (input.shape[3] + 2 * p[1] - d[1] * (KW - 1) - 1) // s[1] + 1
+        if tuple(offset.shape) != (input.shape[0], 2 * KH * KW, Ho, Wo):
+            raise ValueError(f'offset shape {tuple(offset.shape)} != {(input.shape[0], 2 * KH * KW, Ho, Wo)}')
+        if mask is not None and tuple(mask.shape) != (input.shape[0], KH * KW, Ho, Wo):
+            raise ValueError(f'mask shape {tuple(mask.shape)} != {(input.shape[0], KH * KW, Ho, Wo)}')
+        return _deform_conv2d_cpu(input, offset.to(input.dtype), weight.to(input.dtype),
+                                  None if bias is None else bias.to(input.dtype), s, p, d,
+                                  None if mask is None else mask.to(input.dtype))
     s, p, d = _pair(stride), _pair(padding), _pair(dilation)
     if input.dim() != 4 or weight.dim() != 4:
         raise ValueError('input and weight must be 4-D')

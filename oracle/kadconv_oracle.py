@@ -28,8 +28,6 @@ builder-defined operator with no counterpart in the reference) is pinned by
 its closed-form collapse to a single 1x1 convolution when the branches share
 weights and the input is constant per 8x8 block.
 """
-import math
-
 import torch
 import torch.nn.functional as F
 
@@ -232,91 +230,3 @@ def kaddown_forward(sd, x, n=3):
             b = F.interpolate(b, size=(Ho, Wo), mode='bilinear', align_corners=False)
         z = a[i] * b if z is None else z + a[i] * b
     return z * torch.sigmoid(sd['gate']).view(1, -1, 1, 1)
-
-
-# --------------------------------------------------------------------------- #
-# Seeded synthetic weights, generated by state-dict name so that the oracle and
-# the product module load identical values (no dependence on module RNG order).
-# --------------------------------------------------------------------------- #
-def _uniform(gen, shape, bound, dtype):
-    return (torch.rand(shape, generator=gen, dtype=torch.float64) * 2 - 1).mul(bound).to(dtype)
-
-
-def make_dsc_state(c_in, c_out, seed=0, offset_std_px=None, dtype=torch.float32, prefix=''):
-    """Kaiming-uniform weights for one DSC (bound 1/sqrt(fan_in), the
-    ``nn.Conv2d`` default); ``conv_offset`` is random too (the reference
-    zero-initialises it, kad_conv.py:60-61, which would make every offset 0).
-    With ``offset_std_px`` the offset weights are N(0, std/sqrt(9 c_in)) so that
-    offsets are ~N(0, std) px on unit-variance input."""
-    gen = torch.Generator().manual_seed(seed)
-    sd = {}
-    fan = 9 * c_in
-    sd[prefix + 'weight'] = _uniform(gen, (c_out, c_in, 3, 3), 1 / math.sqrt(fan), dtype)
-    sd[prefix + 'bias'] = _uniform(gen, (c_out,), 1 / math.sqrt(fan), dtype)
-    if offset_std_px is None:
-        sd[prefix + 'conv_offset.weight'] = _uniform(gen, (18, c_in, 3, 3), 1 / math.sqrt(fan), dtype)
-    else:
-        sd[prefix + 'conv_offset.weight'] = (torch.randn((18, c_in, 3, 3), generator=gen, dtype=torch.float64)
-                                            * (offset_std_px / math.sqrt(fan))).to(dtype)
-    sd[prefix + 'conv_offset.bias'] = _uniform(gen, (18,), 1 / math.sqrt(fan), dtype) * (
-        0 if offset_std_px is not None else 1)
-    r = prefix + 'RCA_mask.excite.'
-    sd[r + '0.weight'] = _uniform(gen, (c_in, 1, 1, 11), 1 / math.sqrt(11), dtype)
-    sd[r + '0.bias'] = _uniform(gen, (c_in,), 1 / math.sqrt(11), dtype)
-    sd[r + '1.weight'] = (1 + 0.1 * _uniform(gen, (c_in,), 1.0, torch.float64)).to(dtype)
-    sd[r + '1.bias'] = (0.1 * _uniform(gen, (c_in,), 1.0, torch.float64)).to(dtype)
-    sd[r + '1.running_mean'] = (0.1 * _uniform(gen, (c_in,), 1.0, torch.float64)).to(dtype)
-    sd[r + '1.running_var'] = (1 + 0.2 * _uniform(gen, (c_in,), 1.0, torch.float64)).to(dtype)
-    sd[r + '3.weight'] = _uniform(gen, (c_in, 1, 11, 1), 1 / math.sqrt(11), dtype)
-    sd[r + '3.bias'] = _uniform(gen, (c_in,), 1 / math.sqrt(11), dtype)
-    sd[r + '4.weight'] = _uniform(gen, (9, c_in, 1, 1), 1 / math.sqrt(c_in), dtype)
-    sd[r + '4.bias'] = _uniform(gen, (9,), 1 / math.sqrt(c_in), dtype)
-    return sd
-
-
-def make_kadconv_state(dim, n=3, se_min_hidden=32, seed=0, dtype=torch.float32, offset_std_px=None,
-                       bn_random=True):
-    """Synthetic KADConv state dict with the reference's key names
-    (kad_conv.py:96-110).  BN statistics are perturbed away from identity when
-    ``bn_random`` so that the folded epilogue is exercised."""
-    gen = torch.Generator().manual_seed(seed + 7919)
-    sd = {}
-    for i, c in enumerate(branch_widths(dim, n)):
-        p = f'convs.{i}.'
-        sd[p + '0.weight'] = _uniform(gen, (c, dim, 1, 1), 1 / math.sqrt(dim), dtype)
-        sd[p + '0.bias'] = _uniform(gen, (c,), 1 / math.sqrt(dim), dtype)
-        sd.update(make_dsc_state(c, c, seed=seed + 101 * (i + 1), dtype=dtype, prefix=p + '1.',
-                                 offset_std_px=offset_std_px))
-        bn = p + '2.'
-        if bn_random:
-            sd[bn + 'weight'] = (1 + 0.2 * _uniform(gen, (c,), 1.0, torch.float64)).to(dtype)
-            sd[bn + 'bias'] = (0.2 * _uniform(gen, (c,), 1.0, torch.float64)).to(dtype)
-            sd[bn + 'running_mean'] = (0.1 * _uniform(gen, (c,), 1.0, torch.float64)).to(dtype)
-            sd[bn + 'running_var'] = (1 + 0.3 * _uniform(gen, (c,), 1.0, torch.float64)).to(dtype)
-        else:
-            sd[bn + 'weight'] = torch.ones(c, dtype=dtype)
-            sd[bn + 'bias'] = torch.zeros(c, dtype=dtype)
-            sd[bn + 'running_mean'] = torch.zeros(c, dtype=dtype)
-            sd[bn + 'running_var'] = torch.ones(c, dtype=dtype)
-        h = max(se_min_hidden, c)
-        sd[f'fc.{i}.0.weight'] = _uniform(gen, (h, c), 1 / math.sqrt(c), dtype)
-        sd[f'fc.{i}.0.bias'] = _uniform(gen, (h,), 1 / math.sqrt(c), dtype)
-        sd[f'fc.{i}.2.weight'] = _uniform(gen, (c, h), 1 / math.sqrt(h), dtype)
-        sd[f'fc.{i}.2.bias'] = _uniform(gen, (c,), 1 / math.sqrt(h), dtype)
-        sd[f'weight.{i}.0.weight'] = (1 + 0.25 * _uniform(gen, (1, c, 1, 1), 1.0, torch.float64)).to(dtype)
-    return sd
-
-
-def make_kaddown_state(c1, c2, n=3, seed=0, dtype=torch.float32):
-    gen = torch.Generator().manual_seed(seed + 104729)
-    sd = {}
-    for i in range(n):
-        sd[f'proj.{i}.weight'] = _uniform(gen, (c2, c1, 1, 1), 1 / math.sqrt(c1), dtype)
-        sd[f'proj.{i}.bias'] = _uniform(gen, (c2,), 1 / math.sqrt(c1), dtype)
-    sd['alpha'] = torch.randn(n, generator=gen, dtype=torch.float64).to(dtype)
-    sd['gate'] = torch.randn(c2, generator=gen, dtype=torch.float64).to(dtype)
-    return sd
-
-
-def cast_state(sd, dtype):
-    return {k: (v.to(dtype) if v.is_floating_point() else v) for k, v in sd.items()}

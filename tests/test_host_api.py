@@ -7,6 +7,7 @@ import torch.nn as nn
 
 import kadconv
 from kadconv import fast
+from kadconv import synthetic as S
 from oracle import kadconv_oracle as O
 
 
@@ -17,7 +18,7 @@ def test_public_api_names():
 
 def test_state_dict_keys_match_oracle_layout():
     m = kadconv.KADConv(256, se_min_hidden=64)
-    sd = O.make_kadconv_state(256, se_min_hidden=64)
+    sd = S.make_kadconv_state(256, se_min_hidden=64)
     ours = {k for k in m.state_dict() if not k.endswith('num_batches_tracked')}
     assert ours == set(sd)
     for k, v in sd.items():
@@ -67,20 +68,19 @@ def test_disable_removes_instance_forward():
     assert 'forward' not in vars(m)
 
 
-def test_cpu_deform_without_torchvision_raises_clearly():
-    try:
-        import torchvision  # noqa: F401
-        pytest.skip('torchvision present: the CPU path delegates to it')
-    except ImportError:
-        pass
+def test_cpu_deform_rejects_bad_shapes():
+    """The CPU deformable conv checks offset and mask shapes as torchvision does."""
     x = torch.randn(1, 4, 5, 5)
-    with pytest.raises(RuntimeError, match='torchvision'):
-        kadconv.deform_conv2d(x, torch.zeros(1, 18, 5, 5), torch.zeros(4, 4, 3, 3), padding=1)
+    with pytest.raises(ValueError, match='offset shape'):
+        kadconv.deform_conv2d(x, torch.zeros(1, 9, 5, 5), torch.zeros(4, 4, 3, 3), padding=1)
+    with pytest.raises(ValueError, match='mask shape'):
+        kadconv.deform_conv2d(x, torch.zeros(1, 18, 5, 5), torch.zeros(4, 4, 3, 3), padding=1,
+                              mask=torch.zeros(1, 8, 5, 5))
 
 
 def test_kaddown_plain_matches_oracle_on_cpu():
     m = kadconv.KADDown(6, 10)
-    sd = O.make_kaddown_state(6, 10, seed=3)
+    sd = S.make_kaddown_state(6, 10, seed=3)
     m.load_state_dict(sd)
     x = torch.randn(2, 6, 24, 16)
     with torch.no_grad():

@@ -12,6 +12,7 @@ import numpy as np
 import torch
 import torch.nn as nn
 
+from kadconv import synthetic as S
 from oracle import kadconv_oracle as O
 
 
@@ -54,7 +55,7 @@ def _lcsa_closed_form(sd, prefix, x):
 
 
 def test_lcsa_matches_separable_closed_form():
-    sd = O.make_dsc_state(6, 6, seed=3, dtype=torch.float64)
+    sd = S.make_dsc_state(6, 6, seed=3, dtype=torch.float64)
     x = torch.randn(2, 6, 13, 9, generator=torch.Generator().manual_seed(1), dtype=torch.float64)
     got = O.lcsa_forward(sd, 'RCA_mask.', x)
     ref = _lcsa_closed_form(sd, 'RCA_mask.', x)
@@ -92,7 +93,7 @@ class _DSCProbe(nn.Module):
 
 def test_kadconv_one_branch_matches_module_composition():
     dim = 5
-    sd = O.make_kadconv_state(dim, n=1, se_min_hidden=8, seed=2, dtype=torch.float64)
+    sd = S.make_kadconv_state(dim, n=1, se_min_hidden=8, seed=2, dtype=torch.float64)
     conv = nn.Sequential(nn.Conv2d(dim, dim, 1), _DSCProbe(dim), nn.BatchNorm2d(dim, eps=1e-3), nn.ReLU())
     fc = nn.Sequential(nn.Linear(dim, 8), nn.ReLU(), nn.Linear(8, dim), nn.Sigmoid())
     holder = nn.Module()
@@ -111,7 +112,7 @@ def test_kadconv_one_branch_matches_module_composition():
 
 
 def test_kadconv_state_keys_match_reference_layout():
-    sd = O.make_kadconv_state(64)
+    sd = S.make_kadconv_state(64)
     assert O.branch_widths(64) == [22, 21, 21]
     assert O.branch_widths(256) == [86, 85, 85]
     for i, c in enumerate([22, 21, 21]):
@@ -130,7 +131,7 @@ def test_kaddown_collapses_to_single_conv_on_blockwise_constant_input():
     # pyramid level upsamples back to the same map, so the softmax mixture
     # reduces to one 1x1 convolution of the 2x2-pooled input, gated.
     c1, c2 = 4, 6
-    sd = O.make_kaddown_state(c1, c2, seed=1, dtype=torch.float64)
+    sd = S.make_kaddown_state(c1, c2, seed=1, dtype=torch.float64)
     for i in (1, 2):
         sd[f'proj.{i}.weight'] = sd['proj.0.weight'].clone()
         sd[f'proj.{i}.bias'] = sd['proj.0.bias'].clone()
@@ -141,3 +142,94 @@ def test_kaddown_collapses_to_single_conv_on_blockwise_constant_input():
     ref = torch.nn.functional.conv2d(x[:, :, ::2, ::2], sd['proj.0.weight'], sd['proj.0.bias'])
     ref = ref * torch.sigmoid(sd['gate']).view(1, -1, 1, 1)
     assert torch.allclose(got, ref, atol=1e-12, rtol=0)
+
+
+def _sigmoid(v):
+    return 1.0 / (1.0 + np.exp(-v))
+
+
+def test_kadconv_three_branches_zero_dsc_weights_give_constant_branches():
+    """n = 3 pin of the concat order and widths, residual, BN, ReLU, branch scale
+    and SE MLP: with every DSC weight 0 the DSC returns its bias, so branch i is
+    the per-channel constant v_i = scale * relu(bn(bias_i)), gated by
+    att_i = sigmoid(W2 relu(W1 v_i + b1) + b2) (the mean of a constant map is the
+    constant; its bilinear upsample is the same constant).  Expected output:
+    cat_i(v_i * att_i) + x, computed here with numpy from the state dict."""
+    dim = 14
+    sd = S.make_kadconv_state(dim, seed=5, dtype=torch.float64)
+    for i in range(3):
+        sd[f'convs.{i}.1.weight'].zero_()
+    x = torch.randn(2, dim, 12, 16, generator=torch.Generator().manual_seed(6), dtype=torch.float64)
+    got = O.kadconv_forward(sd, x)
+    consts = []
+    for i, c in enumerate(O.branch_widths(dim)):
+        p = f'convs.{i}.'
+        n = lambda k: sd[k].numpy().reshape(-1)  # noqa: E731
+        t = (n(p + '1.bias') - n(p + '2.running_mean')) / np.sqrt(n(p + '2.running_var') + 1e-3) \
+            * n(p + '2.weight') + n(p + '2.bias')
+        v = np.maximum(t, 0.0) * n(f'weight.{i}.0.weight')
+        hdn = np.maximum(sd[f'fc.{i}.0.weight'].numpy() @ v + n(f'fc.{i}.0.bias'), 0.0)
+        att = _sigmoid(sd[f'fc.{i}.2.weight'].numpy() @ hdn + n(f'fc.{i}.2.bias'))
+        assert len(v) == c
+        consts.append(v * att)
+    ref = torch.from_numpy(np.concatenate(consts)).view(1, dim, 1, 1) + x
+    assert torch.allclose(got, ref, atol=1e-12, rtol=0)
+
+
+def test_kadconv_three_branches_pool_factor_and_upsample_rule():
+    """n = 3 pin of the per-branch pool factor 2^i and the bilinear upsample
+    rule (align_corners=False).  Every stage is made a known positive scaling:
+    branch i's projection selects input channels [c_off_i, c_off_i + c_i); the
+    DSC has zero offsets, a centre-tap identity weight and a constant mask
+    m = sigmoid(b4) (LCSA's last 1x1 weight 0); BN is identity up to
+    1/sqrt(1 + eps); the SE weights are 0 so att = sigmoid(b2).  The input is
+    linear, x = a + b h + c w > 0.  Average-pooling a linear map by s samples it
+    at the block centres s k + (s - 1)/2, and upsampling those samples back
+    (src = (j + 0.5)/s - 0.5, clamped to the sample range) reproduces the line
+    inside and holds its end values outside, so branch i equals
+    a + b clamp(h, e, H - 1 - e) + c clamp(w, e, W - 1 - e), e = (2^i - 1)/2,
+    times the stage gains: the border width pins s = 2^i, the clamping pins the
+    align_corners=False rule, the channel windows pin the concat order."""
+    dim, H, W = 9, 16, 24
+    widths = O.branch_widths(dim)
+    sd = S.make_kadconv_state(dim, seed=8, dtype=torch.float64)
+    gains = []
+    c_off = 0
+    for i, c in enumerate(widths):
+        p = f'convs.{i}.'
+        sel = torch.zeros(c, dim, 1, 1, dtype=torch.float64)
+        for j in range(c):
+            sel[j, c_off + j] = 1.0
+        sd[p + '0.weight'], sd[p + '0.bias'] = sel, torch.zeros(c, dtype=torch.float64)
+        w = torch.zeros(c, c, 3, 3, dtype=torch.float64)
+        for j in range(c):
+            w[j, j, 1, 1] = 1.0
+        sd[p + '1.weight'], sd[p + '1.bias'] = w, torch.zeros(c, dtype=torch.float64)
+        sd[p + '1.conv_offset.weight'].zero_()
+        sd[p + '1.conv_offset.bias'].zero_()
+        sd[p + '1.RCA_mask.excite.4.weight'].zero_()
+        b4 = sd[p + '1.RCA_mask.excite.4.bias'].numpy()
+        for k, v in (('weight', 1.0), ('bias', 0.0), ('running_mean', 0.0), ('running_var', 1.0)):
+            sd[p + '2.' + k] = torch.full((c,), v, dtype=torch.float64)
+        sd[f'fc.{i}.0.weight'].zero_()
+        sd[f'fc.{i}.2.weight'].zero_()
+        att = _sigmoid(sd[f'fc.{i}.2.bias'].numpy())
+        scale = sd[f'weight.{i}.0.weight'].numpy().reshape(-1)
+        gains.append(_sigmoid(b4[4]) / math.sqrt(1 + 1e-3) * scale * att)
+        c_off += c
+    g = torch.Generator().manual_seed(9)
+    a = torch.rand(dim, generator=g, dtype=torch.float64) + 0.5
+    b = torch.rand(dim, generator=g, dtype=torch.float64) * 0.2
+    cc = torch.rand(dim, generator=g, dtype=torch.float64) * 0.2
+    hh = torch.arange(H, dtype=torch.float64).view(1, H, 1)
+    ww = torch.arange(W, dtype=torch.float64).view(1, 1, W)
+    x = (a.view(dim, 1, 1) + b.view(dim, 1, 1) * hh + cc.view(dim, 1, 1) * ww).unsqueeze(0)
+    got = O.kadconv_forward(sd, x)
+    ref = x.clone()
+    c_off = 0
+    for i, c in enumerate(widths):
+        e = (2 ** i - 1) / 2
+        lin = a.view(dim, 1, 1) + b.view(dim, 1, 1) * hh.clamp(e, H - 1 - e) + cc.view(dim, 1, 1) * ww.clamp(e, W - 1 - e)
+        ref[0, c_off:c_off + c] += torch.from_numpy(gains[i]).view(c, 1, 1) * lin[c_off:c_off + c]
+        c_off += c
+    assert torch.allclose(got, ref, atol=1e-12, rtol=0), (got - ref).abs().max()

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KAD_ABI_VERSION 2
+#define KAD_ABI_VERSION 3
 
 /* element types */
 #define KAD_F32 0
@@ -132,6 +132,20 @@ int kad_conv3x3_fwd(const kad_dcn_args *a, void *stream);
  * (acceleration/kadc_fused_sm75.py:1414-1421) followed by its DCN kernel
  * (kadc_dcn16.cpp:247-289).  stride <= 2 (also for kad_conv3x3_fwd). */
 int kad_dsc_fwd(const kad_dcn_args *a, void *stream);
+
+/* kad_dsc_fwd that allocates nothing and needs no caller-owned scratch.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture that must not call hipMalloc, tight
+ * serving loops, harnesses that forbid allocation).  The fused
+ * squeeze-excitation's GAP partials and per-image arrival counters live in a
+ * library-owned device array (one per GPU, held until the process ends):
+ * a->gap_partial and a->se_count must be NULL; with a->se_att set, at most
+ * 4096 images and N x kad_dcn_tiles(Ho, Wo) x Cout <= 1048576 partials
+ * (4 MiB), else KAD_EINVAL.  Inputs and outputs are the caller's, as in
+ * kad_dsc_fwd, and the results are identical to it.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams or
+ * host threads) race.  The device is the calling thread's current device. */
+int kad_dsc_fwd_noalloc(const kad_dcn_args *a, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* 1x1 convolution GEMM with fused input average pool and bias/SiLU epilogue */

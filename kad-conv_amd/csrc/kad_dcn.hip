@@ -55,6 +55,8 @@
 // product, so A and B only have to agree with each other; the accumulator
 // layout (lane -> column lane & 15, rows 4 * (lane >> 4) + i) is the MFMA
 // output layout.
+#include <mutex>
+
 #include "kad_common.h"
 
 namespace kad {
@@ -1376,4 +1378,67 @@ extern "C" int kad_dsc_fwd(const kad_dcn_args* a, void* stream) {
     case KAD_BF16: return dispatch_dcn<bf16_t, bf16_t, MODE_FUSED>(*a, st, g);
     default: return fail(KAD_EINVAL, "kad_dsc_fwd: unknown dtype %d", a->dtype);
   }
+}
+
+// ---- kad_dsc_fwd without caller-owned scratch -------------------------------------------------------
+// The fused squeeze-excitation needs two buffers beyond the inputs and outputs: the per-tile GAP
+// partials and the per-image arrival counters.  kad_dsc_fwd_noalloc takes both from `scratch`, a
+// file-scope device array of fixed size, so a caller that cannot allocate passes only inputs and
+// outputs.  Layout: [0, 16 KB) counters (unsigned, one per image; zero when the code object is
+// loaded, as static storage is, and left zero by every call that completes), then the partials.
+// The host-side name `scratch` is not a device address: each device's copy is found once with
+// hipGetSymbolAddress and only that pointer is handed to kernels.  Every call on a device shares
+// that device's array, so calls that overlap on one GPU race.
+namespace kad {
+constexpr int NOALLOC_MAX_IMAGES = 4096;
+constexpr int64_t NOALLOC_MAX_PARTIALS = (int64_t)1 << 20;  // floats: N * tiles * Cout
+constexpr size_t NOALLOC_COUNT_BYTES = (size_t)NOALLOC_MAX_IMAGES * 4;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_COUNT_BYTES + NOALLOC_MAX_PARTIALS * 4];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// This device's address of `scratch`, looked up on the first call per device (current device).
+static int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(KAD_ELAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return fail(KAD_EUNSUPPORTED, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(KAD_ELAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return KAD_OK;
+}
+}  // namespace kad
+
+extern "C" int kad_dsc_fwd_noalloc(const kad_dcn_args* a_in, void* stream) {
+  KAD_CHECK_ARG(a_in, "kad_dsc_fwd_noalloc: null args");
+  KAD_CHECK_ARG(!a_in->gap_partial && !a_in->se_count,
+                "kad_dsc_fwd_noalloc: gap_partial and se_count come from the library's scratch; pass NULL");
+  kad_dcn_args a = *a_in;
+  if (a.se_att) {
+    KAD_CHECK_ARG(a.n > 0 && a.h > 0 && a.w > 0 && a.cout > 0 && a.stride >= 1 && a.pad >= 0,
+                  "kad_dsc_fwd_noalloc: bad shape n=%d h=%d w=%d cout=%d stride=%d pad=%d", a.n, a.h, a.w, a.cout,
+                  a.stride, a.pad);
+    const int ho = (a.h + 2 * a.pad - 3) / a.stride + 1, wo = (a.w + 2 * a.pad - 3) / a.stride + 1;
+    KAD_CHECK_ARG(ho > 0 && wo > 0, "kad_dsc_fwd_noalloc: empty output");
+    const int64_t need = (int64_t)a.n * kad_dcn_tiles(ho, wo) * a.cout;
+    KAD_CHECK_ARG(a.n <= NOALLOC_MAX_IMAGES && need <= NOALLOC_MAX_PARTIALS,
+                  "kad_dsc_fwd_noalloc: N=%d images and %lld GAP partials exceed the scratch limits (%d images, "
+                  "%lld partials = N x tiles x Cout)", a.n, (long long)need, NOALLOC_MAX_IMAGES,
+                  (long long)NOALLOC_MAX_PARTIALS);
+    void* p = nullptr;
+    const int rc = scratch_ptr(&p);
+    if (rc) return rc;
+    a.se_count = (unsigned*)p;
+    a.gap_partial = (float*)((char*)p + NOALLOC_COUNT_BYTES);
+  }
+  return kad_dsc_fwd(&a, stream);
 }

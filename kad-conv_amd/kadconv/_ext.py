@@ -19,7 +19,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libkadconv
 
 KAD_F32, KAD_F16, KAD_BF16 = 0, 1, 2
 KAD_NHWC, KAD_NCHW = 0, 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _DTYPES = {torch.float32: KAD_F32, torch.float16: KAD_F16, torch.bfloat16: KAD_BF16}
 
@@ -89,6 +89,7 @@ SIGNATURES = {
     'kad_dcn_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_conv3x3_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_dsc_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
+    'kad_dsc_fwd_noalloc': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_scale_residual': (c_int, [c_vp, c_vp, c_vp] + [c_int] * 8 + [c_vp]),
     'kad_gemm_wpack_elems': (c_i64, [c_int, c_int]),
     'kad_gemm_pack_weights': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
@@ -205,24 +206,32 @@ def dcn_pack_weights(weight, dtype):
     return out
 
 
-def _set_se(a, se, gap_partial, n, cout, ho, wo):
-    """Fused squeeze-excitation fields of kad_dcn_args: se = (w1 [hid, C], b1, w2 [C, hid], b2, att [N, C],
-    count [N] int32, zero before the first call)."""
-    if se is None:
-        return
-    w1, b1, w2, b2, att, count = se
-    if gap_partial is None:
-        raise ValueError('the fused squeeze-excitation reads the GAP partials: pass gap_partial')
+def _set_se_weights(a, se, n, cout, ho, wo):
+    """MLP fields of the fused squeeze-excitation: se = (w1 [hid, C], b1, w2 [C, hid], b2, att [N, C])."""
+    w1, b1, w2, b2, att = se[:5]
+    _need_gpu(w1, b1, w2, b2, att)
     for t in (w1, b1, w2, b2, att):
         if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
             raise TypeError('SE weights and att must be contiguous float32')
     hid = w1.shape[0]
     if tuple(w1.shape) != (hid, cout) or tuple(w2.shape) != (cout, hid) or tuple(att.shape) != (n, cout):
         raise ValueError('SE shapes: w1 [hid, C], w2 [C, hid], att [N, C]')
+    a.se_w1, a.se_b1, a.se_w2, a.se_b2 = _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2)
+    a.se_att, a.se_hid, a.se_inv_count = _ptr(att), hid, 1.0 / (ho * wo)
+
+
+def _set_se(a, se, gap_partial, n, cout, ho, wo):
+    """Fused squeeze-excitation fields of kad_dcn_args: se = (w1 [hid, C], b1, w2 [C, hid], b2, att [N, C],
+    count [N] int32, zero before the first call)."""
+    if se is None:
+        return
+    count = se[5]
+    if gap_partial is None:
+        raise ValueError('the fused squeeze-excitation reads the GAP partials: pass gap_partial')
+    _set_se_weights(a, se, n, cout, ho, wo)
     if count.dtype != torch.int32 or count.numel() < n:
         raise ValueError('SE counters: int32 [N]')
-    a.se_w1, a.se_b1, a.se_w2, a.se_b2 = _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2)
-    a.se_att, a.se_count, a.se_hid, a.se_inv_count = _ptr(att), _ptr(count), hid, 1.0 / (ho * wo)
+    a.se_count = _ptr(count)
 
 
 def dcn_fwd(x_nhwc, cin, offset, offset_strides, mask, mask_strides, wpack, cout, out, *, stride=1, pad=1,
@@ -256,10 +265,14 @@ def dcn_fwd(x_nhwc, cin, offset, offset_strides, mask, mask_strides, wpack, cout
 
 def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, out, *, stride=1, pad=1,
             bias=None, post_mul=None, post_add=None, post_scale=None, relu=False, out_layout=KAD_NHWC,
-            gap_partial=None, se=None):
+            gap_partial=None, se=None, noalloc=False):
     """conv_offset + deformable conv in one launch (offsets never leave the chip); with `se`,
-    also the squeeze-excitation MLP of the output (see _set_se)."""
+    also the squeeze-excitation MLP of the output (see _set_se).  noalloc=True calls
+    kad_dsc_fwd_noalloc: `se` is then (w1, b1, w2, b2, att) and the GAP partials and arrival
+    counters come from the library's own device scratch (gap_partial must be None)."""
     _need_gpu(x_nhwc, off_wpack, wpack, out)
+    if noalloc and gap_partial is not None:
+        raise ValueError('kad_dsc_fwd_noalloc keeps the GAP partials in its own scratch: pass gap_partial=None')
     N, H, W, cs = x_nhwc.shape
     a = DcnArgs()
     a.x, a.mask, a.wpack = _ptr(x_nhwc), _ptr(mask), _ptr(wpack)
@@ -279,7 +292,13 @@ def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, o
             raise TypeError('offset bias/mask/epilogue/gap tensors must be float32')
     if wpack.dtype != x_nhwc.dtype or off_wpack.dtype != x_nhwc.dtype or out.dtype != x_nhwc.dtype:
         raise TypeError('x, packed weights and out must share a dtype')
-    _set_se(a, se, gap_partial, N, cout, (H + 2 * pad - 3) // stride + 1, (W + 2 * pad - 3) // stride + 1)
+    ho, wo = (H + 2 * pad - 3) // stride + 1, (W + 2 * pad - 3) // stride + 1
+    if noalloc:
+        if se is not None:
+            _set_se_weights(a, se, N, cout, ho, wo)
+        _check(load().kad_dsc_fwd_noalloc(ctypes.byref(a), _stream()), 'kad_dsc_fwd_noalloc')
+        return out
+    _set_se(a, se, gap_partial, N, cout, ho, wo)
     _check(load().kad_dsc_fwd(ctypes.byref(a), _stream()), 'kad_dsc_fwd')
     return out
 

@@ -36,6 +36,11 @@ extern "C" {
 #define KAD_F16 1
 #define KAD_BF16 2
 
+/* activations (kad_dcn_args.relu) */
+#define KAD_ACT_NONE 0
+#define KAD_ACT_RELU 1
+#define KAD_ACT_SILU 2
+
 /* feature-map layouts */
 #define KAD_NHWC 0
 #define KAD_NCHW 1
@@ -92,7 +97,8 @@ typedef struct kad_dcn_args {
   int out_cs;             /* NHWC: channel stride of out; NCHW: channel planes per image of out
                              (both >= Cout: a channel slice of a wider tensor can be written) */
   int dtype;              /* KAD_F32 / KAD_F16 / KAD_BF16 (x, wpack, out) */
-  int relu;               /* nonzero: ReLU between post_add and post_scale */
+  int relu;               /* activation between post_add and post_scale: KAD_ACT_NONE (0), KAD_ACT_SILU (2),
+                             else ReLU (KAD_ACT_RELU = 1) */
   /* Squeeze-excitation of the output, fused (needs gap_partial).  When se_att is
    * not NULL, the last block of each image to finish sums that image's GAP
    * partials in a fixed order and writes
@@ -163,7 +169,9 @@ typedef struct kad_gemm_args {
   const void *x;          /* NCHW [N][Cin][H][W] or NHWC [N][H][W][x_cs], dtype */
   const void *wpack;      /* kad_gemm_pack_weights output */
   const float *bias;      /* [Cout] or NULL */
-  void *out;              /* NCHW [N][Cout][H/pool][W/pool] or NHWC [...][out_cs] (pad channels written 0) */
+  void *out;              /* NCHW [N][Cout][H/pool][W/pool] or NHWC [...][out_cs]: channels [0, Cout) written,
+                             [Cout, min(out_cs, roundup(Cout, 8))) zeroed, the rest of the stride untouched (so
+                             out may be a channel slice of a concat buffer) */
   int n, cin, cout, h, w;
   int pool;               /* s >= 1: avg_pool2d(kernel=s, stride=s, floor) applied to x first */
   int in_layout, x_cs;
@@ -340,6 +348,70 @@ int kad_branch_merge(const kad_merge_args *a, void *stream);
  * k_cat_residual_att0 (acceleration/kadc_fused_sm75.py:1245-1331) for branch 0. */
 int kad_scale_residual(void *out, const float *att, const void *residual, int n, int c, int h, int w, int img_c,
                        int c_off, int layout, int dtype, void *stream);
+
+/* ------------------------------------------------------------------------ */
+/* KAD-CNet-S network ops (NHWC feature maps with explicit channel strides)  */
+/* ------------------------------------------------------------------------ */
+
+/* Plain 3x3 convolution (stride <= 2) whose output has the op's dtype, on the
+ * kad_dcn_args machinery (offset / mask ignored): KAD-CNet's `Conv` with k = 3
+ * after Conv-BN fusion, act(W * x + b) (KAD-CNet/models/common.py:43-57,
+ * fused by yolo.py:574-585).  a->relu selects the activation: 0 none,
+ * 1 ReLU, 2 SiLU (x * sigmoid(x), the `Conv.default_act`).  Grouped convs are
+ * passed with block-diagonal dense weights.  The reference runs these on
+ * cuDNN (KAD-CNet/inference/acceleration/kadc_fused_sm75.py:616-629). */
+int kad_conv_fwd(const kad_dcn_args *a, void *stream);
+
+#define KAD_RS_AVG 0      /* average pool, zero padding counted (count_include_pad=True) */
+#define KAD_RS_MAX 1      /* max pool, padding ignored */
+#define KAD_RS_NEAREST 2  /* nearest upsample by the integer factor s: out[y][x] = in[y / s][x / s] */
+
+typedef struct kad_resample_args {
+  const void *x;         /* NHWC [N][H][W][x_cs], dtype (channels [0, c) used) */
+  void *out;             /* NHWC [N][Ho][Wo][out_cs], dtype (channels [0, c) written) */
+  int n, c, h, w, ho, wo, x_cs, out_cs;
+  int mode;              /* KAD_RS_* */
+  int k, s, p;           /* pool: kernel, stride, padding (floor mode); nearest: s = factor */
+  int dtype;
+} kad_resample_args;
+
+/* Pools, nearest upsampling and channel-slice copies (k = s = 1, p = 0, AVG) of
+ * NHWC maps, reading and writing channel slices of wider tensors in place.
+ * Stands in for AConv's avg_pool2d(x, 2, 1, 0) (KAD-CNet/models/common.py:65-67),
+ * SPPELAN's max pools (common.py:187-193,563-577), the neck's
+ * nn.Upsample(None, 2, 'nearest') and torch.cat (common.py:535-542), and the
+ * reference's Triton helpers for them (acceleration/kadc_fused_sm75.py:197-430). */
+int kad_nhwc_resample(const kad_resample_args *a, void *stream);
+
+#define KAD_MAX_LEVELS 4
+typedef struct kad_decode_args {
+  const void *head[KAD_MAX_LEVELS]; /* level l: NHWC [N][lh][lw][head_cs], box logits in channels
+                                       [0, 4 * reg_max) (side j's bins at reg_max * j + b), class
+                                       logits in [box_ch, box_ch + nc) */
+  int lh[KAD_MAX_LEVELS], lw[KAD_MAX_LEVELS], head_cs[KAD_MAX_LEVELS];
+  int anchor_off[KAD_MAX_LEVELS];   /* first anchor of level l (levels in order, cells row-major) */
+  float stride[KAD_MAX_LEVELS];
+  void *out;                        /* [N][4 + nc][A], dtype: (cx, cy, w, h) * stride, then sigmoid(cls) */
+  int n, nl, nc, reg_max, box_ch, dtype;
+} kad_decode_args;
+
+/* DDetect's inference output y = cat(dist2bbox(DFL(box), anchors, xywh) * strides,
+ * sigmoid(cls)) for all levels (KAD-CNet/models/yolo.py:102-127; DFL
+ * models/common.py:232-244; make_anchors / dist2bbox
+ * utils/tal/anchor_generator.py:8-32, grid offset 0.5).  The reference's
+ * fused Triton decode is KAD-CNet/inference/acceleration/kadc_head_decode.py:9-88. */
+int kad_ddetect_decode(const kad_decode_args *a, void *stream);
+
+#define KAD_NMS_MAX 32768
+/* 64-bit words of the pairwise suppression mask kad_nms needs for n boxes. */
+int64_t kad_nms_mask_words(int n);
+
+/* Greedy non-maximum suppression of n <= KAD_NMS_MAX boxes [n][4] (x1, y1, x2,
+ * y2, fp32) already sorted by descending score: keep[i] = 1 when no kept box
+ * before i has IoU > iou_thr with box i (IoU = inter / (area_i + area_j - inter),
+ * fp32), else 0.  mask: kad_nms_mask_words(n) words of caller scratch.  The
+ * torchvision.ops.nms call of non_max_suppression (KAD-CNet/utils/general.py:961). */
+int kad_nms(const float *boxes, unsigned long long *mask, unsigned char *keep, int n, float iou_thr, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1111,7 +1111,8 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       for (int i = 0; i < 4; ++i) {
         const int pl = wave * (16 * DCN_WM) + m * 16 + grp * 4 + i;
         float v = fmaf(acc[m][b][i], mul, shift);
-        if (a.relu) v = fmaxf(v, 0.f);
+        if (a.relu == KAD_ACT_SILU) v = v * sigmoidf_(v);
+        else if (a.relu) v = fmaxf(v, 0.f);
         v *= scl;
         const OutT o = from_f32<OutT>(v);
         ost[pl * SROW + col] = o;
@@ -1351,6 +1352,20 @@ extern "C" int kad_conv3x3_fwd(const kad_dcn_args* a, void* stream) {
     case KAD_F16: return dispatch_dcn<half_t, float, MODE_PLAIN>(*a, st, g);
     case KAD_BF16: return dispatch_dcn<bf16_t, float, MODE_PLAIN>(*a, st, g);
     default: return fail(KAD_EINVAL, "kad_conv3x3_fwd: unknown dtype %d", a->dtype);
+  }
+}
+
+extern "C" int kad_conv_fwd(const kad_dcn_args* a, void* stream) {
+  DcnGeom g;
+  int rc = validate_dcn(a, MODE_PLAIN, &g);
+  if (rc) return fail(rc, "kad_conv_fwd: %s", kad_last_error());
+  KAD_CHECK_ARG(a->relu >= KAD_ACT_NONE && a->relu <= KAD_ACT_SILU, "kad_conv_fwd: unknown activation %d", a->relu);
+  hipStream_t st = (hipStream_t)stream;
+  switch (a->dtype) {
+    case KAD_F32: return dispatch_dcn<float, float, MODE_PLAIN>(*a, st, g);
+    case KAD_F16: return dispatch_dcn<half_t, half_t, MODE_PLAIN>(*a, st, g);
+    case KAD_BF16: return dispatch_dcn<bf16_t, bf16_t, MODE_PLAIN>(*a, st, g);
+    default: return fail(KAD_EINVAL, "kad_conv_fwd: unknown dtype %d", a->dtype);
   }
 }
 

@@ -150,7 +150,9 @@ __global__ __launch_bounds__(GM_THREADS) void gemm1x1_kernel(kad_gemm_args a, in
   for (int b = 0; b < NBF; ++b) {
     const int co = co0 + b * 16 + row;
     const bool co_ok = co < a.cout;
-    const bool pad_ch = !co_ok && a.out_layout == KAD_NHWC && co < a.out_cs;
+    // NHWC: channels [cout, roundup(cout, 8)) are the output's zero padding; the rest of a
+    // wider channel stride (other slices of a concat buffer) is left untouched
+    const bool pad_ch = !co_ok && a.out_layout == KAD_NHWC && co < a.out_cs && co < round_up(a.cout, 8);
     const float bias = (co_ok && a.bias) ? a.bias[co] : 0.f;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
@@ -384,7 +386,7 @@ template <typename T, int NBF>
 static int launch_gemm(const kad_gemm_args& a, hipStream_t st, int hp, int wp) {
   const int P = hp * wp;
   const int tiles = ceil_div(P, GM_TILE);
-  const int ncols = a.out_layout == KAD_NHWC ? (a.out_cs > a.cout ? a.out_cs : a.cout) : a.cout;
+  const int ncols = a.out_layout == KAD_NHWC ? round_up(a.cout, 8) : a.cout;
   dim3 grid(tiles, ceil_div(ncols, NBF * 16), a.n);
   hipLaunchKernelGGL((gemm1x1_kernel<T, NBF>), grid, dim3(GM_THREADS), 0, st, a, hp, wp, tiles,
                      round_up(a.cin, 32));
@@ -433,7 +435,7 @@ template <typename T>
 static int dispatch_gemm(const kad_gemm_args& a, hipStream_t st, int hp, int wp) {
   if constexpr (sizeof(T) == 2)
     if (nchw_fast_ok(a)) return launch_gemm_nchw<T>(a, st);
-  const int ncols = a.out_layout == KAD_NHWC ? (a.out_cs > a.cout ? a.out_cs : a.cout) : a.cout;
+  const int ncols = a.out_layout == KAD_NHWC ? round_up(a.cout, 8) : a.cout;
   const int nbf = ceil_div(ncols, 16);
   switch (nbf < 8 ? nbf : 8) {
     case 1: return launch_gemm<T, 1>(a, st, hp, wp);
@@ -482,8 +484,7 @@ extern "C" int kad_gemm1x1_fwd(const kad_gemm_args* a, void* stream) {
                 a->w, a->pool);
   KAD_CHECK_ARG(a->in_layout == KAD_NCHW || (a->in_layout == KAD_NHWC && a->x_cs >= a->cin),
                 "kad_gemm1x1_fwd: bad input layout/channel stride");
-  KAD_CHECK_ARG(a->out_layout == KAD_NCHW || (a->out_layout == KAD_NHWC && a->out_cs >= a->cout &&
-                                              a->out_cs <= round_up(round_up(a->cout, 8), 128)),
+  KAD_CHECK_ARG(a->out_layout == KAD_NCHW || (a->out_layout == KAD_NHWC && a->out_cs >= a->cout),
                 "kad_gemm1x1_fwd: bad output layout/channel stride");
   KAD_CHECK_ARG(a->act == 0 || a->act == 1, "kad_gemm1x1_fwd: act must be 0 (none) or 1 (SiLU)");
   const int hp = a->h / a->pool, wp = a->w / a->pool;

@@ -79,6 +79,21 @@ class MergeArgs(ctypes.Structure):
     ]
 
 
+class ResampleArgs(ctypes.Structure):
+    _fields_ = [('x', c_vp), ('out', c_vp)] + [(f, c_int) for f in (
+        'n', 'c', 'h', 'w', 'ho', 'wo', 'x_cs', 'out_cs', 'mode', 'k', 's', 'p', 'dtype')]
+
+
+MAX_LEVELS = 4
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [('head', c_vp * MAX_LEVELS), ('lh', c_int * MAX_LEVELS), ('lw', c_int * MAX_LEVELS),
+                ('head_cs', c_int * MAX_LEVELS), ('anchor_off', c_int * MAX_LEVELS),
+                ('stride', ctypes.c_float * MAX_LEVELS), ('out', c_vp)] + [(f, c_int) for f in (
+                    'n', 'nl', 'nc', 'reg_max', 'box_ch', 'dtype')]
+
+
 # name -> (restype, argtypes); must list every symbol declared in include/kadconv_hip.h
 SIGNATURES = {
     'kad_abi_version': (c_int, []),
@@ -114,6 +129,11 @@ SIGNATURES = {
     'kad_channel_scale': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_to_nhwc': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_branch_merge': (c_int, [ctypes.POINTER(MergeArgs), c_vp]),
+    'kad_conv_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
+    'kad_nhwc_resample': (c_int, [ctypes.POINTER(ResampleArgs), c_vp]),
+    'kad_ddetect_decode': (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
+    'kad_nms_mask_words': (c_i64, [c_int]),
+    'kad_nms': (c_int, [c_vp, c_vp, c_vp, c_int, ctypes.c_float, c_vp]),
 }
 
 _lib = None
@@ -560,3 +580,119 @@ def branch_merge(out, layout, branches, residual=None, gate=None, channels=None)
         a.br_coeff[i] = float(b.get('coeff', 1.0))
     _check(load().kad_branch_merge(ctypes.byref(a), _stream()), 'kad_branch_merge')
     return out
+
+
+# ---------------------------------------------------------------------------- network ops (KAD-CNet-S)
+KAD_ACT_NONE, KAD_ACT_RELU, KAD_ACT_SILU = 0, 1, 2
+KAD_RS_AVG, KAD_RS_MAX, KAD_RS_NEAREST = 0, 1, 2
+
+
+def _nhwc_cs(t):
+    """(N, H, W, channel stride) of an NHWC view whose pixels are dense apart from the channel stride."""
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise ValueError('NHWC view with unit channel step expected')
+    N, H, W, _ = t.shape
+    cs = t.stride(2)
+    if t.stride(1) != W * cs or t.stride(0) != H * W * cs:
+        raise ValueError('NHWC view must be dense apart from its channel stride')
+    return N, H, W, cs
+
+
+def conv_fwd(x_nhwc, cin, wpack, cout, out_nhwc, *, stride=1, pad=1, bias=None, act=KAD_ACT_SILU):
+    """act(conv3x3(x) + bias) in x's dtype; x and out are NHWC views (channel slices allowed)."""
+    _need_gpu(x_nhwc, wpack, out_nhwc, bias)
+    N, H, W, cs = _nhwc_cs(x_nhwc)
+    No, Ho, Wo, ocs = _nhwc_cs(out_nhwc)
+    if (No, Ho, Wo) != (N, (H + 2 * pad - 3) // stride + 1, (W + 2 * pad - 3) // stride + 1) or \
+            out_nhwc.shape[3] < cout or x_nhwc.shape[3] < cin:
+        raise ValueError('conv_fwd: output shape does not match the convolution')
+    if wpack.dtype != x_nhwc.dtype or out_nhwc.dtype != x_nhwc.dtype:
+        raise TypeError('x, packed weights and out must share a dtype')
+    if bias is not None and bias.dtype != torch.float32:
+        raise TypeError('bias must be float32')
+    a = DcnArgs()
+    a.x, a.wpack, a.bias, a.out = _ptr(x_nhwc), _ptr(wpack), _ptr(bias), _ptr(out_nhwc)
+    a.n, a.cin, a.cout, a.h, a.w, a.stride, a.pad = N, cin, cout, H, W, stride, pad
+    a.x_cs, a.out_layout, a.out_cs = cs, KAD_NHWC, ocs
+    a.dtype = kad_dtype(x_nhwc.dtype)
+    a.relu = act
+    _check(load().kad_conv_fwd(ctypes.byref(a), _stream()), 'kad_conv_fwd')
+    return out_nhwc
+
+
+def nhwc_resample(x_nhwc, out_nhwc, c, mode, k=1, s=1, p=0):
+    """Pool (KAD_RS_AVG / KAD_RS_MAX, kernel k, stride s, padding p), nearest upsample
+    (KAD_RS_NEAREST, factor s) or copy (AVG with k = s = 1) of channels [0, c)."""
+    _need_gpu(x_nhwc, out_nhwc)
+    N, H, W, cs = _nhwc_cs(x_nhwc)
+    No, Ho, Wo, ocs = _nhwc_cs(out_nhwc)
+    if No != N or out_nhwc.dtype != x_nhwc.dtype:
+        raise ValueError('nhwc_resample: batch or dtype mismatch')
+    a = ResampleArgs()
+    a.x, a.out = _ptr(x_nhwc), _ptr(out_nhwc)
+    a.n, a.c, a.h, a.w, a.ho, a.wo, a.x_cs, a.out_cs = N, c, H, W, Ho, Wo, cs, ocs
+    a.mode, a.k, a.s, a.p, a.dtype = mode, k, s, p, kad_dtype(x_nhwc.dtype)
+    _check(load().kad_nhwc_resample(ctypes.byref(a), _stream()), 'kad_nhwc_resample')
+    return out_nhwc
+
+
+def ddetect_decode(heads, strides, out, nc, reg_max=16, box_ch=None):
+    """heads: per level NHWC views [N, h, w, >= box_ch + nc]; out [N, 4 + nc, A] (heads' dtype)."""
+    _need_gpu(out, *heads)
+    if len(heads) > MAX_LEVELS:
+        raise ValueError(f'at most {MAX_LEVELS} levels')
+    a = DecodeArgs()
+    off = 0
+    for l, h in enumerate(heads):
+        N, H, W, cs = _nhwc_cs(h)
+        if h.dtype != out.dtype:
+            raise TypeError('heads and out must share a dtype')
+        a.head[l], a.lh[l], a.lw[l], a.head_cs[l] = h.data_ptr(), H, W, cs
+        a.anchor_off[l], a.stride[l] = off, float(strides[l])
+        off += H * W
+    if tuple(out.shape) != (heads[0].shape[0], 4 + nc, off) or not out.is_contiguous():
+        raise ValueError(f'out must be contiguous [N, {4 + nc}, {off}]')
+    a.out = _ptr(out)
+    a.n, a.nl, a.nc, a.reg_max = heads[0].shape[0], len(heads), nc, reg_max
+    a.box_ch = 4 * reg_max if box_ch is None else box_ch
+    a.dtype = kad_dtype(out.dtype)
+    _check(load().kad_ddetect_decode(ctypes.byref(a), _stream()), 'kad_ddetect_decode')
+    return out
+
+
+NMS_MAX = 32768
+
+
+def nms_keep(boxes_sorted, iou_thr):
+    """keep flags (uint8 [n]) of greedy NMS over fp32 xyxy boxes sorted by descending score."""
+    _need_gpu(boxes_sorted)
+    n = boxes_sorted.shape[0]
+    keep = torch.empty(n, dtype=torch.uint8, device=boxes_sorted.device)
+    if n == 0:
+        return keep
+    b = boxes_sorted.to(torch.float32).contiguous()
+    mask = torch.empty(load().kad_nms_mask_words(n), dtype=torch.int64, device=b.device)
+    _check(load().kad_nms(_ptr(b), _ptr(mask), _ptr(keep), n, float(iou_thr), _stream()), 'kad_nms')
+    return keep
+
+
+def gemm1x1_nhwc(x_nhwc, cin, wpack, cout, out_nhwc, *, bias=None, act=KAD_ACT_NONE):
+    """act(W x + b) for NHWC views (channel slices allowed on both sides), act
+    KAD_ACT_NONE or KAD_ACT_SILU: the output's channels [cout, roundup(cout, 8))
+    inside its stride are zeroed."""
+    if act not in (KAD_ACT_NONE, KAD_ACT_SILU):
+        raise NotImplementedError('the 1x1 GEMM epilogue has no activation but SiLU')
+    _need_gpu(x_nhwc, wpack, out_nhwc, bias)
+    N, H, W, cs = _nhwc_cs(x_nhwc)
+    No, Ho, Wo, ocs = _nhwc_cs(out_nhwc)
+    if (No, Ho, Wo) != (N, H, W) or x_nhwc.shape[3] < cin or out_nhwc.shape[3] < cout:
+        raise ValueError('gemm1x1_nhwc: shape mismatch')
+    if wpack.dtype != x_nhwc.dtype or out_nhwc.dtype != x_nhwc.dtype:
+        raise TypeError('x, packed weights and out must share a dtype')
+    a = GemmArgs()
+    a.x, a.wpack, a.bias, a.out = _ptr(x_nhwc), _ptr(wpack), _ptr(bias), _ptr(out_nhwc)
+    a.n, a.cin, a.cout, a.h, a.w, a.pool = N, cin, cout, H, W, 1
+    a.in_layout, a.x_cs, a.out_layout, a.out_cs = KAD_NHWC, cs, KAD_NHWC, ocs
+    a.act, a.dtype = (1 if act == KAD_ACT_SILU else 0), kad_dtype(x_nhwc.dtype)   # kad_gemm_args.act: 1 = SiLU
+    _check(load().kad_gemm1x1_fwd(ctypes.byref(a), _stream()), 'kad_gemm1x1_fwd')
+    return out_nhwc

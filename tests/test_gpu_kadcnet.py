@@ -1,0 +1,284 @@
+"""KAD-CNet-S on the HIP kernels against the CPU oracle
+(oracle/kadcnet_oracle.py), plus the network-level ops on their own.
+
+Network tolerances (stated here, measured on MI355X):
+  fp32: every layer output, the head maps and y within 1e-4 x max|ref| of the
+        float64 oracle (the north-star fp32 bound, applied per tensor);
+  fp16: the head maps (logits, |ref| <= ~15) within 1e-2 x max|ref|, i.e. an
+        absolute error of ~0.1 logit after 22 layers of fp16 storage, and the
+        decoded boxes within 1e-2 x max|ref| too.  The north-star 1e-2 absolute
+        bound is for one operator; each fp16 layer adds its own output
+        rounding, so a network is checked relative to its output scale.
+The per-operator fp16 bound (1e-2 absolute) is kept by the op tests below."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kadcnet_oracle as KO
+from tests._util import check_close
+
+pytestmark = pytest.mark.gpu
+
+DT = {'f32': torch.float32, 'f16': torch.float16, 'bf16': torch.bfloat16}
+
+
+def _nhwc(t):
+    return t.permute(0, 2, 3, 1)
+
+
+# ---------------------------------------------------------------------------- ops
+@pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
+@pytest.mark.parametrize('mode,k,s,p', [('avg', 2, 1, 0), ('max', 5, 1, 2), ('nearest', 1, 2, 0), ('copy', 1, 1, 0)])
+def test_nhwc_resample(dt, mode, k, s, p):
+    """Pools, nearest upsample and copies between channel slices of wider NHWC
+    buffers: channels outside the written slice stay untouched.  Max, nearest and
+    copy are bit-exact; the average is the fp32 mean of the dtype inputs rounded once."""
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(k * 10 + s)
+    N, H, W, C = 2, 13, 11, 16
+    src = torch.randn(N, H, W, 40, generator=g).to(dtype)
+    x = src[..., 8:8 + C]                              # a slice at channel 8 of a 40-channel buffer
+    xr = x.permute(0, 3, 1, 2).double()
+    if mode == 'avg':
+        ref, m = F.avg_pool2d(xr, k, s, p), _ext.KAD_RS_AVG
+    elif mode == 'max':
+        ref, m = F.max_pool2d(xr, k, s, p), _ext.KAD_RS_MAX
+    elif mode == 'nearest':
+        ref, m = F.interpolate(xr, scale_factor=s, mode='nearest'), _ext.KAD_RS_NEAREST
+    else:
+        ref, m = xr, _ext.KAD_RS_AVG
+    Ho, Wo = ref.shape[2:]
+    dst = torch.full((N, Ho, Wo, 48), 7.0, dtype=dtype, device=dev)
+    _ext.nhwc_resample(src.to(dev)[..., 8:8 + C], dst[..., 16:16 + C], C, m, k=k, s=s, p=p)
+    torch.cuda.synchronize()
+    got = dst.cpu().double()
+    assert (got[..., :16] == 7.0).all() and (got[..., 16 + C:] == 7.0).all()
+    # a 16-bit 2x2 mean is exact in fp32, so the output is the exact mean rounded once
+    exp = _nhwc(ref).to(dtype).double() if mode == 'avg' else _nhwc(ref)
+    tol = 1e-6 if (mode == 'avg' and dtype == torch.float32) else 0.0
+    err = (got[..., 16:16 + C] - exp).abs().max().item()
+    assert err <= tol, f'{mode} {dt}: max|d| = {err}'
+
+
+@pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
+@pytest.mark.parametrize('cin,cout,stride,groups,act', [(3, 40, 2, 1, 'silu'), (72, 144, 2, 1, 'silu'),
+                                                        (32, 32, 1, 1, 'silu'), (64, 64, 1, 4, 'silu'),
+                                                        (144, 40, 1, 1, 'none'), (16, 24, 1, 1, 'relu')])
+def test_conv3x3_fwd(dt, cin, cout, stride, groups, act):
+    """kad_conv_fwd (KAD-CNet's 3x3 Conv after Conv-BN fusion) against F.conv2d in
+    float64 on the dtype-rounded operands; input read from a channel slice, output
+    written into one; grouped convs through block-diagonal dense weights."""
+    from kadcnet.fast import _ConvOp
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(cin * 7 + cout)
+    N, H, W = 2, 19, 23
+    conv = torch.nn.Conv2d(cin, cout, 3, stride, 1, groups=groups, bias=True)
+    with torch.no_grad():
+        conv.weight.copy_(torch.randn(conv.weight.shape, generator=g) * (1.0 / (9 * cin / groups) ** 0.5))
+        conv.bias.copy_(torch.randn(cout, generator=g) * 0.1)
+    code = {'silu': _ext.KAD_ACT_SILU, 'none': _ext.KAD_ACT_NONE, 'relu': _ext.KAD_ACT_RELU}[act]
+    w64, b64 = conv.weight.detach().double(), conv.bias.detach().double()
+    op = _ConvOp(conv.to(dev), act=code)
+    cs_in = (cin + 8 + 7) // 8 * 8
+    buf = torch.zeros(N, H, W, cs_in)
+    xq = torch.randn(N, H, W, cin, generator=g).to(dtype)
+    buf[..., 8:8 + cin] = xq.float()
+    buf = buf.to(dev, dtype)
+    Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
+    out = torch.full((N, Ho, Wo, cout + 16), 5.0, dtype=dtype, device=dev)
+    print(f'conv3x3 {dt} {cin}->{cout} s{stride} g{groups} {act}', flush=True)
+    op(buf[..., 8:8 + cin], out[..., 8:8 + cout])
+    torch.cuda.synchronize()
+    w = w64.to(dtype).double() if dtype != torch.float32 else w64
+    ref = F.conv2d(xq.permute(0, 3, 1, 2).double(), w, b64, stride, 1, groups=groups)
+    ref = {'silu': F.silu, 'none': lambda t: t, 'relu': torch.relu}[act](ref)
+    got = out.cpu().double()
+    assert (got[..., :8] == 5.0).all() and (got[..., 8 + cout:] == 5.0).all()
+    check_close(got[..., 8:8 + cout].permute(0, 3, 1, 2), ref, dtype, f'conv3x3 {dt} {cin}->{cout}')
+
+
+@pytest.mark.parametrize('dt', ['f16', 'f32'])
+def test_gemm1x1_into_slice(dt):
+    """kad_gemm1x1_fwd NHWC into a channel slice of a wider buffer: channels
+    [cout, roundup(cout, 8)) are zeroed, everything else outside the slice kept."""
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(3)
+    N, H, W, cin, cout = 2, 9, 14, 40, 20
+    x = torch.randn(N, H, W, 64, generator=g).to(dtype)
+    wt = torch.randn(cout, cin, generator=g) * 0.15
+    b = torch.randn(cout, generator=g) * 0.1
+    out = torch.full((N, H, W, 96), 3.0, dtype=dtype, device=dev)
+    wp = _ext.gemm_pack_weights(wt.to(dev), dtype)
+    _ext.gemm1x1_nhwc(x.to(dev)[..., 16:16 + cin], cin, wp, cout, out[..., 64:64 + cout], bias=b.to(dev),
+                      act=_ext.KAD_ACT_SILU)
+    torch.cuda.synchronize()
+    got = out.cpu().double()
+    assert (got[..., :64] == 3.0).all() and (got[..., 88:] == 3.0).all()
+    assert (got[..., 84:88] == 0).all()
+    wq = wt.to(dtype).double() if dtype != torch.float32 else wt.double()
+    ref = F.silu(torch.einsum('nhwc,oc->nhwo', x[..., 16:16 + cin].double(), wq) + b.double())
+    check_close(got[..., 64:84], ref, dtype, f'gemm into slice {dt}')
+
+
+@pytest.mark.parametrize('dt', ['f32', 'f16'])
+def test_ddetect_decode_matches_oracle(dt):
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(11)
+    sizes, strides, nc = [(12, 10), (6, 5), (3, 3)], [8.0, 16.0, 32.0], 20
+    heads_nchw = [(torch.randn(2, 84, h, w, generator=g) * 3).to(dtype) for h, w in sizes]
+    heads = []
+    for t in heads_nchw:
+        buf = torch.zeros(2, t.shape[2], t.shape[3], 88, dtype=dtype)
+        buf[..., :84] = _nhwc(t)
+        heads.append(buf.to(dev))
+    A = sum(h * w for h, w in sizes)
+    y = torch.empty(2, 4 + nc, A, dtype=dtype, device=dev)
+    _ext.ddetect_decode(heads, strides, y, nc, reg_max=16, box_ch=64)
+    torch.cuda.synchronize()
+    ref = KO.ddetect_decode([t.double() for t in heads_nchw], strides, nc)
+    got = y.cpu().double()
+    # boxes: relative to their scale (up to ~500 px); class probabilities: absolute
+    box_tol = 1e-5 if dtype == torch.float32 else 2e-3
+    assert (got[:, :4] - ref[:, :4]).abs().max().item() <= box_tol * ref[:, :4].abs().max().item()
+    check_close(got[:, 4:], ref[:, 4:], dtype, 'decode classes')
+
+
+@pytest.mark.parametrize('n,spread', [(3000, 100.0), (500, 20.0), (1, 10.0), (20000, 400.0)])
+def test_nms_matches_oracle(n, spread):
+    """kad_nms (bitmask + sweep) keeps exactly the oracle's indices, in order, on
+    random overlapping boxes with score ties (fp16-like quantised scores)."""
+    from kadcnet import postprocess
+    rng = np.random.default_rng(n)
+    xy = rng.uniform(0, spread, (n, 2))
+    wh = rng.uniform(2, 30, (n, 2))
+    boxes = np.concatenate((xy, xy + wh), 1).astype(np.float32)
+    scores = np.round(rng.uniform(0, 1, n) * 64) / 64      # many exact ties
+    print(f'nms n={n}', flush=True)
+    got = postprocess.nms(torch.from_numpy(boxes).cuda(), torch.from_numpy(scores).float().cuda(), 0.45)
+    torch.cuda.synchronize()
+    ref = KO.nms(boxes, scores, 0.45)
+    assert got.cpu().tolist() == ref
+
+
+# ---------------------------------------------------------------------------- network
+def _model(dtype, seed=0, fuse=False):
+    import kadcnet
+    m = kadcnet.build_kadcnet_s(seed=seed)
+    if fuse:
+        m = m.fuse()
+    sd = {k: v.detach().to(dtype).double() for k, v in m.state_dict().items()}
+    return m.to('cuda', dtype).eval(), sd
+
+
+def _rel(got, ref):
+    return (got - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+
+
+@pytest.mark.parametrize('dt,fuse', [('f32', False), ('f16', True), ('bf16', True)])
+def test_kadcnet_plan_matches_oracle(dt, fuse):
+    """Whole network, layer by layer, at [2, 3, 256, 192] (non-square; 4 x 3 cells at
+    stride 64 under the deepest KAD-Conv branch), unfused (BN folded by the plan)
+    and fused models."""
+    import kadcnet
+    dtype = DT[dt]
+    m, sd = _model(dtype, seed=1, fuse=fuse)
+    x = torch.rand(2, 3, 256, 192, generator=torch.Generator().manual_seed(2)).to(dtype)
+    plan = kadcnet.KADCNetPlan(m)
+    with torch.no_grad():
+        (y, heads), layers = plan.forward(x.cuda(), keep_layers=True)
+    torch.cuda.synchronize()
+    ref_layers = []
+    yo, ho = KO.kadcnet_forward(sd, kadcnet.DIOR_S_BASE, x.double(), layers=ref_layers)
+    tol = {'f32': 1e-4, 'f16': 1e-2, 'bf16': 3e-2}[dt]
+    worst = []
+    for i, (a, b) in enumerate(zip(layers[:-1], ref_layers)):
+        r = _rel(a.permute(0, 3, 1, 2).double().cpu(), b)
+        worst.append(r)
+        print(f'layer {i}: rel {r:.2e}', flush=True)
+    for l, (a, b) in enumerate(zip(heads, ho)):
+        r = _rel(a.double().cpu(), b)
+        print(f'head {l}: rel {r:.2e} max|ref| {b.abs().max().item():.2f}', flush=True)
+        assert r <= tol, f'head {l} {dt}: rel {r:.2e} > {tol}'
+    ry = _rel(y.double().cpu()[:, :4], yo[:, :4])
+    print(f'boxes: rel {ry:.2e}', flush=True)
+    assert ry <= tol
+    assert max(worst) <= tol, f'worst layer rel {max(worst):.2e}'
+    if dtype == torch.float32:
+        check_close(y.cpu()[:, 4:], yo[:, 4:], dtype, 'class probabilities')
+
+
+def test_kadcnet_fast_switch_and_graph_replay():
+    """kadcnet.enable_fast_inference installs the plan (CPU inputs still take the
+    plain forward); HIP-graph replays of the plan equal the eager forward bit for
+    bit, with eager work between replays."""
+    import kadcnet
+    m, _ = _model(torch.float16, seed=2, fuse=True)
+    kadcnet.enable_fast_inference(m)
+    assert hasattr(m, '_kad_plan')
+    static_x = torch.rand(2, 3, 160, 160, generator=torch.Generator().manual_seed(0)).half().cuda()
+    with torch.no_grad():
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            m(static_x)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            static_y, _ = m(static_x)
+        for seed in (1, 2):
+            xin = torch.rand(2, 3, 160, 160, generator=torch.Generator().manual_seed(seed)).half().cuda()
+            ref = m(xin)[0].clone()
+            torch.cuda.synchronize()
+            static_x.copy_(xin)
+            g.replay()
+            torch.cuda.synchronize()
+            print(f'kadcnet graph replay {seed}', flush=True)
+            assert torch.equal(static_y, ref)
+    kadcnet.disable_fast_inference(m)
+    assert 'forward' not in vars(m)
+
+
+def test_kadcnet_config5_full_size():
+    """batch 16, 3 x 800 x 800 ~U[0, 1], fp16, fused model.  The
+    batch runs on the HIP plan; images 0 and 15 are checked against the float32
+    CPU oracle (every computation is per image).  NMS (conf_thres 0, the class
+    logits of a random-init head sit near -10) then runs on both y's: the HIP NMS
+    on the HIP y must keep exactly what the oracle NMS keeps on that y, and the top
+    100 detections of the HIP path and of the oracle agree by anchor and class."""
+    import kadcnet
+    dtype = torch.float16
+    m, sd = _model(dtype, seed=0, fuse=True)
+    sd32 = {k: v.float() for k, v in sd.items()}
+    x = torch.rand(16, 3, 800, 800, generator=torch.Generator().manual_seed(0)).to(dtype)
+    plan = kadcnet.KADCNetPlan(m)
+    print('config 5: HIP forward', flush=True)
+    with torch.no_grad():
+        y, heads = plan.forward(x.cuda())
+    torch.cuda.synchronize()
+    assert y.shape == (16, 24, 13125) and torch.isfinite(y).all()
+    for img in (0, 15):
+        print(f'config 5: oracle image {img}', flush=True)
+        yo, ho = KO.kadcnet_forward(sd32, kadcnet.DIOR_S_BASE, x[img:img + 1].float())
+        for l, (a, b) in enumerate(zip(heads, ho)):
+            r = _rel(a[img:img + 1].double().cpu(), b.double())
+            print(f'  head {l}: rel {r:.2e}', flush=True)
+            assert r <= 1e-2
+        assert _rel(y[img:img + 1, :4].double().cpu(), yo[:, :4].double()) <= 1e-2
+        # NMS: the HIP kernels against the oracle's NMS on the same (HIP) prediction
+        det = kadcnet.non_max_suppression(y[img:img + 1].float(), conf_thres=0.0, iou_thres=0.45, max_det=300)[0]
+        det_ref = KO.non_max_suppression(y[img:img + 1].float().cpu(), conf_thres=0.0, iou_thres=0.45, max_det=300)[0]
+        assert det.shape == det_ref.shape and torch.equal(det.cpu(), det_ref), 'HIP NMS differs from the oracle NMS'
+        # end to end: the strongest detections of both paths
+        top = torch.argsort(y[img, 4:].float().amax(0).cpu(), descending=True, stable=True)[:100]
+        top_ref = torch.argsort(yo[0, 4:].amax(0), descending=True, stable=True)[:100]
+        overlap = len(set(top.tolist()) & set(top_ref.tolist()))
+        print(f'  top-100 anchors shared: {overlap}', flush=True)
+        assert overlap >= 90
+        cls = y[img, 4:].float().argmax(0).cpu()[top_ref]
+        cls_ref = yo[0, 4:].argmax(0)[top_ref]
+        assert (cls == cls_ref).float().mean() >= 0.95

@@ -1,15 +1,17 @@
 """Benchmark of the KAD-Conv inference hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--no-cpu] [--per-op-only]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-ops] [--no-cpu] [--no-kadcnet]
+                    [--per-op-only] [--kadcnet-only]
 
 Step = one fused KADConv(256) forward on x [8, 256, 100, 100] fp16 (BASELINE
 config 2's metric shape), inputs resident in HBM, weights random from a seed
 (synthetic; no checkpoint exists offline).  The forward is captured once in a
-HIP graph and replayed (the reference protocol, KAD-CNet/inference/benchmark_s.py:9-25);
-K replays are timed between events after W warm-up replays.
+HIP graph and replayed (the reference protocol, KAD-CNet/inference/benchmark_s.py:9-25):
+W warm-up replays, then 3 trials of K replays timed between events; the
+median trial is reported.
 
 Printed: one JSON line with
-  value / ms_per_step      microseconds per forward (lower is better);
+  value / ms_per_step      microseconds per forward (lower is better), median of 3 trials;
   roofline                 the dominant kernel (branch-0 DCN) timed alone with
                            events on its launch stream: algorithmic FLOPs / duration
                            against the fp16 dense MFMA peak;
@@ -17,8 +19,13 @@ Printed: one JSON line with
                            over the measured time;
   cpu_baseline             the oracle's fp32 CPU restatement of the reference forward
                            (plain PyTorch ops), same shape, on this host's cores;
-  stages                   per-stage event timings of one forward;
-  per_op                   the other BASELINE configs (DSC, KADDown, 1x1+SiLU, SE).
+  stages_us                per-stage event timings of one forward;
+  kadcnet_s_img_per_s      BASELINE config 5: KAD-CNet-S forward, batch 16, 800 x 800, fp16
+                           (details and its CPU baseline under kadcnet_s);
+  per_op                   configs 2-4 (DSC, KADDown, 1x1+SiLU, SE): GPU us, floor, and the
+                           oracle's fp32 CPU us of the same workload;
+  config1                  config 1: KADConv(64) / DSC(64) at [1, 64, 80, 80] fp32, the plain
+                           CPU forward, the oracle's CPU time and the GPU fast path.
 """
 import argparse
 import json
@@ -41,8 +48,11 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_graph(fn, steps, warmup):
-    """Capture fn in a graph, replay warmup + steps times, return us per replay."""
+def time_graph(fn, steps, warmup, trials=3):
+    """Capture fn in a graph, replay it `warmup` times, then time `trials` runs of
+    `steps` replays between events (the reference protocol,
+    KAD-CNet/inference/benchmark_s.py:9-25).  Returns (median us per replay,
+    [us per replay of each trial], graph)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -55,13 +65,16 @@ def time_graph(fn, steps, warmup):
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
-    a, b = _events()
-    a.record()
-    for _ in range(steps):
-        g.replay()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) * 1e3 / steps, g
+    vals = []
+    for _ in range(trials):
+        a, b = _events()
+        a.record()
+        for _ in range(steps):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        vals.append(a.elapsed_time(b) * 1e3 / steps)
+    return sorted(vals)[len(vals) // 2], vals, g
 
 
 def time_eager(fn, steps, warmup=3):
@@ -100,28 +113,12 @@ def cpu_baseline(shape, runs=5, warmup=2):
     (oracle/kadconv_oracle.py:kadconv_forward), timed on this host."""
     from oracle import kadconv_oracle as O
     threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
     sd = metric_state(shape[1])
     x = torch.randn(*shape, generator=torch.Generator().manual_seed(0))
-    ts = []
-    with torch.no_grad():
-        for i in range(warmup + runs):
-            t0 = time.perf_counter()
-            O.kadconv_forward(sd, x)
-            if i >= warmup:
-                ts.append(time.perf_counter() - t0)
-    ts.sort()
-    cpu_model = ''
-    try:
-        for line in open('/proc/cpuinfo'):
-            if line.startswith('model name'):
-                cpu_model = line.split(':', 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {'value': ts[len(ts) // 2] * 1e6, 'unit': 'us', 'cores': torch.get_num_threads(), 'kind': 'port',
+    sec = _cpu_time(lambda: O.kadconv_forward(sd, x), runs=runs, warmup=warmup)
+    return {'value': sec * 1e6, 'unit': 'us', 'cores': torch.get_num_threads(), 'kind': 'port',
             'sample': f'full workload x{list(shape)} fp32, median of {runs} after {warmup} warm-up runs '
-                      f'(os.cpu_count={os.cpu_count()}, affinity={threads}, cpu="{cpu_model}")'}
+                      f'(os.cpu_count={os.cpu_count()}, affinity={threads}, cpu="{_cpu_model()}")'}
 
 
 def per_op_workloads():
@@ -162,13 +159,127 @@ def per_op_workloads():
     return out
 
 
-def per_op(steps, warmup):
-    """The other BASELINE configs, graph-timed (us per call) with their floors."""
+def _cpu_model():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return ''
+
+
+def _cpu_time(fn, runs=5, warmup=2):
+    """Median seconds of fn() on this host's cores (all threads of the affinity set)."""
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    ts = []
+    with torch.no_grad():
+        for i in range(warmup + runs):
+            t0 = time.perf_counter()
+            fn()
+            if i >= warmup:
+                ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def per_op_cpu():
+    """The oracle's fp32 CPU restatement of each per-op workload (the reference's plain
+    PyTorch path, torchvision's deform_conv2d restated), same shapes and seeds as
+    per_op_workloads(): name -> median us."""
+    from kadconv import synthetic as S
+    from oracle import kadconv_oracle as O
+    out = {}
+    g = torch.Generator().manual_seed(0)
+    for C, H in [(128, 100), (256, 50), (512, 25)]:
+        sd = S.make_dsc_state(C, C, seed=C, offset_std_px=2.0)
+        x = torch.randn(8, C, H, H, generator=g)
+        out[f'dsc_{C}x{H}'] = _cpu_time(lambda sd=sd, x=x: O.dsc_forward(sd, '', x)) * 1e6
+    sd = S.make_kaddown_state(256, 512)
+    x = torch.randn(8, 256, 100, 100, generator=g)
+    out['kaddown_256to512_100'] = _cpu_time(lambda: O.kaddown_forward(sd, x)) * 1e6
+    w, b = torch.randn(512, 512) * 0.02, torch.randn(512) * 0.02
+    x = torch.randn(16, 512, 50, 50, generator=g)
+    out['conv1x1_silu_512_50'] = _cpu_time(lambda: O.conv1x1_silu(x, w, b)) * 1e6
+    se = torch.nn.Sequential(torch.nn.Linear(1024, 64), torch.nn.ReLU(), torch.nn.Linear(64, 1024))
+    p = [t.detach() for t in (se[0].weight, se[0].bias, se[2].weight, se[2].bias)]
+    x = torch.randn(16, 1024, 25, 25, generator=g)
+    out['se_1024_25'] = _cpu_time(lambda: O.se_forward(x, *p)) * 1e6
+    return out
+
+
+def per_op(steps, warmup, cpu=True):
+    """The other BASELINE configs, graph-timed (median of 3 trials, us per call) with
+    their floors, and the oracle's fp32 CPU time of the same workload."""
     res = {}
     for name, fn, floor in per_op_workloads():
-        us, _ = time_graph(fn, steps, warmup)
-        res[name] = {'us': round(us, 2), 'floor_us': round(floor, 2), 'frac': round(floor / us, 4)}
+        us, trials, _ = time_graph(fn, steps, warmup)
+        res[name] = {'us': round(us, 2), 'trials_us': [round(t, 2) for t in trials], 'floor_us': round(floor, 2),
+                     'frac': round(floor / us, 4)}
+    if cpu:
+        for name, us in per_op_cpu().items():
+            res[name]['cpu_us'] = round(us, 1)
     return res
+
+
+def config1(steps, warmup, cpu=True):
+    """KADConv(64) and DSC(64) on [1, 64, 80, 80] fp32, every weight
+    kaiming-uniform from seed 0.  Reported: the product's plain CPU forward (the
+    plumbing the config asks for), the oracle's (the reference's plain path restated),
+    and the fast HIP forward on the GPU for scale."""
+    import kadconv
+    from kadconv import synthetic as S
+    from oracle import kadconv_oracle as O
+    out = {}
+    x = torch.randn(1, 64, 80, 80, generator=torch.Generator().manual_seed(0))
+    for name, mk, sdf, ref in [
+            ('kadconv_64_80_f32', lambda: kadconv.KADConv(64), lambda: S.make_kadconv_state(64, seed=0),
+             lambda sd: O.kadconv_forward(sd, x)),
+            ('dsc_64_80_f32', lambda: kadconv.DSC(64, 64), lambda: S.make_dsc_state(64, 64, seed=0),
+             lambda sd: O.dsc_forward(sd, '', x))]:
+        m = mk()
+        sd = sdf()
+        m.load_state_dict(sd, strict=False)
+        m.eval()
+        row = {}
+        if cpu:
+            row['cpu_plain_us'] = round(_cpu_time(lambda: m(x)) * 1e6, 1)
+            row['cpu_us'] = round(_cpu_time(lambda: ref(sd)) * 1e6, 1)
+        md = m.to('cuda')
+        kadconv.enable_fast_inference(md)
+        xd = x.cuda()
+        with torch.no_grad():
+            us, _, _ = time_graph(lambda: md(xd), steps, warmup)
+        row['us'] = round(us, 2)
+        out[name] = row
+    return out
+
+
+def kadcnet_s(iterations, warmup, cpu=True, batch=16, hw=800):
+    """the whole KAD-CNet-S forward (fused model, random init from
+    seed 0, kadcnet.build_kadcnet_s), batch 16, 3 x 800 x 800 ~U[0, 1], fp16,
+    model forward only (no NMS), HIP-graph replay, median of 3 trials
+    (KAD-CNet/inference/benchmark_s.py:9-25).  CPU baseline: the oracle's fp32
+    restatement on a bounded sample of 2 images of the batch (img/s)."""
+    import kadcnet
+    model = kadcnet.build_kadcnet_s(seed=0).fuse()
+    m = model.to('cuda', torch.float16).eval()
+    kadcnet.enable_fast_inference(m)
+    x = torch.rand(batch, 3, hw, hw, generator=torch.Generator().manual_seed(0))
+    xd = x.to('cuda', torch.float16)
+    with torch.no_grad():
+        us, trials, _ = time_graph(lambda: m(xd), iterations, warmup)
+    out = {'img_per_s': round(batch / (us * 1e-6), 1), 'ms_per_batch': round(us / 1e3, 3),
+           'trials_ms': [round(t / 1e3, 3) for t in trials], 'batch': batch, 'hw': [hw, hw], 'dtype': 'f16',
+           'iterations': iterations, 'warmup': warmup}
+    if cpu:
+        from oracle import kadcnet_oracle as KO
+        sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+        xs = x[:2].float()
+        sec = _cpu_time(lambda: KO.kadcnet_forward(sd, kadcnet.DIOR_S_BASE, xs), runs=3, warmup=1)
+        out['cpu_baseline'] = {'value': round(2 / sec, 3), 'unit': 'img/s', 'cores': torch.get_num_threads(),
+                               'kind': 'port', 'sample': f'2 of the 16 images, fp32, median of 3 after 1 warm-up '
+                                                         f'(cpu="{_cpu_model()}")'}
+    return out
 
 
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'dsc0_traffic.json')
@@ -359,6 +470,10 @@ def main():
                     help='print the per-kernel counter table from a kernel trace and three --pmc CSVs')
     ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
                     help='compute profiles/dsc0_traffic.json from the two --pmc counter CSVs')
+    ap.add_argument('--no-kadcnet', action='store_true', help='skip the KAD-CNet-S (config 5) throughput')
+    ap.add_argument('--kadcnet-iters', type=int, default=20, help='graph replays per trial for config 5')
+    ap.add_argument('--kadcnet-only', action='store_true',
+                    help='print only the config-5 throughput (a short program for rocprofv3 kernel traces)')
     ap.add_argument('--trace-md', nargs='+', metavar='ARG',
                     help='TRACE_CSV TITLE COMMAND [DESCRIPTION]: print the markdown summary of a kernel trace')
     args = ap.parse_args()
@@ -379,7 +494,10 @@ def main():
         return
     if args.per_op_only:
         with torch.no_grad():
-            print(json.dumps(per_op(args.steps, args.warmup)))
+            print(json.dumps(per_op(args.steps, args.warmup, cpu=False)))
+        return
+    if args.kadcnet_only:
+        print(json.dumps(kadcnet_s(args.kadcnet_iters, 5, cpu=False)), flush=True)
         return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU: every GPU box of this build has one MI355X and the KAD-Conv forward '
@@ -398,7 +516,7 @@ def main():
     with torch.no_grad():
         # whole forward, graph-replayed; bracket with synchronize (one rank: no barrier needed)
         torch.cuda.synchronize()
-        us, _ = time_graph(lambda: m(x), args.steps, args.warmup)
+        us, trials, _ = time_graph(lambda: m(x), args.steps, args.warmup)
 
         # dominant kernel alone: branch-0 DCN, events on the stream it is launched on
         plan = m._kad_plan
@@ -424,6 +542,7 @@ def main():
         'steps': args.steps,
         'warmup': args.warmup,
         'ms_per_step': round(us / 1e3, 6),
+        'trials_us': [round(t, 3) for t in trials],
         'higher_is_better': False,
         'scaling': 'weak',
         'vs_baseline': None,
@@ -434,6 +553,8 @@ def main():
                    'batch': 8, 'channels': 256, 'hw': [100, 100], 'branches': 3},
         'roofline': {'bound': 'mfma', 'achieved': round(achieved / 1e12, 3), 'peak': PEAK_MFMA_F16 / 1e12,
                      'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_MFMA_F16, 4), 'traffic': traffic,
+                     'traffic_source': 'profiles/dsc0_traffic.json (FETCH_SIZE / WRITE_SIZE of bench.py '
+                                       '--traffic-probe, scaled by a 64 MiB copy); not measured in this run',
                      'kernel': 'dcn_fwd_kernel<half,half,6,FUSED> (branch-0 DSC: conv_offset + DCN, c=86, '
                                '8x100x100)', 'kernel_us': round(dcn_us, 3),
                      'flops_per_launch': flops},
@@ -441,8 +562,13 @@ def main():
         'stages_us': stage_us,
         'kadcnet_s_img_per_s': None,
     }
+    if not args.no_kadcnet:
+        ks = kadcnet_s(args.kadcnet_iters, 5, cpu=not args.no_cpu)
+        out['kadcnet_s_img_per_s'] = ks['img_per_s']
+        out['kadcnet_s'] = ks
     if not args.no_ops:
-        out['per_op'] = per_op(max(args.steps // 4, 20), 5)
+        out['per_op'] = per_op(max(args.steps // 4, 20), 5, cpu=not args.no_cpu)
+        out['config1'] = config1(max(args.steps // 4, 20), 5, cpu=not args.no_cpu)
     if not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline(shape)
     else:

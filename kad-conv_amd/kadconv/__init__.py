@@ -2,9 +2,12 @@
 
 Public API of the reference (KAD-Conv/kadconv/__init__.py:1-4): ``KADConv``,
 ``DSC``, ``LCSA``, ``enable_fast_inference``, ``disable_fast_inference``.
-Added here: ``deform_conv2d`` (torchvision-compatible DCNv2 on the GPU) and
-the fused blocks ``Conv1x1SiLU``, ``SqueezeExcitation`` and ``KADDown``.
+Added here: ``deform_conv2d`` (torchvision-compatible DCNv2 on the GPU), the
+fused blocks ``Conv1x1SiLU``, ``SqueezeExcitation`` and ``KADDown``, and the
+typed custom operators ``torch.ops.kadconv.deform_conv2d`` /
+``torch.ops.kadconv.layer_fwd`` (kadconv.library).
 """
+from . import library  # registers the kadconv:: custom operators
 from .blocks import Conv1x1SiLU, KADDown, SqueezeExcitation
 from .fast import disable_fast_inference, enable_fast_inference
 from .kad_conv import DSC, LCSA, KADConv

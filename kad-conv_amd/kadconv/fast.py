@@ -24,7 +24,7 @@ import types
 
 import torch
 
-from . import _ext
+from . import _ext, library
 from .fused import DSCPlan, KADConvPlan
 
 _LAYER_TYPES = {'KADConv', 'KADC4', 'KADC4_m'}
@@ -37,15 +37,20 @@ def _is_gfx950(device):
 
 
 def _install(module, plan):
+    """Replace the instance's forward: eligible eval-mode calls run the plan through the
+    typed custom op kadconv::layer_fwd (so torch.compile traces it as one operator),
+    everything else the class's plain forward."""
     plain = types.MethodType(type(module).forward, module)
+    handle = library.register_plan(plan)
 
     def forward(x):
         if module.training or not plan.eligible(x):
             return plain(x)
         with torch.no_grad():
-            return plan.forward(x)
+            return torch.ops.kadconv.layer_fwd(x, handle)
 
     module._kad_plan = plan
+    module._kad_handle = handle
     module.forward = forward
 
 
@@ -91,4 +96,7 @@ def disable_fast_inference(model):
             del m.forward
             if hasattr(m, '_kad_plan'):
                 del m._kad_plan
+            if hasattr(m, '_kad_handle'):
+                library.release_plan(m._kad_handle)
+                del m._kad_handle
     return model

@@ -93,6 +93,10 @@ class DSCPlan:
         return (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float16, torch.bfloat16)
                 and x.shape[1] == self.cin and self.stride == 1 and self.pad == 1 and x.numel() > 0)
 
+    def out_shape(self, h, w):
+        """(Cout, Ho, Wo) of the forward on an h x w input."""
+        return self.cout, (h + 2 * self.pad - 3) // self.stride + 1, (w + 2 * self.pad - 3) // self.stride + 1
+
     def stages(self, y, n, h, w, out, out_layout, bias=None, post_mul=None, post_add=None, post_scale=None,
                relu=False, gap=None, tag='', sums=None, se=None, mask_split=True, x_nchw=None):
         """DSC on an NHWC map y [N, h, w, cs] (cin channels) as a list of
@@ -209,6 +213,10 @@ class KADConvPlan:
             return False
         s = 2 ** (self.n - 1)
         return x.shape[2] >= s and x.shape[3] >= s
+
+    def out_shape(self, h, w):
+        """(C, H, W): shape-preserving."""
+        return self.dim, h, w
 
     def stages(self, x):
         """The fused forward as (name, launch) pairs in stream order; returns (stages, out)."""

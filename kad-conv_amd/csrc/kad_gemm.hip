@@ -382,6 +382,136 @@ __global__ void gemm_pack_kernel(const float* w, T* out, int cin, int cout, int 
   }
 }
 
+// ---- NHWC fast path ---------------------------------------------------------------------------------
+// 16-bit NHWC input and output, no pooling, Cin a multiple of 8 (whole 16-byte channel pieces).
+// In NHWC both MFMA operands are contiguous 16-byte runs, so a wave loads them straight from
+// memory into registers, with no LDS staging and no barriers:
+//  * A = weights, 16 output channels x 32 input channels: lane (r, g) reads row r's input
+//    channels 8g .. 8g + 7 of the packed [Cout_pad][Cin_pad] rows (L2-resident, shared by all waves);
+//  * B = input, 32 input channels x 16 pixels: lane (c, g) reads pixel c's channels 8g .. 8g + 7
+//    (four lanes cover a pixel's 64 contiguous bytes of the k-step).
+// A wave owns 64 pixels (4 pixel fragments) x 16 NB output channels.  The accumulator of
+// (pixel fragment m, channel fragment f) in lane (c, g) holds output channels 16 f + 4 g .. + 3
+// of pixel 16 m + c: one 8-byte store.  The next k-step's operands are loaded before this step's
+// MFMAs.  Input channels past Cin inside a k-step are read as 0 (they may belong to another slice
+// of a concat buffer); weight rows past Cout are zero in the packing.
+constexpr int GH_PXW = 64;    // pixels per wave
+constexpr int GH_WAVES = 4;   // waves per block (independent work items)
+
+template <typename T, int NB>
+__global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args a, int P, int tiles_px, int co_blocks,
+                                                                 int total, int cin_pad) {
+  typedef typename GemmOps<T>::frag frag;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int item = blockIdx.x * GH_WAVES + wave;
+  if (item >= total) return;
+  const int cb = item % co_blocks;  // the channel blocks of a pixel tile run in neighbouring waves
+  const int t = item / co_blocks;
+  const int n = t / tiles_px, p0 = (t - n * tiles_px) * GH_PXW;
+  const int co0 = cb * NB * 16;
+  const int c = lane & 15, g = lane >> 4;
+  const T* x = (const T*)a.x + (int64_t)n * P * a.x_cs;
+  const T* wt = (const T*)a.wpack;
+  const T* xp[4];
+  bool pok[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int p = p0 + 16 * m + c;
+    pok[m] = p < P;
+    xp[m] = x + (int64_t)(pok[m] ? p : 0) * a.x_cs + 8 * g;
+  }
+  const T* wr[NB];
+#pragma unroll
+  for (int f = 0; f < NB; ++f) wr[f] = wt + (int64_t)(co0 + 16 * f + c) * cin_pad + 8 * g;
+  floatx4 acc[4][NB];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int f = 0; f < NB; ++f) acc[m][f] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const frag zero = frag{};
+  frag xa[4], wa[NB];
+  auto load = [&](int k0, frag* xv, frag* wv) {
+    const bool kok = k0 + 8 * g < a.cin;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) xv[m] = (pok[m] && kok) ? *(const frag*)(xp[m] + k0) : zero;
+#pragma unroll
+    for (int f = 0; f < NB; ++f) wv[f] = *(const frag*)(wr[f] + k0);
+  };
+  load(0, xa, wa);
+  for (int k0 = 0; k0 < cin_pad; k0 += 32) {
+    frag xn[4], wn[NB];
+    const bool more = k0 + 32 < cin_pad;
+    if (more) load(k0 + 32, xn, wn);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int f = 0; f < NB; ++f) acc[m][f] = GemmOps<T>::mma(wa[f], xa[m], acc[m][f]);
+    if (more) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) xa[m] = xn[m];
+#pragma unroll
+      for (int f = 0; f < NB; ++f) wa[f] = wn[f];
+    }
+  }
+  // ---- epilogue: bias, activation, 8-byte stores of 4 channels; zero the pad channels ----------
+  const int cpad = round_up(a.cout, 8) < a.out_cs ? round_up(a.cout, 8) : a.out_cs;
+  T* out = (T*)a.out + (int64_t)n * P * a.out_cs;
+#pragma unroll
+  for (int f = 0; f < NB; ++f) {
+    const int co = co0 + 16 * f + 4 * g;
+    if (co >= cpad) continue;
+    float b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = (a.bias && co + i < a.cout) ? a.bias[co + i] : 0.f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      if (!pok[m]) continue;
+      T o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = acc[m][f][i] + b[i];
+        if (a.act == 1) v = v * sigmoidf_(v);
+        o[i] = from_f32<T>(co + i < a.cout ? v : 0.f);
+      }
+      T* dst = out + (int64_t)(p0 + 16 * m + c) * a.out_cs + co;
+      if (co + 4 <= cpad) {
+        *(half4_t*)dst = __builtin_bit_cast(half4_t, o);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (co + i < cpad) dst[i] = o[i];
+      }
+    }
+  }
+}
+
+// The NHWC fast path covers 16-bit NHWC -> NHWC without pooling when Cin and the input channel
+// stride are multiples of 8 (16-byte pieces) and the output stride a multiple of 4 (8-byte stores).
+static bool nhwc_fast_ok(const kad_gemm_args& a) {
+  return a.dtype != KAD_F32 && a.pool == 1 && a.in_layout == KAD_NHWC && a.out_layout == KAD_NHWC &&
+         a.cin % 8 == 0 && a.x_cs % 8 == 0 && a.out_cs % 4 == 0 && ((uintptr_t)a.x % 16) == 0 &&
+         ((uintptr_t)a.out % 8) == 0;
+}
+
+template <typename T, int NB>
+static void launch_gemm_nhwc_nb(const kad_gemm_args& a, hipStream_t st) {
+  const int P = a.h * a.w;
+  const int tiles_px = ceil_div(P, GH_PXW), co_blocks = ceil_div(round_up(a.cout, 8), NB * 16);
+  const int total = a.n * tiles_px * co_blocks;
+  hipLaunchKernelGGL((gemm_nhwc_kernel<T, NB>), dim3(ceil_div(total, GH_WAVES)), dim3(64 * GH_WAVES), 0, st, a, P,
+                     tiles_px, co_blocks, total, round_up(a.cin, 32));
+}
+
+template <typename T>
+static int launch_gemm_nhwc(const kad_gemm_args& a, hipStream_t st) {
+  const int nf = ceil_div(round_up(a.cout, 8), 16);  // 16-channel fragments of the output
+  if (nf <= 1) launch_gemm_nhwc_nb<T, 1>(a, st);
+  else if (nf <= 2) launch_gemm_nhwc_nb<T, 2>(a, st);
+  else if (nf <= 4) launch_gemm_nhwc_nb<T, 4>(a, st);
+  else launch_gemm_nhwc_nb<T, 8>(a, st);
+  return check_launch("kad_gemm1x1_fwd");
+}
+
 template <typename T, int NBF>
 static int launch_gemm(const kad_gemm_args& a, hipStream_t st, int hp, int wp) {
   const int P = hp * wp;
@@ -433,8 +563,10 @@ static bool nchw_fast_ok(const kad_gemm_args& a) {
 
 template <typename T>
 static int dispatch_gemm(const kad_gemm_args& a, hipStream_t st, int hp, int wp) {
-  if constexpr (sizeof(T) == 2)
+  if constexpr (sizeof(T) == 2) {
     if (nchw_fast_ok(a)) return launch_gemm_nchw<T>(a, st);
+    if (nhwc_fast_ok(a)) return launch_gemm_nhwc<T>(a, st);
+  }
   const int ncols = a.out_layout == KAD_NHWC ? round_up(a.cout, 8) : a.cout;
   const int nbf = ceil_div(ncols, 16);
   switch (nbf < 8 ? nbf : 8) {

@@ -124,6 +124,41 @@ def test_gemm1x1_into_slice(dt):
     check_close(got[..., 64:84], ref, dtype, f'gemm into slice {dt}')
 
 
+@pytest.mark.parametrize('dt', ['f16', 'bf16'])
+@pytest.mark.parametrize('n,p,cin,cout,act', [(2, 1000, 8, 20, 'silu'), (1, 4096, 72, 64, 'silu'),
+                                              (3, 130, 360, 300, 'none'), (2, 77, 504, 192, 'silu'),
+                                              (1, 64, 64, 84, 'none')])
+def test_gemm1x1_nhwc_fast_path(dt, n, p, cin, cout, act):
+    """The NHWC MFMA path of kad_gemm1x1_fwd: input read from a slice whose
+    neighbouring channels hold NaN (channels past Cin inside a k-step must not be
+    used), ragged pixel counts, Cout not a multiple of 16, several 128-channel
+    blocks; output into a slice, its pad channels zeroed and the rest untouched."""
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(p + cin + cout)
+    xs = torch.full((n, p, 1, cin + 40), float('nan'))
+    xv = torch.randn(n, p, 1, cin, generator=g)
+    xs[..., 8:8 + cin] = xv
+    wt = torch.randn(cout, cin, generator=g) * (0.5 / cin ** 0.5)
+    b = torch.randn(cout, generator=g) * 0.1
+    ocs = (cout + 7) // 8 * 8 + 24
+    out = torch.full((n, p, 1, ocs), 3.0, dtype=dtype, device=dev)
+    wp = _ext.gemm_pack_weights(wt.to(dev), dtype)
+    code = _ext.KAD_ACT_SILU if act == 'silu' else _ext.KAD_ACT_NONE
+    print(f'gemm nhwc {dt} n={n} p={p} {cin}->{cout} {act}', flush=True)
+    _ext.gemm1x1_nhwc(xs.to(dtype).to(dev)[..., 8:8 + cin], cin, wp, cout, out[..., 8:8 + cout], bias=b.to(dev),
+                      act=code)
+    torch.cuda.synchronize()
+    got = out.cpu().double()
+    c8 = (cout + 7) // 8 * 8
+    assert (got[..., :8] == 3.0).all() and (got[..., 8 + c8:] == 3.0).all()
+    assert (got[..., 8 + cout:8 + c8] == 0).all()
+    ref = torch.einsum('nhwc,oc->nhwo', xv.to(dtype).double(), wt.to(dtype).double()) + b.double()
+    if act == 'silu':
+        ref = F.silu(ref)
+    check_close(got[..., 8:8 + cout], ref, dtype, f'gemm nhwc {dt} {cin}->{cout}')
+
+
 @pytest.mark.parametrize('dt', ['f32', 'f16'])
 def test_ddetect_decode_matches_oracle(dt):
     from kadconv import _ext

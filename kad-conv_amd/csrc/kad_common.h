@@ -97,6 +97,9 @@ __device__ __forceinline__ void src_index(int dst, int in, int out, float scale,
   l1 = s - (float)i0;
 }
 
+// 8 consecutive elements, moved as 16-byte (16-bit types) or 2 x 16-byte (fp32) pieces.
+template <typename T> struct alignas(16) Vec8 { T v[8]; };
+
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ inline int round_up(int a, int b) { return ceil_div(a, b) * b; }
 

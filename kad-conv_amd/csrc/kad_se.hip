@@ -786,6 +786,71 @@ __global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
   }
 }
 
+// NHWC output, window and channel count multiples of 8: one thread per (pixel, 8-channel group),
+// 16-byte loads of the residual and 16-byte stores.  Each channel takes its value from the branch
+// whose window holds it; a branch at the output's resolution is read at the pixel itself (it may be
+// the output's own channel slice: the thread reads it before writing the same 16 bytes), an
+// upsampled one through its four bilinear corners, whose row / column indices are computed once
+// per thread and branch.  Lets a channels-last KAD-Conv merge all its branches in one launch.
+template <typename T>
+__global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, int64_t npix, int ngroups) {
+  typedef Vec8<T> V;
+  const int64_t total = npix * ngroups;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int grp = (int)(i % ngroups);
+    const int64_t p = i / ngroups;
+    const int x = (int)(p % a.w);
+    const int64_t t = p / a.w;
+    const int y = (int)(t % a.h), n = (int)(t / a.h);
+    const int c0 = a.c_begin + 8 * grp;
+    const int64_t oi = p * a.c + c0;
+    float v[8];
+    if (a.residual) {
+      const V r = *(const V*)((const T*)a.residual + oi);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = to_f32(r.v[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+    for (int b = 0; b < a.nbranch; ++b) {
+      const int lo = a.br_c_off[b], hi = lo + a.br_c[b];
+      if (hi <= c0 || lo >= c0 + 8) continue;
+      const T* z = (const T*)a.br_z[b] + (int64_t)n * a.br_h[b] * a.br_w[b] * a.br_cs[b];
+      const float* att = a.br_att[b] ? a.br_att[b] + (int64_t)n * a.br_c[b] : nullptr;
+      const float coeff = a.br_coeff[b];
+      const bool same = a.br_h[b] == a.h && a.br_w[b] == a.w;
+      int x0, x1, y0, y1;
+      float lx, ly;
+      src_index(x, a.br_w[b], a.w, (float)a.br_w[b] / (float)a.w, x0, x1, lx);
+      src_index(y, a.br_h[b], a.h, (float)a.br_h[b] / (float)a.h, y0, y1, ly);
+      const int cs = a.br_cs[b], bw = a.br_w[b];
+      const T* r0 = z + (int64_t)y0 * bw * cs;
+      const T* r1 = z + (int64_t)y1 * bw * cs;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = c0 + e;
+        if (c < lo || c >= hi) continue;
+        const int cb = c - lo;
+        float s;
+        if (same) {
+          s = to_f32(r0[(int64_t)x * cs + cb]);
+        } else {
+          const float v00 = to_f32(r0[(int64_t)x0 * cs + cb]), v01 = to_f32(r0[(int64_t)x1 * cs + cb]);
+          const float v10 = to_f32(r1[(int64_t)x0 * cs + cb]), v11 = to_f32(r1[(int64_t)x1 * cs + cb]);
+          s = (1.f - ly) * ((1.f - lx) * v00 + lx * v01) + ly * ((1.f - lx) * v10 + lx * v11);
+        }
+        if (att) s *= att[cb];
+        v[e] += coeff * s;
+      }
+    }
+    V o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o.v[e] = from_f32<T>(a.gate ? v[e] * a.gate[c0 + e] : v[e]);
+    *(V*)((T*)a.out + oi) = o;
+  }
+}
+
 // ---- NCHW -> NHWC with a padded channel stride (pad channels written 0) ----------------
 // 64 x 64 (pixel x channel) tiles transposed through LDS: reads coalesced along
 // pixels, writes coalesced along channels.
@@ -1119,6 +1184,18 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
       case KAD_F32: hipLaunchKernelGGL(merge_nchw_kernel<float>, grid, dim3(256), 0, st, *a); break;
       case KAD_F16: hipLaunchKernelGGL(merge_nchw_kernel<half_t>, grid, dim3(256), 0, st, *a); break;
       case KAD_BF16: hipLaunchKernelGGL(merge_nchw_kernel<bf16_t>, grid, dim3(256), 0, st, *a); break;
+      default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
+    }
+  } else if (a->c % 8 == 0 && a->c_begin % 8 == 0 && a->c_end % 8 == 0 && ((uintptr_t)a->out % 16) == 0 &&
+             ((uintptr_t)a->residual % 16) == 0) {
+    const int64_t npix = (int64_t)a->n * a->h * a->w;
+    const int ngroups = (a->c_end - a->c_begin) / 8;
+    const int64_t total = npix * ngroups;
+    const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+    switch (a->dtype) {
+      case KAD_F32: hipLaunchKernelGGL(merge_nhwc_vec_kernel<float>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;
+      case KAD_F16: hipLaunchKernelGGL(merge_nhwc_vec_kernel<half_t>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;
+      case KAD_BF16: hipLaunchKernelGGL(merge_nhwc_vec_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;
       default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
     }
   } else {

@@ -576,7 +576,8 @@ def branch_merge(out, layout, branches, residual=None, gate=None, channels=None)
         att = b.get('att')
         a.br_att[i] = att.data_ptr() if att is not None else None
         a.br_c[i], a.br_c_off[i] = b['c'], b['c_off']
-        a.br_h[i], a.br_w[i], a.br_cs[i] = z.shape[1], z.shape[2], z.shape[3]
+        _, zh, zw, zcs = _nhwc_cs(z)   # z may be a channel slice (e.g. the output's own window)
+        a.br_h[i], a.br_w[i], a.br_cs[i] = zh, zw, zcs
         a.br_coeff[i] = float(b.get('coeff', 1.0))
     _check(load().kad_branch_merge(ctypes.byref(a), _stream()), 'kad_branch_merge')
     return out

@@ -253,7 +253,7 @@ class KADConvPlan:
             pyr.append({'wpack': br.proj_packed(dtype), 'bias': br.proj_b, 'cout': br.c, 'out': y,
                         'rowpart': rows, 'colpart': cols})
         st.append(('pyramid', lambda: _ext.pyramid_proj(xin, in_layout, C, pyr)))
-        chains = []
+        chains, merges = [], []
         for i, br in enumerate(self.branches):
             h, w = H >> i, W >> i
             P = h * w
@@ -275,7 +275,10 @@ class KADConvPlan:
             ch = br.dsc.stages(ys[i], N, h, w, z, z_layout, post_mul=br.bn_a, post_add=br.bn_b,
                                post_scale=br.scale, relu=True, gap=gap, tag=str(i), sums=sums[i], se=se,
                                mask_split=False)
-            if full:
+            if out_layout == _ext.KAD_NHWC:
+                # channels-last: one merge of every branch after the join (below)
+                merges.append({'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att})
+            elif full:
                 ch.append((f'merge{i}', lambda br=br, att=att: _ext.scale_residual(
                     out_v, att, xin, br.c_off, br.c, out_layout)))
             else:
@@ -284,7 +287,12 @@ class KADConvPlan:
                 ch.append((f'merge{i}', lambda mb=mb, br=br: _ext.branch_merge(
                     out_v, out_layout, mb, residual=xin, channels=(br.c_off, br.c_off + br.c))))
             chains.append(ch)
-        return st, chains, [], out
+        post = []
+        if merges:
+            # NHWC: all branches in one launch, a thread per pixel and 8-channel piece (the full-
+            # resolution branch is read from its own window of the output, in place)
+            post.append(('merge', lambda: _ext.branch_merge(out_v, out_layout, merges, residual=xin)))
+        return st, chains, post, out
 
     def _se_counters(self, dev, i, n):
         """Per-image arrival counters of branch i's fused SE (zero between calls), kept per device.

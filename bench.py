@@ -298,7 +298,7 @@ def traffic_probe():
         st, _ = m._kad_plan.stages(x)
         for _, fn in st:
             fn()
-        dsc0 = dict(st)['dsc0']
+        dsc0 = dict(st).get('dsc') or dict(st)['dsc0']
         a = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device='cuda')
         b = torch.empty_like(a)
         torch.cuda.synchronize()
@@ -352,7 +352,8 @@ def traffic_from(fetch_csv, write_csv):
                 continue
             name = r['Kernel_Name']
             grid = int(r.get('Grid_Size') or r.get('Grid_Size_X') or 0)
-            kind = 'dsc0' if 'dcn_fwd_kernel' in name else 'copy' if 'copy' in name.lower() else None
+            kind = 'dsc0' if ('dcn_fwd_kernel' in name or 'dcn_group_kernel' in name) else \
+                'copy' if 'copy' in name.lower() else None
             if kind:
                 rows[kind].append((grid, float(r['Counter_Value'])))
         out = {}
@@ -524,10 +525,17 @@ def main():
         for _, fn in stages:
             fn()
         stage_us = {name: round(time_eager(fn, 20), 2) for name, fn in stages}
-        dsc0 = dict(stages)['dsc0']
-        c0 = plan.branches[0].c
+        sd = dict(stages)
+        if 'dsc' in sd:  # grouped: one launch runs every branch's DSC (+ SE)
+            dsc0 = sd['dsc']
+            flops = sum(dsc_flops(shape[0], shape[2] >> i, shape[3] >> i, br.c) for i, br in enumerate(plan.branches))
+            kname = ('dcn_group_kernel<half,half,6,FUSED> (the three branches\' DSCs in one launch: conv_offset + '
+                     'DCN + fused SE, c=86/85/85 at 100^2/50^2/25^2, batch 8)')
+        else:
+            dsc0 = sd['dsc0']
+            flops = dsc_flops(shape[0], shape[2], shape[3], plan.branches[0].c)
+            kname = 'dcn_fwd_kernel<half,half,6,FUSED> (branch-0 DSC: conv_offset + DCN, c=86, 8x100x100)'
         dcn_us = time_eager(dsc0, args.steps, args.warmup)
-        flops = dsc_flops(shape[0], shape[2], shape[3], c0)
         achieved = flops / (dcn_us * 1e-6)
 
     traffic = None
@@ -555,8 +563,7 @@ def main():
                      'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_MFMA_F16, 4), 'traffic': traffic,
                      'traffic_source': 'profiles/dsc0_traffic.json (FETCH_SIZE / WRITE_SIZE of bench.py '
                                        '--traffic-probe, scaled by a 64 MiB copy); not measured in this run',
-                     'kernel': 'dcn_fwd_kernel<half,half,6,FUSED> (branch-0 DSC: conv_offset + DCN, c=86, '
-                               '8x100x100)', 'kernel_us': round(dcn_us, 3),
+                     'kernel': kname, 'kernel_us': round(dcn_us, 3),
                      'flops_per_launch': flops},
         'forward_roofline': {'floor_us': FORWARD_FLOOR_US, 'frac': round(FORWARD_FLOOR_US / us, 4)},
         'stages_us': stage_us,

@@ -139,6 +139,15 @@ int kad_conv3x3_fwd(const kad_dcn_args *a, void *stream);
  * (kadc_dcn16.cpp:247-289).  stride <= 2 (also for kad_conv3x3_fwd). */
 int kad_dsc_fwd(const kad_dcn_args *a, void *stream);
 
+/* Up to KAD_DCN_GROUP_MAX independent kad_dsc_fwd problems in one launch (the
+ * three branches of a KAD-Conv layer): a[0..count) as for kad_dsc_fwd, all with
+ * the same dtype and the same ceil(Cout / 16) (capped at 8).  Each problem's
+ * results are those of kad_dsc_fwd on it; problems must not share outputs or SE
+ * counters.  No reference counterpart (scheduling: one launch instead of three
+ * concurrent streams, whose overlap a HIP graph does not guarantee). */
+#define KAD_DCN_GROUP_MAX 4
+int kad_dsc_fwd_group(const kad_dcn_args *a, int count, void *stream);
+
 /* kad_dsc_fwd that allocates nothing and needs no caller-owned scratch.  No
  * counterpart in the reference: it is for callers that cannot allocate device
  * memory (code under HIP graph capture that must not call hipMalloc, tight
@@ -283,6 +292,27 @@ int64_t kad_lcsa_mask_work_elems(int n, int h, int w, int ksplit);
 int kad_lcsa_mask_split(const float *arow, const float *colm, const float *params, const void *emat,
                         const float *ebias, float *mask, int n, int c, int h, int w, int emat_dtype, int ksplit,
                         float *work, void *stream);
+
+/* The LCSA stages of several problems (the branches of a KAD-Conv layer) as
+ * one launch each: kad_lcsa_prep_group computes every problem's means from its
+ * partial sums (kad_lcsa_prep), kad_lcsa_mask_group every problem's mask
+ * (kad_lcsa_mask, unsplit), all with one emat dtype.  No reference counterpart
+ * (scheduling: one launch instead of three concurrent streams). */
+#define KAD_LCSA_GROUP_MAX 4
+typedef struct kad_lcsa_args {
+  const float *rows;    /* [N][nrp][H][C] partial row sums */
+  const float *cols;    /* [N][ncp][W][C] partial column sums */
+  int nrp, ncp;
+  float *arow;          /* [N][H][C] row means (prep output, mask input) */
+  float *colm;          /* [N][W][C] column means */
+  const float *params;  /* kad_lcsa_params_elems(C) fp32 block */
+  const void *emat;     /* kad_lcsa_pack output */
+  const float *ebias;   /* [16] */
+  float *mask;          /* [N][H][W][9] */
+  int n, c, h, w;
+} kad_lcsa_args;
+int kad_lcsa_prep_group(const kad_lcsa_args *a, int count, void *stream);
+int kad_lcsa_mask_group(const kad_lcsa_args *a, int count, int emat_dtype, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* Squeeze-excitation                                                        */

@@ -682,8 +682,11 @@ __device__ __forceinline__ void se_tail(const float* __restrict__ partial, const
 }
 
 // ---- kernel ------------------------------------------------------------------------------------
+// The block's work: tile-order index bx (XCD-aware, see below) and column block by of ny, of the
+// problem (a, g).  dcn_fwd_kernel runs one problem per launch, dcn_group_kernel several.
 template <typename T, typename OutT, int NBF, int MODE>
-__global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a, DcnGeom g) {
+__device__ __forceinline__ void dcn_block(const kad_dcn_args& a, const DcnGeom& g, const int bx, const int by,
+                                          const int ny) {
   typedef DcnFrag<T> Ops;
   typedef typename Ops::frag frag;
   typedef typename InfoOf<T>::type Info;
@@ -702,11 +705,10 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
   // XCD-aware tile order over (image, tile) flattened: block b runs on XCD b % 8, which takes a
   // contiguous run of it (8 images: one image per XCD), so neighbouring tiles share their halos
   // through one L2; the column blocks of a tile (blockIdx.y) land on the same XCD.
-  const int bx = blockIdx.x;
   const int q = (bx & 7) * (g.grid_x >> 3) + (bx >> 3);
   if (q >= a.n * g.tiles) return;  // whole block, before any barrier
   const int n = q / g.tiles, tile = q - n * g.tiles;
-  const int co0 = blockIdx.y * NB;
+  const int co0 = by * NB;
   const int tyi = tile / g.tiles_x;
   const int ty0 = tyi * g.th, tx0 = (tile - tyi * g.tiles_x) * g.tw;
   const int P = g.ho * g.wo;
@@ -1200,7 +1202,7 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       // not for the acknowledgements of the output stores, which no one here reads.
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (tid == 0) {
-        const unsigned total = (unsigned)g.tiles * gridDim.y;
+        const unsigned total = (unsigned)g.tiles * ny;
         const unsigned prev = __hip_atomic_fetch_add(a.se_count + n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int last = prev + 1u == total;
         if (last) {
@@ -1216,6 +1218,37 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a,
       }
     }
   }
+}
+
+template <typename T, typename OutT, int NBF, int MODE>
+__global__ __launch_bounds__(DCN_THREADS, 1) void dcn_fwd_kernel(kad_dcn_args a, DcnGeom g) {
+  dcn_block<T, OutT, NBF, MODE>(a, g, blockIdx.x, blockIdx.y, gridDim.y);
+}
+
+// Several independent problems of one instantiation (same dtype, mode and column-fragment count)
+// in one grid: problem p owns blocks [start[p], start[p + 1]) (its grid_x x ny blocks, start a
+// multiple of 8 so a block's XCD, id % 8, is its tile order's).  The three branches of a KAD-Conv
+// layer run their DSCs this way, as one launch instead of three concurrent streams.
+struct DcnGroup {
+  kad_dcn_args a[KAD_DCN_GROUP_MAX];
+  DcnGeom g[KAD_DCN_GROUP_MAX];
+  int start[KAD_DCN_GROUP_MAX + 1];
+  int ny[KAD_DCN_GROUP_MAX];
+  int count;
+};
+
+template <typename T, typename OutT, int NBF, int MODE>
+__global__ __launch_bounds__(DCN_THREADS, 1) void dcn_group_kernel(DcnGroup grp) {
+  const int id = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < KAD_DCN_GROUP_MAX; ++i)
+    if (i < grp.count && id >= grp.start[i]) p = i;
+  if (id >= grp.start[p + 1]) return;
+  const int local = id - grp.start[p];
+  const int gx = grp.g[p].grid_x;
+  // p is uniform over the block: the problem's fields are scalar loads from kernel-argument memory
+  dcn_block<T, OutT, NBF, MODE>(grp.a[p], grp.g[p], local % gx, local / gx, grp.ny[p]);
 }
 
 // ---- weight packing ------------------------------------------------------------------------------
@@ -1392,6 +1425,60 @@ extern "C" int kad_dsc_fwd(const kad_dcn_args* a, void* stream) {
     case KAD_F16: return dispatch_dcn<half_t, half_t, MODE_FUSED>(*a, st, g);
     case KAD_BF16: return dispatch_dcn<bf16_t, bf16_t, MODE_FUSED>(*a, st, g);
     default: return fail(KAD_EINVAL, "kad_dsc_fwd: unknown dtype %d", a->dtype);
+  }
+}
+
+namespace kad {
+template <typename T, typename OutT, int NBF>
+static int launch_group(const DcnGroup& grp, hipStream_t st) {
+  hipLaunchKernelGGL((dcn_group_kernel<T, OutT, NBF, MODE_FUSED>), dim3(grp.start[grp.count]), dim3(DCN_THREADS), 0,
+                     st, grp);
+  return check_launch("kad_dsc_fwd_group");
+}
+
+template <typename T, typename OutT>
+static int dispatch_group(const DcnGroup& grp, int nbf, hipStream_t st) {
+  switch (nbf) {
+    case 1: return launch_group<T, OutT, 1>(grp, st);
+    case 2: return launch_group<T, OutT, 2>(grp, st);
+    case 3: return launch_group<T, OutT, 3>(grp, st);
+    case 4: return launch_group<T, OutT, 4>(grp, st);
+    case 5: return launch_group<T, OutT, 5>(grp, st);
+    case 6: return launch_group<T, OutT, 6>(grp, st);
+    case 7: return launch_group<T, OutT, 7>(grp, st);
+    default: return launch_group<T, OutT, 8>(grp, st);
+  }
+}
+}  // namespace kad
+
+extern "C" int kad_dsc_fwd_group(const kad_dcn_args* a, int count, void* stream) {
+  KAD_CHECK_ARG(a && count >= 1 && count <= KAD_DCN_GROUP_MAX, "kad_dsc_fwd_group: count %d outside [1, %d]", count,
+                KAD_DCN_GROUP_MAX);
+  DcnGroup grp;
+  grp.count = count;
+  int nbf = 0;
+  int64_t blocks = 0;
+  for (int p = 0; p < count; ++p) {
+    int rc = validate_dcn(&a[p], MODE_FUSED, &grp.g[p]);
+    if (rc) return fail(rc, "kad_dsc_fwd_group: problem %d: %s", p, kad_last_error());
+    const int nb = ceil_div(a[p].cout, 16) < 8 ? ceil_div(a[p].cout, 16) : 8;
+    KAD_CHECK_ARG(a[p].dtype == a[0].dtype && (p == 0 || nb == nbf),
+                  "kad_dsc_fwd_group: problem %d differs in dtype or ceil(Cout / 16) from problem 0", p);
+    nbf = nb;
+    grp.a[p] = a[p];
+    grp.ny[p] = ceil_div(a[p].cout, nb * 16);
+    grp.start[p] = (int)blocks;
+    blocks += (int64_t)grp.g[p].grid_x * grp.ny[p];  // grid_x is a multiple of 8
+  }
+  KAD_CHECK_ARG(blocks < (1ll << 31), "kad_dsc_fwd_group: too many blocks");
+  grp.start[count] = (int)blocks;
+  for (int p = count + 1; p <= KAD_DCN_GROUP_MAX; ++p) grp.start[p] = (int)blocks;
+  hipStream_t st = (hipStream_t)stream;
+  switch (a[0].dtype) {
+    case KAD_F32: return dispatch_group<float, float>(grp, nbf, st);
+    case KAD_F16: return dispatch_group<half_t, half_t>(grp, nbf, st);
+    case KAD_BF16: return dispatch_group<bf16_t, bf16_t>(grp, nbf, st);
+    default: return fail(KAD_EINVAL, "kad_dsc_fwd_group: unknown dtype %d", a[0].dtype);
   }
 }
 

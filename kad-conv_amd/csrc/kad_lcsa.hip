@@ -138,9 +138,8 @@ __global__ void lcsa_pack_kernel(const float* params, ET* emat, float* ebias, in
 
 // ---- axial means from partial slices -----------------------------------------------------------
 // grid (H + W, N): block l < H reduces row l's slices, else column l - H's.
-__global__ __launch_bounds__(256) void lcsa_prep_kernel(const float* rows, int nrp, const float* cols, int ncp,
-                                                       float* arow, float* colm, int c, int h, int w) {
-  const int n = blockIdx.y, l = blockIdx.x;
+__device__ __forceinline__ void lcsa_prep_row(const float* rows, int nrp, const float* cols, int ncp, float* arow,
+                                              float* colm, int c, int h, int w, int n, int l) {
   if (l < h) {
     const float inv = 1.f / (float)w;
     for (int ch = threadIdx.x; ch < c; ch += 256) {
@@ -159,6 +158,11 @@ __global__ __launch_bounds__(256) void lcsa_prep_kernel(const float* rows, int n
       colm[((int64_t)n * w + x) * c + ch] = s * inv;
     }
   }
+}
+
+__global__ __launch_bounds__(256) void lcsa_prep_kernel(const float* rows, int nrp, const float* cols, int ncp,
+                                                       float* arow, float* colm, int c, int h, int w) {
+  lcsa_prep_row(rows, nrp, cols, ncp, arow, colm, c, h, w, blockIdx.y, blockIdx.x);
 }
 
 // ---- mask GEMM ------------------------------------------------------------------------------------
@@ -207,10 +211,10 @@ constexpr int LM_SCS = LM_SC + 4;                       // fp32 row stride of th
 // requested first, u = relu(alpha a + beta) is written to LDS meanwhile, then
 // 11 x 4 MFMAs.
 template <typename ET>
-__global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* arow, const float* colm,
-                                                                 const float* params, const ET* emat,
-                                                                 const float* ebias, float* mask, int c, int h,
-                                                                 int w, int cp, int ksplit, float* part) {
+__device__ __forceinline__ void lcsa_mask_block(const float* arow, const float* colm, const float* params,
+                                                const ET* emat, const float* ebias, float* mask, int c, int h, int w,
+                                                int cp, int ksplit, float* part, const int bx, const int by,
+                                                const int bz, const int nz) {
   constexpr int LDU = LmCfg<ET>::ldu;
   __shared__ __align__(16) ET us[LM_UR * LM_TW * LDU];
   __shared__ __align__(16) float s_col[LM_UR][LM_SCS];   // column means, columns w0 - 5 .. w0 + 20
@@ -223,8 +227,8 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
   const float* bna = params + 12 * c;
   const float* bnb = params + 13 * c;
   // grid.z = N x ksplit: split sp takes the chunks [kc0, kc1) of the channel contraction
-  const int n = blockIdx.z / ksplit, sp = blockIdx.z - n * ksplit;
-  const int h0 = blockIdx.y * LM_TH, w0 = blockIdx.x * LM_TW;
+  const int n = bz / ksplit, sp = bz - n * ksplit;
+  const int h0 = by * LM_TH, w0 = bx * LM_TW;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, grp = lane >> 4;
   const float* colm_n = colm + (int64_t)n * w * c;
@@ -414,9 +418,48 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* a
       if (ksplit == 1)
         mask[(((int64_t)n * h + gy) * w + gx) * 9 + j] = mask_sigmoid(acc[f][i] + eb[i]);
       else  // raw logits of this split; lcsa_mask_reduce_kernel adds the splits up
-        part[((((int64_t)sp * gridDim.z / ksplit + n) * h + gy) * w + gx) * 9 + j] = acc[f][i];
+        part[((((int64_t)sp * nz / ksplit + n) * h + gy) * w + gx) * 9 + j] = acc[f][i];
     }
   }
+}
+
+template <typename ET>
+__global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_kernel(const float* arow, const float* colm,
+                                                                 const float* params, const ET* emat,
+                                                                 const float* ebias, float* mask, int c, int h,
+                                                                 int w, int cp, int ksplit, float* part) {
+  lcsa_mask_block<ET>(arow, colm, params, emat, ebias, mask, c, h, w, cp, ksplit, part, blockIdx.x, blockIdx.y,
+                      blockIdx.z, gridDim.z);
+}
+
+// Several LCSA problems (the branches of a KAD-Conv layer) in one launch: problem p owns blocks
+// [start[p], start[p + 1]) = its ceil(W/16) x ceil(H/16) x N tiles, unsplit.
+struct LcsaGroup {
+  kad_lcsa_args a[KAD_LCSA_GROUP_MAX];
+  int start[KAD_LCSA_GROUP_MAX + 1];
+  int count;
+};
+
+template <typename ET>
+__global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_group_kernel(LcsaGroup grp) {
+  const int id = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < KAD_LCSA_GROUP_MAX; ++i)
+    if (i < grp.count && id >= grp.start[i]) p = i;
+  const kad_lcsa_args& a = grp.a[p];
+  const int local = id - grp.start[p];
+  const int tx = ceil_div(a.w, LM_TW), ty = ceil_div(a.h, LM_TH);
+  lcsa_mask_block<ET>(a.arow, a.colm, a.params, (const ET*)a.emat, a.ebias, a.mask, a.c, a.h, a.w,
+                      round_up(a.c, 32), 1, nullptr, local % tx, (local / tx) % ty, local / (tx * ty), a.n);
+}
+
+// The axial means of several problems in one launch: grid (max H + W, max N, count).
+__global__ __launch_bounds__(256) void lcsa_prep_group_kernel(LcsaGroup grp) {
+  const kad_lcsa_args& a = grp.a[blockIdx.z];
+  const int n = blockIdx.y, l = blockIdx.x;
+  if (n >= a.n || l >= a.h + a.w) return;
+  lcsa_prep_row(a.rows, a.nrp, a.cols, a.ncp, a.arow, a.colm, a.c, a.h, a.w, n, l);
 }
 
 // mask = sigmoid(sum over the splits, in split order, + ebias): one thread per (pixel, logit).
@@ -527,6 +570,60 @@ extern "C" int kad_lcsa_mask(const float* arow, const float* colm, const float* 
   KAD_CHECK_ARG(((uintptr_t)emat) % 16 == 0, "kad_lcsa_mask: emat must be 16-byte aligned");
   return kad::launch_lcsa_mask(arow, colm, params, emat, ebias, mask, n, c, h, w, emat_dtype, 1, nullptr,
                                (hipStream_t)stream);
+}
+
+static int validate_lcsa_group(const kad_lcsa_args* a, int count, const char* what) {
+  KAD_CHECK_ARG(a && count >= 1 && count <= KAD_LCSA_GROUP_MAX, "%s: count %d outside [1, %d]", what, count,
+                KAD_LCSA_GROUP_MAX);
+  for (int p = 0; p < count; ++p) {
+    const kad_lcsa_args& b = a[p];
+    KAD_CHECK_ARG(b.rows && b.cols && b.arow && b.colm && b.params && b.emat && b.ebias && b.mask,
+                  "%s: problem %d: null pointer", what, p);
+    KAD_CHECK_ARG(b.n > 0 && b.c > 0 && b.h > 0 && b.w > 0 && b.nrp > 0 && b.ncp > 0, "%s: problem %d: bad shape",
+                  what, p);
+    KAD_CHECK_ARG((int64_t)(b.h > b.w ? b.h : b.w) * b.c < (1ll << 31), "%s: problem %d: H or W times C too large",
+                  what, p);
+    KAD_CHECK_ARG(((uintptr_t)b.emat) % 16 == 0, "%s: problem %d: emat must be 16-byte aligned", what, p);
+  }
+  return KAD_OK;
+}
+
+extern "C" int kad_lcsa_prep_group(const kad_lcsa_args* a, int count, void* stream) {
+  int rc = validate_lcsa_group(a, count, "kad_lcsa_prep_group");
+  if (rc) return rc;
+  kad::LcsaGroup grp;
+  grp.count = count;
+  int maxl = 0, maxn = 0;
+  for (int p = 0; p < count; ++p) {
+    grp.a[p] = a[p];
+    maxl = a[p].h + a[p].w > maxl ? a[p].h + a[p].w : maxl;
+    maxn = a[p].n > maxn ? a[p].n : maxn;
+  }
+  hipLaunchKernelGGL(kad::lcsa_prep_group_kernel, dim3(maxl, maxn, count), dim3(256), 0, (hipStream_t)stream, grp);
+  return check_launch("kad_lcsa_prep_group");
+}
+
+extern "C" int kad_lcsa_mask_group(const kad_lcsa_args* a, int count, int emat_dtype, void* stream) {
+  int rc = validate_lcsa_group(a, count, "kad_lcsa_mask_group");
+  if (rc) return rc;
+  kad::LcsaGroup grp;
+  grp.count = count;
+  int64_t blocks = 0;
+  for (int p = 0; p < count; ++p) {
+    grp.a[p] = a[p];
+    grp.start[p] = (int)blocks;
+    blocks += (int64_t)ceil_div(a[p].w, kad::LM_TW) * ceil_div(a[p].h, kad::LM_TH) * a[p].n;
+  }
+  KAD_CHECK_ARG(blocks < (1ll << 31), "kad_lcsa_mask_group: too many blocks");
+  for (int p = count; p <= KAD_LCSA_GROUP_MAX; ++p) grp.start[p] = (int)blocks;
+  hipStream_t st = (hipStream_t)stream;
+  if (emat_dtype == KAD_F32)
+    hipLaunchKernelGGL(kad::lcsa_mask_group_kernel<float>, dim3((unsigned)blocks), dim3(kad::LM_THREADS), 0, st, grp);
+  else if (emat_dtype == KAD_F16)
+    hipLaunchKernelGGL(kad::lcsa_mask_group_kernel<half_t>, dim3((unsigned)blocks), dim3(kad::LM_THREADS), 0, st, grp);
+  else
+    return fail(KAD_EINVAL, "kad_lcsa_mask_group: emat dtype must be KAD_F32 or KAD_F16");
+  return check_launch("kad_lcsa_mask_group");
 }
 
 extern "C" int kad_lcsa_mask_splits(int n, int c, int h, int w) {

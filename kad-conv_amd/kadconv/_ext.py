@@ -45,6 +45,12 @@ class DcnArgs(ctypes.Structure):
     ]
 
 
+class LcsaArgs(ctypes.Structure):
+    _fields_ = [('rows', c_vp), ('cols', c_vp), ('nrp', c_int), ('ncp', c_int), ('arow', c_vp), ('colm', c_vp),
+                ('params', c_vp), ('emat', c_vp), ('ebias', c_vp), ('mask', c_vp),
+                ('n', c_int), ('c', c_int), ('h', c_int), ('w', c_int)]
+
+
 class GemmArgs(ctypes.Structure):
     _fields_ = [
         ('x', c_vp), ('wpack', c_vp), ('bias', c_vp), ('out', c_vp),
@@ -105,6 +111,9 @@ SIGNATURES = {
     'kad_conv3x3_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_dsc_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_dsc_fwd_noalloc': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
+    'kad_dsc_fwd_group': (c_int, [ctypes.POINTER(DcnArgs), c_int, c_vp]),
+    'kad_lcsa_prep_group': (c_int, [ctypes.POINTER(LcsaArgs), c_int, c_vp]),
+    'kad_lcsa_mask_group': (c_int, [ctypes.POINTER(LcsaArgs), c_int, c_int, c_vp]),
     'kad_scale_residual': (c_int, [c_vp, c_vp, c_vp] + [c_int] * 8 + [c_vp]),
     'kad_gemm_wpack_elems': (c_i64, [c_int, c_int]),
     'kad_gemm_pack_weights': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
@@ -283,13 +292,10 @@ def dcn_fwd(x_nhwc, cin, offset, offset_strides, mask, mask_strides, wpack, cout
     return out
 
 
-def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, out, *, stride=1, pad=1,
-            bias=None, post_mul=None, post_add=None, post_scale=None, relu=False, out_layout=KAD_NHWC,
-            gap_partial=None, se=None, noalloc=False):
-    """conv_offset + deformable conv in one launch (offsets never leave the chip); with `se`,
-    also the squeeze-excitation MLP of the output (see _set_se).  noalloc=True calls
-    kad_dsc_fwd_noalloc: `se` is then (w1, b1, w2, b2, att) and the GAP partials and arrival
-    counters come from the library's own device scratch (gap_partial must be None)."""
+def dsc_args(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, out, *, stride=1, pad=1,
+             bias=None, post_mul=None, post_add=None, post_scale=None, relu=False, out_layout=KAD_NHWC,
+             gap_partial=None, se=None, noalloc=False):
+    """kad_dcn_args of one fused DSC problem (checked), for kad_dsc_fwd / _noalloc / _group."""
     _need_gpu(x_nhwc, off_wpack, wpack, out)
     if noalloc and gap_partial is not None:
         raise ValueError('kad_dsc_fwd_noalloc keeps the GAP partials in its own scratch: pass gap_partial=None')
@@ -316,11 +322,48 @@ def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, o
     if noalloc:
         if se is not None:
             _set_se_weights(a, se, N, cout, ho, wo)
+    else:
+        _set_se(a, se, gap_partial, N, cout, ho, wo)
+    return a
+
+
+def dsc_fwd(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, out, *, noalloc=False, **kw):
+    """conv_offset + deformable conv in one launch (offsets never leave the chip); with `se`,
+    also the squeeze-excitation MLP of the output (see _set_se).  noalloc=True calls
+    kad_dsc_fwd_noalloc: `se` is then (w1, b1, w2, b2, att) and the GAP partials and arrival
+    counters come from the library's own device scratch (gap_partial must be None)."""
+    a = dsc_args(x_nhwc, cin, off_wpack, off_bias, mask, mask_strides, wpack, cout, out, noalloc=noalloc, **kw)
+    if noalloc:
         _check(load().kad_dsc_fwd_noalloc(ctypes.byref(a), _stream()), 'kad_dsc_fwd_noalloc')
-        return out
-    _set_se(a, se, gap_partial, N, cout, ho, wo)
-    _check(load().kad_dsc_fwd(ctypes.byref(a), _stream()), 'kad_dsc_fwd')
+    else:
+        _check(load().kad_dsc_fwd(ctypes.byref(a), _stream()), 'kad_dsc_fwd')
     return out
+
+
+def dsc_fwd_group(args):
+    """Several fused DSC problems (kad_dcn_args from dsc_args) in one launch."""
+    arr = (DcnArgs * len(args))(*args)
+    _check(load().kad_dsc_fwd_group(arr, len(args), _stream()), 'kad_dsc_fwd_group')
+
+
+def lcsa_args(rows, nrp, cols, ncp, arow, colm, params, emat, ebias, mask, n, c, h, w):
+    _need_gpu(rows, cols, arow, colm, params, emat, ebias, mask)
+    a = LcsaArgs()
+    a.rows, a.cols, a.nrp, a.ncp = _ptr(rows), _ptr(cols), nrp, ncp
+    a.arow, a.colm, a.params, a.emat, a.ebias, a.mask = _ptr(arow), _ptr(colm), _ptr(params), _ptr(emat), \
+        _ptr(ebias), _ptr(mask)
+    a.n, a.c, a.h, a.w = n, c, h, w
+    return a
+
+
+def lcsa_prep_group(args):
+    arr = (LcsaArgs * len(args))(*args)
+    _check(load().kad_lcsa_prep_group(arr, len(args), _stream()), 'kad_lcsa_prep_group')
+
+
+def lcsa_mask_group(args, emat_dtype):
+    arr = (LcsaArgs * len(args))(*args)
+    _check(load().kad_lcsa_mask_group(arr, len(args), kad_dtype(emat_dtype), _stream()), 'kad_lcsa_mask_group')
 
 
 def conv3x3_fwd(x_nhwc, cin, wpack, cout, out, *, stride=1, pad=1, bias=None, out_layout=KAD_NHWC):

@@ -31,6 +31,8 @@ from . import _ext
 
 DCN_BLOCK_COLS = 128  # output channels per block of the DCN kernels (8 MFMA column fragments)
 SPLIT_MIN_TILES = 128  # tiles per launch from which a separate offset conv pays (half the CUs)
+GROUPED = True         # KADConvPlan: branch stages as grouped launches on one stream for small layers
+GROUP_MAX_WORK = 2048  # ... whose full-resolution DSC has less work: N x tiles x column fragments
 
 
 def _f32(t):
@@ -205,6 +207,22 @@ class KADConvPlan:
             raise ValueError('branch widths do not add up to the layer width')
         if self.n > 3:
             raise NotImplementedError('the fused forward covers n <= 3 branches (the paper uses 3)')
+        # grouped: the branches' LCSA and DSC stages run as one launch each (all branches), on the
+        # caller's stream; else each branch chain runs on a side stream of its own (see _grouped)
+        self.groupable = GROUPED and all(br.dsc.use_mask for br in self.branches)
+
+    def _grouped(self, x):
+        """Grouped launches unless the full-resolution DSC is heavy: N x tiles x 16-channel
+        column fragments >= GROUP_MAX_WORK.  Small layers are bound by launch and queue
+        latency, and under HIP-graph replay the three side-stream chains of a small layer
+        were measured to run one after another (KAD-CNet-S: 9.62 -> 9.14 ms per batch with
+        every KADC4 grouped).  A heavy layer keeps the side streams: the coarse branches'
+        DSCs and merges then fill the last, partly empty round of the full-resolution DSC
+        (KADConv(256) at [8, 256, 100, 100], 640 tiles x 6 fragments: 210 us with streams,
+        227 us grouped)."""
+        frags = min((self.branches[0].c + 15) // 16, 8)
+        work = x.shape[0] * _ext.dcn_tiles(x.shape[2], x.shape[3]) * frags
+        return self.groupable and work < GROUP_MAX_WORK
 
     def eligible(self, x):
         if not (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float16, torch.bfloat16)):
@@ -220,8 +238,82 @@ class KADConvPlan:
 
     def stages(self, x):
         """The fused forward as (name, launch) pairs in stream order; returns (stages, out)."""
+        if self._grouped(x):
+            return self.schedule_grouped(x)
         pre, branches, post, out = self.schedule(x)
         return pre + [s for b in branches for s in b] + post, out
+
+    def _io(self, x):
+        """(x view for the kernels, its layout, out, out view, out layout)."""
+        nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
+        if nhwc:
+            out = torch.empty_like(x, memory_format=torch.channels_last)
+            return x.permute(0, 2, 3, 1), _ext.KAD_NHWC, out, out.permute(0, 2, 3, 1), _ext.KAD_NHWC
+        x = x.contiguous()
+        out = torch.empty_like(x)
+        return x, _ext.KAD_NCHW, out, out, _ext.KAD_NCHW
+
+    def schedule_grouped(self, x):
+        """The forward as one chain of launches on one stream: the pyramid, then the LCSA
+        means, the LCSA masks and the fused DSCs (+ SE) of all branches as one launch each
+        (kad_lcsa_prep_group, kad_lcsa_mask_group, kad_dsc_fwd_group), then the merges.
+        Returns (stages, out)."""
+        N, C, H, W = x.shape
+        dev, dtype = x.device, x.dtype
+        xin, in_layout, out, out_v, out_layout = self._io(x)
+        ntx, nty = _ext.pyramid_tiles(H, W)
+        pyr, lcsa, dcn, keep, merges = [], [], {}, [], []
+        edt = torch.float32 if dtype == torch.float32 else torch.float16
+        st = []
+        for i, br in enumerate(self.branches):
+            h, w = H >> i, W >> i
+            P = h * w
+            full = (h, w) == (H, W)
+            y = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
+            rows = torch.empty(N, ntx, h, br.c, dtype=torch.float32, device=dev)
+            cols = torch.empty(N, nty, w, br.c, dtype=torch.float32, device=dev)
+            pyr.append({'wpack': br.proj_packed(dtype), 'bias': br.proj_b, 'cout': br.c, 'out': y,
+                        'rowpart': rows, 'colpart': cols})
+            wp, owp, emat, ebias = br.dsc.packed(dtype)
+            arow = torch.empty(N, h, br.c, dtype=torch.float32, device=dev)
+            colm = torch.empty(N, w, br.c, dtype=torch.float32, device=dev)
+            mask = torch.empty(N, h, w, 9, dtype=torch.float32, device=dev)
+            lcsa.append(_ext.lcsa_args(rows, ntx, cols, nty, arow, colm, br.dsc.lcsa, emat, ebias, mask, N, br.c, h,
+                                       w))
+            gap = torch.empty(N, _ext.dcn_tiles(h, w), br.c, dtype=torch.float32, device=dev)
+            if full:  # written straight into its channel slice of the output
+                z = out_v[:, br.c_off:br.c_off + br.c] if out_layout == _ext.KAD_NCHW \
+                    else out_v[..., br.c_off:br.c_off + br.c]
+                z_layout = out_layout
+            else:
+                z = torch.empty(N, h, w, br.cs, dtype=dtype, device=dev)
+                z_layout = _ext.KAD_NHWC
+            att = torch.empty(N, br.c, dtype=torch.float32, device=dev)
+            se = (br.w1, br.b1, br.w2, br.b2, att, self._se_counters(dev, i, N))
+            a = _ext.dsc_args(y, br.c, owp, br.dsc.off_b, mask, (P * 9, 9, 1), wp, br.c, z, bias=br.dsc.bias,
+                              post_mul=br.bn_a, post_add=br.bn_b, post_scale=br.scale, relu=True,
+                              out_layout=z_layout, gap_partial=gap, se=se)
+            dcn.setdefault(min((br.c + 15) // 16, 8), []).append(a)   # one launch per instantiation
+            keep += [y, rows, cols, arow, colm, mask, gap, z, att]
+            merges.append((full, {'z': z, 'c': br.c, 'c_off': br.c_off, 'att': att}))
+        st.append(('pyramid', lambda: _ext.pyramid_proj(xin, in_layout, C, pyr)))
+        st.append(('lcsa_prep', lambda keep=keep: _ext.lcsa_prep_group(lcsa)))
+        st.append(('lcsa_mask', lambda keep=keep: _ext.lcsa_mask_group(lcsa, edt)))
+        for k, args in dcn.items():
+            st.append(('dsc' if len(dcn) == 1 else f'dsc_nb{k}', lambda args=args, keep=keep: _ext.dsc_fwd_group(args)))
+        if out_layout == _ext.KAD_NHWC:
+            mb = [m for _, m in merges]
+            st.append(('merge', lambda: _ext.branch_merge(out_v, out_layout, mb, residual=xin)))
+        else:
+            for full, m in merges:
+                if full:
+                    st.append(('merge0', lambda m=m: _ext.scale_residual(out_v, m['att'], xin, m['c_off'], m['c'],
+                                                                        out_layout)))
+            up = [m for full, m in merges if not full]
+            if up:  # the upsampled branches' windows are contiguous: one band merge
+                lo, hi = up[0]['c_off'], up[-1]['c_off'] + up[-1]['c']
+                st.append(('merge', lambda: _ext.branch_merge(out_v, out_layout, up, residual=xin, channels=(lo, hi))))
+        return st, out
 
     def schedule(self, x):
         """(pre, [per-branch stages], post, out): the branch chains (LCSA, DSC,
@@ -320,9 +412,14 @@ class KADConvPlan:
         return streams[key]
 
     def forward(self, x):
-        """pyramid on the caller's stream, the branch chains forked onto side
-        streams (concurrent on the GPU; HIP-graph capture records the fork/join
-        as graph edges), merge after the join."""
+        """Grouped: every stage on the caller's stream.  Else the pyramid on the caller's
+        stream, the branch chains forked onto side streams (concurrent on the GPU;
+        HIP-graph capture records the fork/join as graph edges), merge after the join."""
+        if self._grouped(x):
+            st, out = self.schedule_grouped(x)
+            for _, fn in st:
+                fn()
+            return out
         pre, chains, post, out = self.schedule(x)
         for _, fn in pre:
             fn()

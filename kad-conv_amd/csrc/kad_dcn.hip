@@ -603,7 +603,7 @@ __device__ __forceinline__ void offset_conv16(floatx4 (&oacc)[DCN_WM][2], __amdg
 // partials in a fixed order (thread (slice s, channel c) takes tiles s,
 // s + nsl, ...; the slices are then added in order), so the result does not
 // depend on which block came last; then att = sigmoid(W2 relu(W1 g + b1) + b2)
-// with 8 lanes per output and a shuffle reduction.  lds: Cout + hid + 512 floats.
+// with 4 lanes per output and a shuffle reduction.  lds: Cout + hid + THREADS floats.
 __device__ __forceinline__ float dev_load(const float* p) {
   return __uint_as_float(__hip_atomic_load((const unsigned*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
@@ -612,20 +612,21 @@ __device__ __forceinline__ void rmw_store(float* p, float v) {
   asm volatile("" ::"v"(old));  // the returning form: the thread's wait covers it
 }
 
+template <int THREADS>
 __device__ __forceinline__ void se_tail(const float* __restrict__ partial, const float* __restrict__ w1,
                                         const float* __restrict__ b1, const float* __restrict__ w2,
                                         const float* __restrict__ b2, float* __restrict__ att, float inv_count, int C,
                                         int hid, int n, int tiles, float* lds) {
   constexpr int PB = 16;   // loads in flight per thread per batch
   constexpr int LPO = 4;   // lanes per MLP output (shuffle-reduced)
-  constexpr int OPP = DCN_THREADS / LPO;  // outputs per pass
+  constexpr int OPP = THREADS / LPO;  // outputs per pass
   const int tid = threadIdx.x;
   float* g = lds;          // [C]
   float* hb = g + C;       // [hid]
   float* red = hb + hid;   // [nsl][C]
   const float* pn = partial + (int64_t)n * tiles * C;
-  const int nsl = C < DCN_THREADS ? DCN_THREADS / C : 1;
-  for (int e = tid; e < nsl * C; e += DCN_THREADS) {
+  const int nsl = C < THREADS ? THREADS / C : 1;
+  for (int e = tid; e < nsl * C; e += THREADS) {
     const int s = e / C, ch = e - s * C;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int t0 = s; t0 < tiles; t0 += PB * nsl) {
@@ -641,7 +642,7 @@ __device__ __forceinline__ void se_tail(const float* __restrict__ partial, const
     red[e] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   }
   __syncthreads();
-  for (int ch = tid; ch < C; ch += DCN_THREADS) {
+  for (int ch = tid; ch < C; ch += THREADS) {
     float v = 0.f;
     for (int s = 0; s < nsl; ++s) v += red[s * C + ch];
     g[ch] = v * inv_count;
@@ -1213,7 +1214,7 @@ __device__ __forceinline__ void dcn_block(const kad_dcn_args& a, const DcnGeom& 
       }
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if (s_last) {
-        se_tail(a.gap_partial, a.se_w1, a.se_b1, a.se_w2, a.se_b2, a.se_att, a.se_inv_count, a.cout, a.se_hid, n,
+        se_tail<DCN_THREADS>(a.gap_partial, a.se_w1, a.se_b1, a.se_w2, a.se_b2, a.se_att, a.se_inv_count, a.cout, a.se_hid, n,
                 g.tiles, (float*)region);
       }
     }
@@ -1249,6 +1250,674 @@ __global__ __launch_bounds__(DCN_THREADS, 1) void dcn_group_kernel(DcnGroup grp)
   const int gx = grp.g[p].grid_x;
   // p is uniform over the block: the problem's fields are scalar loads from kernel-argument memory
   dcn_block<T, OutT, NBF, MODE>(grp.a[p], grp.g[p], local % gx, local / gx, grp.ny[p]);
+}
+
+// ---- 16-bit DCN / DSC with two blocks per CU ------------------------------------------------------
+// The 16-bit FUSED and EXT paths at stride 1 with up to 64 output channels and many tiles (KAD-CNet's
+// small DSCs; the dispatch rule and its measurements are at d2_ok).  On gfx950 LDS delivers ~128 B/clk per CU and L1 hits ~64 B/clk; the
+// tap loop of the 8-wave kernel above is bound by LDS reads, most of them weight fragments that
+// every wave re-reads for its 16 pixels.  Here:
+//  * 4 waves x 32 pixels (two 16-pixel A fragments per wave): half the weight-fragment reads per
+//    pixel, and they come from global memory (L1 / L2 hits: a column block's packed weights are
+//    at most 9 x 64 x 64 x 2 bytes), so LDS carries only the corner reads;
+//  * LDS < 80 KB, so two blocks share a CU and one block's latency-bound phases (conv_offset,
+//    sample setup, epilogue) overlap the other's taps;
+//  * input channels in 16-channel half-chunks: a Cin of 10 .. 16 is padded to 16, not 32;
+//  * the input region is staged per 16-channel half-chunk by direct global -> LDS loads
+//    (buffer_load_dwordx4 ... lds: lane l's 16 bytes land at base + 16 l, out-of-range pieces as
+//    zeros), double-buffered: no registers hold the prefetch.  32 bytes per region pixel
+//    (channels 8 h .. 8 h + 7 at byte 16 h);
+//  * one MFMA k-step covers two taps of a half-chunk: lane groups 0-1 take tap 2 j, groups 2-3
+//    tap 2 j + 1 (tap 9 is zero); five k-steps per half-chunk;
+//  * the sample records (corner offset, corner steps, blend weights) are built once and held in
+//    registers through all half-chunks (ten per lane).
+// Vector-memory loads retire in issue order (one counter), so a weight load issued after a
+// region prefetch also waits for the prefetch.  The next half-chunk's region is requested right
+// after the current half-chunk's last weight loads (a three-stage weight pipeline) and waited for
+// at the half-chunk barrier.
+constexpr int D2_THREADS = 256;
+constexpr int D2_WAVES = 4;
+constexpr int D2_TILE = 128;                   // pixels per block: wave w owns [32 w, 32 w + 32)
+constexpr int D2_PPT = 5;                      // samples per thread: pixel tid % 128, taps tid / 128 + 2 u
+constexpr int D2_RCAP = 1024;                  // region pixels per half-chunk buffer
+constexpr int D2_RBUF = D2_RCAP * 32;          // bytes per region buffer
+constexpr int D2_U = 2 * D2_RBUF;              // shared area: conv_offset staging, offsets, regions, epilogue
+constexpr int D2_RINST = D2_RCAP * 2 / 64 / D2_WAVES;  // direct loads per wave per half-chunk
+constexpr int D2_NBF_MAX = 4;
+constexpr unsigned D2_SLOW = 0x80000000u;      // record flag: sample outside the region (read from memory)
+static_assert(DCN_TILE == D2_TILE && D2_THREADS / D2_TILE == 2, "sample geometry");
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 bytes per lane from buffer r at voff (0 if voff is out of range) to LDS: lane l writes
+// lds_base + 16 l; lds_base must be wave-uniform.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds_base, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds_base, 16, voff, 0, 0, 0);
+}
+
+// conv_offset of the tile (stride 1) with 4 waves x two pixel fragments: per round G 32-channel
+// chunks of the footprint [fpix][8 R] and of the 18 filters [9 taps x 18][8 R] (R = 4 G + 1
+// 16-byte slots per row, the last one zero: rows 16 bytes apart in bank space) are loaded
+// straight into LDS, then 9 G k-steps of 2 x 2 MFMA.  oacc[m][b]: offset channel 16 b + row.
+template <typename T>
+__device__ __forceinline__ void d2_offset_conv(floatx4 (&oacc)[2][2], __amdgpu_buffer_rsrc_t rx, const kad_dcn_args& a,
+                                               const DcnGeom& g, int fy0, int fx0, int cin8, unsigned char* su) {
+  typedef DcnFrag<T> Ops;
+  typedef typename Ops::frag frag;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = lane & 15, grp = lane >> 4;
+  const int fpix = g.fh * g.fw, npx = g.th * g.tw;
+  const __amdgpu_buffer_rsrc_t rwo = make_rsrc(a.off_wpack, (uint32_t)(32 * g.nchunk * 9 * 32 * (int)sizeof(T)));
+  int apix[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    int pl = wave * 32 + m * 16 + row;
+    if (pl >= npx) pl = 0;  // padding lane: any in-bounds address, result discarded
+    const int py = (int)(((float)pl + 0.5f) * g.inv_tw), px = pl - py * g.tw;
+    apix[m] = py * g.fw + px;
+  }
+  for (int c0 = 0; c0 < g.nchunk;) {
+    int G = g.nchunk - c0 < 3 ? g.nchunk - c0 : 3;
+    while (G > 1 && (ceil_div(fpix * (4 * G + 1), 64) + ceil_div(9 * DCN_NOFF * (4 * G + 1), 64)) * 1024 > D2_U) --G;
+    const int R = 4 * G + 1, GS = 8 * R;
+    const float inv_r = 1.f / (float)R;
+    const int nif = ceil_div(fpix * R, 64), niw = ceil_div(9 * DCN_NOFF * R, 64);
+    const T* foot = (const T*)su;
+    const T* filt = (const T*)(su + nif * 1024);
+    for (int i = wave; i < nif + niw; i += D2_WAVES) {  // wave-uniform: one direct load per i
+      uint32_t o = KAD_OOB;
+      if (i < nif) {
+        const int s = i * 64 + lane;
+        const int q = (int)(((float)s + 0.5f) * inv_r), r = s - q * R;
+        if (q < fpix && r < 4 * G) {
+          const int qy = (int)(((float)q + 0.5f) * g.inv_fw), qx = q - qy * g.fw;
+          const int gy = fy0 + qy, gx = fx0 + qx, ch = c0 * 32 + r * 8;
+          if (gy >= 0 && gy < a.h && gx >= 0 && gx < a.w && ch < cin8)
+            o = (uint32_t)(((gy * a.w + gx) * a.x_cs + ch) * (int)sizeof(T));
+        }
+        lds_load16(rx, su + i * 1024, o);
+      } else {
+        const int s = (i - nif) * 64 + lane;
+        const int kc = (int)(((float)s + 0.5f) * inv_r), r = s - kc * R;
+        if (kc < 9 * DCN_NOFF && r < 4 * G) {
+          const int k = kc / DCN_NOFF, col = kc - k * DCN_NOFF;
+          o = (uint32_t)((((col * g.nchunk + c0 + (r >> 2)) * 9 + k) * 32 + (r & 3) * 8) * (int)sizeof(T));
+        }
+        lds_load16(rwo, su + i * 1024, o);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int gi = 0; gi < G; ++gi) {
+      const int cofs = gi * 32 + grp * 8;
+#pragma unroll
+      for (int k = 0; k < 9; ++k) {
+        const frag b0 = ld8<T>(filt + (k * DCN_NOFF + row) * GS + cofs);
+        frag b1 = zero8<T>();
+        if (row < DCN_NOFF - 16) b1 = ld8<T>(filt + (k * DCN_NOFF + 16 + row) * GS + cofs);
+        const int toff = (k / 3) * g.fw + k % 3;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const frag af = ld8<T>(foot + (apix[m] + toff) * GS + cofs);
+          oacc[m][0] = Ops::mma(af, b0, oacc[m][0]);
+          oacc[m][1] = Ops::mma(af, b1, oacc[m][1]);
+        }
+      }
+    }
+    __syncthreads();  // staging consumed before the next round (or the caller) reuses it
+    c0 += G;
+  }
+}
+
+template <typename T, int NBF, int MODE>
+__device__ __forceinline__ void dsc2_block(const kad_dcn_args& a, const DcnGeom& g, const int bx, const int by,
+                                           const int ny) {
+  static_assert(sizeof(T) == 2 && NBF <= D2_NBF_MAX && MODE != MODE_PLAIN, "16-bit DCN / DSC only");
+  typedef DcnFrag<T> Ops;
+  typedef typename Ops::frag frag;
+  constexpr int NB = NBF * 16;
+  __shared__ __align__(16) unsigned char s_u[D2_U];  // staging / offsets / region buffers / epilogue / SE
+  __shared__ unsigned s_ia[9 * D2_TILE];            // [tap][pixel] record: region offset + steps, or D2_SLOW
+  __shared__ uint2 s_iw[9 * D2_TILE];               // [tap][pixel] corner weights (2 x half2)
+  __shared__ float s_par[3][NB];                    // shift, mul, scale
+  __shared__ int s_box[4];
+  __shared__ int s_reg[5];
+
+  // XCD-aware tile order, as dcn_block
+  const int q = (bx & 7) * (g.grid_x >> 3) + (bx >> 3);
+  if (q >= a.n * g.tiles) return;  // whole block, before any barrier
+  const int n = q / g.tiles, tile = q - n * g.tiles;
+  const int co0 = by * NB;
+  const int tyi = tile / g.tiles_x;
+  const int ty0 = tyi * g.th, tx0 = (tile - tyi * g.tiles_x) * g.tw;
+  const int P = g.ho * g.wo, npx = g.th * g.tw;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = lane & 15, grp = lane >> 4;
+  const T* xb = (const T*)a.x + (int64_t)n * a.h * a.w * a.x_cs;
+  const int cin8 = round_up(a.cin, 8);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xb, (uint32_t)(a.h * a.w * a.x_cs * (int)sizeof(T)));
+  const __amdgpu_buffer_rsrc_t rwp =
+      make_rsrc(a.wpack, (uint32_t)(g.cout_pad * g.nchunk * 9 * 32 * (int)sizeof(T)));
+  const int fy0 = ty0 - a.pad, fx0 = tx0 - a.pad;
+
+  // ---- 0. independent loads ------------------------------------------------------------------------
+  float par[4] = {0.f, 1.f, 0.f, 1.f};
+  if (tid < NB) {
+    const int co = co0 + tid;
+    if (co < a.cout) {
+      if (a.bias) par[0] = a.bias[co];
+      if (a.post_mul) par[1] = a.post_mul[co];
+      if (a.post_add) par[2] = a.post_add[co];
+      if (a.post_scale) par[3] = a.post_scale[co];
+    }
+  }
+  const int ppl = tid & (D2_TILE - 1);
+  const int ppy = (int)(((float)ppl + 0.5f) * g.inv_tw), ppx = ppl - ppy * g.tw;
+  const int poy = ty0 + ppy, pox = tx0 + ppx;
+  const bool plive = ppl < npx && poy < g.ho && pox < g.wo;
+  const int64_t pp = (int64_t)poy * g.wo + pox;
+  float pre_dy[D2_PPT], pre_dx[D2_PPT], pre_m[D2_PPT];
+#pragma unroll
+  for (int u = 0; u < D2_PPT; ++u) {
+    const int k = (tid >> 7) + 2 * u;
+    pre_dy[u] = pre_dx[u] = 0.f;
+    pre_m[u] = 1.f;
+    if (k < 9 && plive) {
+      if constexpr (MODE == MODE_EXT) {
+        pre_dy[u] = a.offset[n * a.off_sn + pp * a.off_sp + (2 * k) * a.off_sc];
+        pre_dx[u] = a.offset[n * a.off_sn + pp * a.off_sp + (2 * k + 1) * a.off_sc];
+      }
+      if (a.mask) pre_m[u] = a.mask[n * a.mask_sn + pp * a.mask_sp + k * a.mask_sc];
+    }
+  }
+  if (tid == 0) {
+    s_box[0] = 0x7fffffff;
+    s_box[1] = -1;
+    s_box[2] = 0x7fffffff;
+    s_box[3] = -1;
+  }
+
+  // ---- 1. FUSED: offsets = conv_offset(x) over the tile -> s_off [128][18] (fp32, in s_u) ---------
+  const float* s_off = (const float*)s_u;
+  if constexpr (MODE == MODE_FUSED) {
+    floatx4 oacc[2][2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) oacc[m][0] = oacc[m][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+    d2_offset_conv<T>(oacc, rx, a, g, fy0, fx0, cin8, s_u);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int ch = b * 16 + row;
+      if (ch < DCN_NOFF) {
+        const float ob = a.off_bias ? a.off_bias[ch] : 0.f;
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            ((float*)s_u)[(wave * 32 + m * 16 + grp * 4 + i) * DCN_NOFF + ch] = oacc[m][b][i] + ob;
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- 2. samples: clamped corners, weights, bounding box ----------------------------------------------
+  int bymin = 0x7fffffff, bymax = -1, bxmin = 0x7fffffff, bxmax = -1;
+  int smp_yx[D2_PPT], smp_st[D2_PPT];
+  float smp_w[D2_PPT][4];
+#pragma unroll
+  for (int u = 0; u < D2_PPT; ++u) {
+    const int k = (tid >> 7) + 2 * u;
+    float* w = smp_w[u];
+    w[0] = w[1] = w[2] = w[3] = 0.f;
+    int cy0 = 0, cx0 = 0, sy = 0, sx = 0;
+    if (k < 9 && plive) {
+      const int ky = k / 3, kx = k - (k / 3) * 3;
+      float dy = pre_dy[u], dx = pre_dx[u];
+      if constexpr (MODE == MODE_FUSED) {
+        dy = s_off[ppl * DCN_NOFF + 2 * k];
+        dx = s_off[ppl * DCN_NOFF + 2 * k + 1];
+      }
+      const float py = (float)(poy - a.pad + ky) + dy;
+      const float px = (float)(pox - a.pad + kx) + dx;
+      sample_geom(py, px, pre_m[u], a.h, a.w, cy0, cx0, sy, sx, w);
+    }
+    const bool live = w[0] != 0.f || w[1] != 0.f || w[2] != 0.f || w[3] != 0.f;
+    if (live) {
+      bymin = min(bymin, cy0);
+      bymax = max(bymax, cy0 + sy);
+      bxmin = min(bxmin, cx0);
+      bxmax = max(bxmax, cx0 + sx);
+    }
+    smp_yx[u] = (cy0 << 15) | cx0;
+    smp_st[u] = (sy << 1) | sx;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    bymin = min(bymin, __shfl_xor(bymin, o));
+    bymax = max(bymax, __shfl_xor(bymax, o));
+    bxmin = min(bxmin, __shfl_xor(bxmin, o));
+    bxmax = max(bxmax, __shfl_xor(bxmax, o));
+  }
+  __syncthreads();  // s_box initialised; every s_off read done (s_u is free from here)
+  if (lane == 0) {
+    atomicMin(&s_box[0], bymin);
+    atomicMax(&s_box[1], bymax);
+    atomicMin(&s_box[2], bxmin);
+    atomicMax(&s_box[3], bxmax);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int ry0 = s_box[0], ry1 = s_box[1], rx0 = s_box[2], rx1 = s_box[3];
+    int capped = 0;
+    if (ry1 < ry0 || rx1 < rx0) {  // no live sample at all
+      ry0 = ry1 = rx0 = rx1 = 0;
+    } else if ((ry1 - ry0 + 1) * (rx1 - rx0 + 1) > D2_RCAP) {
+      // keep the tile's own footprint plus the widest halo m that fits
+      const int fy0c = max(fy0, 0), fy1 = min(fy0 + g.fh - 1, a.h - 1);
+      const int fx0c = max(fx0, 0), fx1 = min(fx0 + g.fw - 1, a.w - 1);
+      int m = 0;
+      while (m < 4096) {
+        const int y0n = max(ry0, fy0c - m - 1), y1n = min(ry1, fy1 + m + 1);
+        const int x0n = max(rx0, fx0c - m - 1), x1n = min(rx1, fx1 + m + 1);
+        if ((y1n - y0n + 1) * (x1n - x0n + 1) > D2_RCAP) break;
+        ++m;
+      }
+      const int y0n = max(ry0, fy0c - m), y1n = min(ry1, fy1 + m);
+      const int x0n = max(rx0, fx0c - m), x1n = min(rx1, fx1 + m);
+      if ((y1n - y0n + 1) * (x1n - x0n + 1) <= D2_RCAP && y1n >= y0n && x1n >= x0n) {
+        ry0 = y0n;
+        ry1 = y1n;
+        rx0 = x0n;
+        rx1 = x1n;
+      } else {  // degenerate: a 1 x 1 region, everything from memory
+        ry1 = ry0;
+        rx1 = rx0;
+      }
+      capped = 1;
+    }
+    s_reg[0] = ry0;
+    s_reg[1] = rx0;
+    s_reg[2] = ry1 - ry0 + 1;
+    s_reg[3] = rx1 - rx0 + 1;
+    s_reg[4] = capped;
+  }
+  __syncthreads();
+  const int ry0 = s_reg[0], rx0 = s_reg[1], rh = s_reg[2], rw = s_reg[3];
+  const bool block_may_slow = s_reg[4] != 0;
+  const int rpix = rh * rw;
+
+  // ---- 3. region staging: slot s = 64 (wave + 4 u) + lane holds region pixel s / 2, half s % 2 -----
+  uint32_t rpx[D2_RINST];
+  {
+    const float inv_rw = 1.f / (float)rw;
+#pragma unroll
+    for (int u = 0; u < D2_RINST; ++u) {
+      const int s = 64 * (wave + D2_WAVES * u) + lane, rq = s >> 1;
+      uint32_t o = KAD_OOB;
+      if (rq < rpix) {
+        const int qy = (int)(((float)rq + 0.5f) * inv_rw);
+        o = (uint32_t)((((ry0 + qy) * a.w + rx0 + rq - qy * rw) * a.x_cs + 8 * (s & 1)) * (int)sizeof(T));
+      }
+      rpx[u] = o;
+    }
+  }
+  // Every wave issues all D2_RINST loads (slots past the region read out of range and store
+  // zeros, inside the buffer): a fixed count lets the compiler's waits on later weight loads
+  // count past them instead of waiting for them.
+  auto stage = [&](int h) {  // half-chunk h (channels 16 h .. 16 h + 15) into buffer h % 2
+    const bool ch_ok = 16 * h + 8 * (lane & 1) < cin8;
+    unsigned char* dst = s_u + (h & 1) * D2_RBUF + 1024 * wave;
+#pragma unroll
+    for (int u = 0; u < D2_RINST; ++u)
+      lds_load16(rx, dst + 1024 * D2_WAVES * u, (ch_ok && rpx[u] != KAD_OOB) ? rpx[u] + 32 * h : KAD_OOB);
+  };
+  stage(0);
+
+  // sample records (region byte offset | sx << 16 | sy << 17, or D2_SLOW with the image corner)
+#pragma unroll
+  for (int u = 0; u < D2_PPT; ++u) {
+    const int k = (tid >> 7) + 2 * u;
+    if (k >= 9) break;
+    const float* w = smp_w[u];
+    const int cy0 = smp_yx[u] >> 15, cx0 = smp_yx[u] & 0x7fff;
+    const int sy = smp_st[u] >> 1, sx = smp_st[u] & 1;
+    const int ly = cy0 - ry0, lx = cx0 - rx0;
+    const bool dead = w[0] == 0.f && w[1] == 0.f && w[2] == 0.f && w[3] == 0.f;
+    unsigned ia = 0u;
+    if (!dead) {
+      if (ly >= 0 && ly + sy < rh && lx >= 0 && lx + sx < rw)
+        ia = (unsigned)((ly * rw + lx) * 32) | ((unsigned)sx << 16) | ((unsigned)sy << 17);
+      else
+        ia = D2_SLOW | ((unsigned)sy << 30) | ((unsigned)sx << 29) | ((unsigned)cy0 << 14) | (unsigned)cx0;
+    }
+    s_ia[k * D2_TILE + ppl] = ia;
+    s_iw[k * D2_TILE + ppl] = make_uint2(pack_h2(w[0], w[1]), pack_h2(w[2], w[3]));
+  }
+  __syncthreads();  // records visible
+
+  // this lane's records: k-step j, fragment m -> tap 2 j + (grp >> 1), pixel 32 wave + 16 m + row
+  unsigned r_a[5][2], r_w01[5][2], r_w23[5][2];
+#pragma unroll
+  for (int j = 0; j < 5; ++j) {
+    const int kt = 2 * j + (grp >> 1);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      unsigned ia = 0u;
+      uint2 wv = make_uint2(0u, 0u);
+      if (kt < 9) {
+        const int qi = kt * D2_TILE + wave * 32 + m * 16 + row;
+        ia = s_ia[qi];
+        wv = s_iw[qi];
+        if (ia & D2_SLOW) {  // added by the pass from memory
+          ia = 0u;
+          wv = make_uint2(0u, 0u);
+        }
+      }
+      r_a[j][m] = ia;
+      r_w01[j][m] = wv.x;
+      r_w23[j][m] = wv.y;
+    }
+  }
+
+  // weight fragment (column fragment f, half-chunk h, k-step j): lane (row, grp) reads column
+  // co0 + 16 f + row, tap 2 j + (grp >> 1), channels 16 h + 8 (grp & 1) .. + 7 of the packed
+  // [cout_pad][nchunk][9][32] weights; tap 9 reads nothing (zero)
+  uint32_t wcol[NBF];
+#pragma unroll
+  for (int f = 0; f < NBF; ++f) {
+    const int co = co0 + f * 16 + row;
+    wcol[f] = (uint32_t)(((co < g.cout_pad ? co : 0) * g.nchunk * 288 + (grp >> 1) * 32 + (grp & 1) * 8) *
+                         (int)sizeof(T));
+  }
+  auto ld_w = [&](int h, int j, frag (&d)[NBF]) {
+    const bool pad = j == 4 && (grp >> 1) != 0;
+    const uint32_t so = (uint32_t)((((h >> 1) * 9 + 2 * j) * 32 + (h & 1) * 16) * (int)sizeof(T));
+#pragma unroll
+    for (int f = 0; f < NBF; ++f) d[f] = buf_ld8<T>(rwp, pad ? KAD_OOB : wcol[f] + so);
+  };
+
+  floatx4 acc[2][NBF];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int f = 0; f < NBF; ++f) acc[m][f] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // ---- 4. taps: nh half-chunks x 5 k-steps -----------------------------------------------------------
+  // Per k-step: the weights of the next k-step and the corners of the next k-step are requested
+  // before this k-step's MFMAs; the corners are blended as soon as they arrive (A fragments of one
+  // k-step ahead).  Weights alternate between two register sets; the next half-chunk's region is
+  // requested after the last weight load of this half-chunk (k-step 4's, issued at k-step 3).
+  const int nh = ceil_div(a.cin, 16);
+  const int rw32 = rw * 32;
+  const unsigned lds_base = (unsigned)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)s_u;
+  frag bwa[NBF], bwb[NBF];
+  ld_w(0, 0, bwa);
+  for (int h = 0; h < nh; ++h) {
+    // the records are loop-invariant: keep the compiler from hoisting values derived from them
+    // (splat weights, corner addresses) for all ten records out of the loop
+#pragma unroll
+    for (int j = 0; j < 5; ++j)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) asm volatile("" : "+v"(r_a[j][m]), "+v"(r_w01[j][m]), "+v"(r_w23[j][m]));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's share of region h has landed
+    __syncthreads();  // everyone's share landed; everyone is done with region h - 1 (buffer of h + 1)
+    // Corner reads are issued as inline ds_read_b128 with an explicit lgkmcnt wait tied to their
+    // registers (wait_c).  Plain loads would make the compiler wait for the region prefetch in
+    // flight (it cannot tell that those LDS writes go to the other buffer); the barrier above
+    // orders them after this buffer's writes.
+    const unsigned rb = lds_base + (unsigned)((h & 1) * D2_RBUF + 16 * (grp & 1));
+    auto ld_c = [&](int j, frag (&c)[2][4]) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const unsigned ia = r_a[j][m];
+        const unsigned p0 = rb + (ia & 0xffffu), dx = (ia >> 11) & 32u;
+        const unsigned p2 = p0 + ((ia & (1u << 17)) ? (unsigned)rw32 : 0u);
+        asm volatile("ds_read_b128 %0, %1" : "=v"(c[m][0]) : "v"(p0));
+        asm volatile("ds_read_b128 %0, %1" : "=v"(c[m][1]) : "v"(p0 + dx));
+        asm volatile("ds_read_b128 %0, %1" : "=v"(c[m][2]) : "v"(p2));
+        asm volatile("ds_read_b128 %0, %1" : "=v"(c[m][3]) : "v"(p2 + dx));
+      }
+    };
+    auto wait_c = [&](frag (&c)[2][4]) {
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(c[0][0]), "+v"(c[0][1]), "+v"(c[0][2]), "+v"(c[0][3]), "+v"(c[1][0]), "+v"(c[1][1]),
+                     "+v"(c[1][2]), "+v"(c[1][3]));
+    };
+    auto blend = [&](int j, const frag (&c)[2][4], frag (&af)[2]) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        Info16 in;
+        in.o01 = in.o23 = 0u;
+        in.w01 = r_w01[j][m];
+        in.w23 = r_w23[j][m];
+        af[m] = Ops::blend(c[m][0], c[m][1], c[m][2], c[m][3], in);
+      }
+    };
+    auto mma = [&](const frag (&af)[2], const frag (&bw)[NBF]) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int f = 0; f < NBF; ++f) acc[m][f] = Ops::mma(af[m], bw[f], acc[m][f]);
+    };
+    const bool more = h + 1 < nh;
+    frag raw[2][4], af0[2], af1[2];
+    ld_c(0, raw);
+    wait_c(raw);
+    blend(0, raw, af0);
+    ld_w(h, 1, bwb);
+    ld_c(1, raw);
+    mma(af0, bwa);  // k-step 0
+    wait_c(raw);
+    blend(1, raw, af1);
+    ld_w(h, 2, bwa);
+    ld_c(2, raw);
+    mma(af1, bwb);  // k-step 1
+    wait_c(raw);
+    blend(2, raw, af0);
+    ld_w(h, 3, bwb);
+    ld_c(3, raw);
+    mma(af0, bwa);  // k-step 2
+    wait_c(raw);
+    blend(3, raw, af1);
+    ld_w(h, 4, bwa);
+    if (more) stage(h + 1);  // after the half-chunk's last weight load
+    ld_c(4, raw);
+    mma(af1, bwb);  // k-step 3
+    wait_c(raw);
+    blend(4, raw, af0);
+    if (more) ld_w(h + 1, 0, bwb);
+    mma(af0, bwa);  // k-step 4
+#pragma unroll
+    for (int f = 0; f < NBF; ++f) bwa[f] = bwb[f];
+  }
+
+  // ---- 4b. samples outside a capped region: straight from memory (rare) -------------------------------
+  if (block_may_slow) {
+    for (int h = 0; h < nh; ++h) {
+      const int ch = 16 * h + 8 * (grp & 1);
+      const bool ch_ok = ch < cin8;
+#pragma unroll 1
+      for (int j = 0; j < 5; ++j) {
+        const int kt = 2 * j + (grp >> 1);
+        frag af[2];
+        bool any = false;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          af[m] = zero8<T>();
+          if (kt < 9 && ch_ok) {
+            const int qi = kt * D2_TILE + wave * 32 + m * 16 + row;
+            const unsigned ia = s_ia[qi];
+            if (ia & D2_SLOW) {
+              const int cy0 = (int)((ia >> 14) & 0x7fffu), cx0 = (int)(ia & 0x3fffu);
+              const int sx = (int)((ia >> 29) & 1u), sy = (int)((ia >> 30) & 1u);
+              const uint2 wv = s_iw[qi];
+              Info16 in;
+              in.o01 = in.o23 = 0u;
+              in.w01 = wv.x;
+              in.w23 = wv.y;
+              const T* g0 = xb + ((int64_t)cy0 * a.w + cx0) * a.x_cs + ch;
+              af[m] = Ops::blend(ld8<T>(g0), ld8<T>(g0 + sx * a.x_cs), ld8<T>(g0 + (int64_t)sy * a.w * a.x_cs),
+                                 ld8<T>(g0 + ((int64_t)sy * a.w + sx) * a.x_cs), in);
+              any = true;
+            }
+          }
+        }
+        if (__builtin_amdgcn_ballot_w64(any) == 0) continue;
+        frag bw[NBF];
+        ld_w(h, j, bw);
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int f = 0; f < NBF; ++f) acc[m][f] = Ops::mma(af[m], bw[f], acc[m][f]);
+      }
+    }
+  }
+
+  // ---- 5. epilogue: values -> LDS tile -> row-contiguous stores; GAP partials ------------------------
+  typedef T OutT;
+  constexpr int SROW = NB + 16 / (int)sizeof(OutT);
+  constexpr int STAGE_BYTES = D2_TILE * SROW * (int)sizeof(OutT);
+  static_assert(STAGE_BYTES + D2_WAVES * NB * 4 <= D2_U, "epilogue tile must fit the shared area");
+  OutT* ost = (OutT*)s_u;
+  float(*gap_red)[NB] = (float(*)[NB])(s_u + STAGE_BYTES);
+  if (tid < NB) {  // v = acc * mul + (bias * mul + add)
+    s_par[0][tid] = par[0] * par[1] + par[2];
+    s_par[1][tid] = par[1];
+    s_par[2][tid] = par[3];
+  }
+  __syncthreads();  // every wave is done reading the region; s_par staged
+  bool pix_ok[2][4];
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int pl = wave * 32 + m * 16 + grp * 4 + i;
+      const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+      pix_ok[m][i] = pl < npx && ty0 + oyl < g.ho && tx0 + pl - oyl * g.tw < g.wo;
+    }
+  float gsum[NBF];
+#pragma unroll
+  for (int f = 0; f < NBF; ++f) {
+    gsum[f] = 0.f;
+    const int col = f * 16 + row;
+    const bool co_ok = co0 + col < a.cout;
+    const float shift = s_par[0][col], mul = s_par[1][col], scl = s_par[2][col];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pl = wave * 32 + m * 16 + grp * 4 + i;
+        float v = fmaf(acc[m][f][i], mul, shift);
+        if (a.relu == KAD_ACT_SILU) v = v * sigmoidf_(v);
+        else if (a.relu) v = fmaxf(v, 0.f);
+        v *= scl;
+        const OutT o = from_f32<OutT>(v);
+        ost[pl * SROW + col] = o;
+        if (co_ok && pix_ok[m][i]) gsum[f] += to_f32(o);
+      }
+  }
+  if (a.gap_partial) {
+#pragma unroll
+    for (int f = 0; f < NBF; ++f) {
+      const float v = sum_xor32(sum_xor16(gsum[f]));
+      if (grp == 0) gap_red[wave][f * 16 + row] = v;
+    }
+  }
+  __syncthreads();
+  OutT* out = (OutT*)a.out;
+  constexpr int VEC = 16 / (int)sizeof(OutT);
+  const bool vec_ok = a.out_layout == KAD_NHWC && (a.out_cs * (int)sizeof(OutT)) % 16 == 0 &&
+                      ((uintptr_t)a.out & 15) == 0;
+  if (vec_ok) {
+    constexpr int VPP = NB / VEC;
+    for (int j = tid; j < D2_TILE * VPP; j += D2_THREADS) {
+      const int pl = j / VPP, v = j - pl * VPP;
+      const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+      const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
+      const int co = co0 + v * VEC;
+      if (pl >= npx || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
+      const OutT* src = ost + pl * SROW + v * VEC;
+      OutT* dst = out + ((int64_t)n * P + (int64_t)oy * g.wo + ox) * a.out_cs + co;
+      if (co + VEC <= a.cout) {
+        *(intx4*)dst = *(const intx4*)src;
+      } else {
+        for (int e = 0; e < a.cout - co; ++e) dst[e] = src[e];
+      }
+    }
+  } else if (a.out_layout == KAD_NHWC) {
+    for (int j = tid; j < D2_TILE * NB; j += D2_THREADS) {
+      const int pl = j / NB, col = j - pl * NB;
+      const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+      const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
+      const int co = co0 + col;
+      if (pl >= npx || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
+      out[((int64_t)n * P + (int64_t)oy * g.wo + ox) * a.out_cs + co] = ost[pl * SROW + col];
+    }
+  } else {  // NCHW: consecutive lanes along the tile's pixels; a thread keeps its pixel
+    constexpr int CSTEP = D2_THREADS / D2_TILE;
+    const int pl = tid % D2_TILE, col0 = tid / D2_TILE;
+    const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
+    const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
+    if (pl < npx && oy < g.ho && ox < g.wo) {
+      OutT* dst = out + ((int64_t)n * a.out_cs + co0 + col0) * P + (int64_t)oy * g.wo + ox;
+      const OutT* src = ost + pl * SROW + col0;
+      const int ncol = a.cout - co0 < NB ? a.cout - co0 : NB;
+#pragma unroll 4
+      for (int col = col0; col < ncol; col += CSTEP) {
+        *dst = *src;
+        dst += (int64_t)CSTEP * P;
+        src += CSTEP;
+      }
+    }
+  }
+  if (a.gap_partial && tid < NB) {
+    const int co = co0 + tid;
+    if (co < a.cout) {
+      float v = 0.f;
+#pragma unroll
+      for (int i = 0; i < D2_WAVES; ++i) v += gap_red[i][tid];
+      float* dst = a.gap_partial + ((int64_t)n * g.tiles + tile) * a.cout + co;
+      if (a.se_att)
+        rmw_store(dst, v);  // read by another block of this launch (fused SE)
+      else
+        *dst = v;
+    }
+  }
+
+  // ---- 6. fused squeeze-excitation: the image's last block runs the MLP (protocol at se_tail) ----------
+  if (a.se_att && a.gap_partial) {
+    __shared__ int s_last;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (tid == 0) {
+      const unsigned total = (unsigned)g.tiles * ny;
+      const unsigned prev = __hip_atomic_fetch_add(a.se_count + n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev + 1u == total;
+      if (last) {
+        const unsigned z = __hip_atomic_exchange(a.se_count + n, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(z));
+      }
+      s_last = last;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (s_last)
+      se_tail<D2_THREADS>(a.gap_partial, a.se_w1, a.se_b1, a.se_w2, a.se_b2, a.se_att, a.se_inv_count, a.cout,
+                          a.se_hid, n, g.tiles, (float*)s_u);
+  }
+}
+
+template <typename T, int NBF, int MODE>
+__global__ __launch_bounds__(D2_THREADS, 2) void dsc2_kernel(kad_dcn_args a, DcnGeom g) {
+  dsc2_block<T, NBF, MODE>(a, g, blockIdx.x, blockIdx.y, gridDim.y);
+}
+
+template <typename T, int NBF>
+__global__ __launch_bounds__(D2_THREADS, 2) void dsc2_group_kernel(DcnGroup grp) {
+  const int id = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < KAD_DCN_GROUP_MAX; ++i)
+    if (i < grp.count && id >= grp.start[i]) p = i;
+  if (id >= grp.start[p + 1]) return;
+  const int local = id - grp.start[p];
+  const int gx = grp.g[p].grid_x;
+  dsc2_block<T, NBF, MODE_FUSED>(grp.a[p], grp.g[p], local % gx, local / gx, grp.ny[p]);
 }
 
 // ---- weight packing ------------------------------------------------------------------------------
@@ -1347,6 +2016,60 @@ static int validate_dcn(const kad_dcn_args* a, int mode, DcnGeom* g_out) {
 
 using namespace kad;
 
+namespace kad {
+// The two-blocks-per-CU kernel: 16-bit, stride 1, at most D2_COUT_MAX output channels (one column
+// block), and enough blocks (>= D2_MIN_BLOCKS over all problems of a launch) for two to share a
+// CU.  Measured per launch on KAD-CNet-S (bs16, 800^2, fp16): 1680 blocks of Cout <= 16: 90 ->
+// 59 us; 432 blocks: 33 -> 22 us; but 128 blocks of Cout 32: 19.8 -> 21.7 us (one 4-wave block
+// per CU), and the KAD-Conv(256) branches (Cout 86 at 100^2 / 50^2 / 25^2: 640 / 160 / 40
+// blocks) 87 / 32 / 31 -> 89 / 44 / 44 us.  Everything else runs on dcn_fwd_kernel.
+constexpr int D2_COUT_MAX = 16 * D2_NBF_MAX;
+constexpr int64_t D2_MIN_BLOCKS = 384;
+static bool d2_shape_ok(const kad_dcn_args& a) {
+  return (a.dtype == KAD_F16 || a.dtype == KAD_BF16) && a.stride == 1 && a.cout <= D2_COUT_MAX;
+}
+static bool d2_ok(const kad_dcn_args& a, const DcnGeom& g) {
+  return d2_shape_ok(a) && (int64_t)a.n * g.tiles >= D2_MIN_BLOCKS;
+}
+
+template <typename T, int NBF, int MODE>
+static int launch_d2(const kad_dcn_args& a, hipStream_t st, const DcnGeom& g) {
+  hipLaunchKernelGGL((dsc2_kernel<T, NBF, MODE>), dim3(g.grid_x, 1, 1), dim3(D2_THREADS), 0, st, a, g);
+  return check_launch(MODE == MODE_FUSED ? "kad_dsc_fwd" : "kad_dcn_fwd");
+}
+
+template <typename T, int MODE>
+static int dispatch_d2(const kad_dcn_args& a, hipStream_t st, const DcnGeom& g) {
+  switch (ceil_div(a.cout, 16)) {
+    case 1: return launch_d2<T, 1, MODE>(a, st, g);
+    case 2: return launch_d2<T, 2, MODE>(a, st, g);
+    case 3: return launch_d2<T, 3, MODE>(a, st, g);
+    default: return launch_d2<T, 4, MODE>(a, st, g);
+  }
+}
+
+template <int MODE>
+static int dispatch_d2_dtype(const kad_dcn_args& a, hipStream_t st, const DcnGeom& g) {
+  return a.dtype == KAD_F16 ? dispatch_d2<half_t, MODE>(a, st, g) : dispatch_d2<bf16_t, MODE>(a, st, g);
+}
+
+template <typename T, int NBF>
+static int launch_group_d2(const DcnGroup& grp, hipStream_t st) {
+  hipLaunchKernelGGL((dsc2_group_kernel<T, NBF>), dim3(grp.start[grp.count]), dim3(D2_THREADS), 0, st, grp);
+  return check_launch("kad_dsc_fwd_group");
+}
+
+template <typename T>
+static int dispatch_group_d2(const DcnGroup& grp, int nbf, hipStream_t st) {
+  switch (nbf) {
+    case 1: return launch_group_d2<T, 1>(grp, st);
+    case 2: return launch_group_d2<T, 2>(grp, st);
+    case 3: return launch_group_d2<T, 3>(grp, st);
+    default: return launch_group_d2<T, 4>(grp, st);
+  }
+}
+}  // namespace kad
+
 extern "C" int64_t kad_dcn_wpack_elems(int cin, int cout) {
   if (cin <= 0 || cout <= 0) return 0;
   return (int64_t)round_up(cout, 16) * ceil_div(cin, 32) * 9 * 32;
@@ -1407,6 +2130,7 @@ extern "C" int kad_dcn_fwd(const kad_dcn_args* a, void* stream) {
   int rc = validate_dcn(a, MODE_EXT, &g);
   if (rc) return fail(rc, "kad_dcn_fwd: %s", kad_last_error());
   hipStream_t st = (hipStream_t)stream;
+  if (d2_ok(*a, g)) return dispatch_d2_dtype<MODE_EXT>(*a, st, g);
   switch (a->dtype) {
     case KAD_F32: return dispatch_dcn<float, float, MODE_EXT>(*a, st, g);
     case KAD_F16: return dispatch_dcn<half_t, half_t, MODE_EXT>(*a, st, g);
@@ -1420,6 +2144,7 @@ extern "C" int kad_dsc_fwd(const kad_dcn_args* a, void* stream) {
   int rc = validate_dcn(a, MODE_FUSED, &g);
   if (rc) return fail(rc, "kad_dsc_fwd: %s", kad_last_error());
   hipStream_t st = (hipStream_t)stream;
+  if (d2_ok(*a, g)) return dispatch_d2_dtype<MODE_FUSED>(*a, st, g);
   switch (a->dtype) {
     case KAD_F32: return dispatch_dcn<float, float, MODE_FUSED>(*a, st, g);
     case KAD_F16: return dispatch_dcn<half_t, half_t, MODE_FUSED>(*a, st, g);
@@ -1474,6 +2199,12 @@ extern "C" int kad_dsc_fwd_group(const kad_dcn_args* a, int count, void* stream)
   grp.start[count] = (int)blocks;
   for (int p = count + 1; p <= KAD_DCN_GROUP_MAX; ++p) grp.start[p] = (int)blocks;
   hipStream_t st = (hipStream_t)stream;
+  bool all_d2 = blocks >= D2_MIN_BLOCKS;
+  for (int p = 0; p < count; ++p) all_d2 = all_d2 && d2_shape_ok(a[p]);
+  if (all_d2) {
+    if (a[0].dtype == KAD_F16) return dispatch_group_d2<half_t>(grp, nbf, st);
+    return dispatch_group_d2<bf16_t>(grp, nbf, st);
+  }
   switch (a[0].dtype) {
     case KAD_F32: return dispatch_group<float, float>(grp, nbf, st);
     case KAD_F16: return dispatch_group<half_t, half_t>(grp, nbf, st);

@@ -72,6 +72,22 @@ def test_dcn_small(dt, shape):
     check_close(got, _ref(x, off, mask, w, b, dtype), dtype, f'{dt} {shape}')
 
 
+@pytest.mark.parametrize('dt', ['f16', 'bf16'])
+@pytest.mark.parametrize('shape,pixel_major', [((8, 12, 16, 100, 100), True), ((12, 20, 44, 64, 64), False)])
+def test_dcn_two_blocks_per_cu(dt, shape, pixel_major):
+    """16-bit, stride 1, Cout <= 64 and >= 384 tile blocks: the launch runs on the
+    two-blocks-per-CU kernel (16-channel half-chunks, records in registers)."""
+    from kadconv import _ext
+    N, C, Co, H, W = shape
+    assert N * _ext.dcn_tiles(H, W) >= 384
+    dtype = DT[dt]
+    x, off, mask, w, b = _inputs(N, C, Co, H, W, seed=C + Co)
+    print(f'dcn_two_per_cu dt={dt} shape={shape}', flush=True)
+    got = _run(x, off, mask, w, b, dtype, pixel_major=pixel_major, out_layout='nhwc' if pixel_major else 'nchw')
+    torch.cuda.synchronize()
+    check_close(got, _ref(x, off, mask, w, b, dtype), dtype, f'{dt} {shape}')
+
+
 @pytest.mark.parametrize('dt', ['f16', 'f32', 'bf16'])
 @pytest.mark.parametrize('C,H', [(128, 100), (256, 50), (512, 25)])
 def test_dcn_config2_shapes(dt, C, H):

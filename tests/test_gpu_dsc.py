@@ -72,7 +72,7 @@ def _run_dsc(x, ow, ob, w, b, mask, dtype, stride=1, out_layout='nchw', epi=None
 
 @pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
 @pytest.mark.parametrize('shape', [(2, 8, 8, 9, 11), (1, 22, 22, 20, 20), (2, 86, 86, 17, 23), (1, 40, 72, 13, 7),
-                                   (1, 33, 130, 12, 70)])
+                                   (1, 33, 130, 12, 70), (2, 3, 16, 11, 9), (1, 16, 24, 3, 190), (1, 96, 96, 5, 6)])
 def test_dsc_small(dt, shape):
     N, C, Co, H, W = shape
     dtype = DT[dt]
@@ -99,6 +99,43 @@ def test_dsc_branch0_shape(dt, off_std):
     check_close(got, _ref(x, ow, ob, w, b, mask, dtype), dtype, f'{dt} off_std={off_std}')
 
 
+@pytest.mark.parametrize('dt', ['f16', 'bf16'])
+@pytest.mark.parametrize('shape,off_std,layout', [((8, 10, 12, 100, 100), 2.0, 'nhwc'), ((12, 16, 16, 64, 64), 4.0, 'nchw'),
+                                                  ((8, 22, 44, 80, 80), 2.0, 'nchw'), ((12, 3, 64, 60, 70), 1.0, 'nhwc'),
+                                                  ((6, 40, 33, 90, 90), 12.0, 'nhwc')])
+def test_dsc_two_blocks_per_cu(dt, shape, off_std, layout):
+    """16-bit, stride 1, Cout <= 64 and >= 384 tile blocks: the launch runs on the
+    two-blocks-per-CU kernel.  Cin 3 / 10 / 22 / 40 (one half-chunk partly
+    padded, two, three), Cout not a multiple of 16, NCHW and NHWC outputs,
+    offsets up to 12 px (capped regions: samples from global memory)."""
+    from kadconv import _ext
+    N, C, Co, H, W = shape
+    assert N * _ext.dcn_tiles(H, W) >= 384
+    dtype = DT[dt]
+    x, ow, ob, w, b = _inputs(N, C, Co, H, W, seed=C * 3 + Co, off_std=off_std)
+    mask = _mask(N, H, W, seed=C)
+    print(f'dsc_two_per_cu dt={dt} shape={shape} off_std={off_std}', flush=True)
+    got = _run_dsc(x, ow, ob, w, b, mask, dtype, out_layout=layout)
+    torch.cuda.synchronize()
+    check_close(got, _ref(x, ow, ob, w, b, mask, dtype), dtype, f'{dt} {shape} off_std={off_std}')
+
+
+@pytest.mark.parametrize('dt', ['f16', 'bf16'])
+def test_dsc_two_blocks_per_cu_gap(dt):
+    """GAP partials of the two-blocks-per-CU kernel: fp32 sums of the rounded outputs."""
+    from kadconv import _ext
+    N, C, Co, H, W = 8, 16, 20, 100, 100
+    assert N * _ext.dcn_tiles(H, W) >= 384
+    x, ow, ob, w, b = _inputs(N, C, Co, H, W, seed=5)
+    mask = _mask(N, H, W, seed=5)
+    gap = torch.full((N, _ext.dcn_tiles(H, W), Co), float('nan'), device='cuda')
+    out = _run_dsc(x, ow, ob, w, b, mask, DT[dt], out_layout='nhwc', gap=gap)
+    torch.cuda.synchronize()
+    got = gap.sum(1).cpu().double() / (H * W)
+    ref = out.double().mean(dim=(2, 3)).cpu()
+    assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5)
+
+
 @pytest.mark.parametrize('dt', ['f32', 'f16'])
 def test_dsc_stride2_epilogue_nomask(dt):
     dtype = DT[dt]
@@ -115,16 +152,32 @@ def test_dsc_stride2_epilogue_nomask(dt):
     check_close(got, ref, dtype, f'stride2 {dt}')
 
 
-def test_dsc_gap_partials_sum_to_mean():
+@pytest.mark.parametrize('dt', ['f32', 'f16'])
+def test_dsc_gap_partials_sum_to_mean(dt):
+    """The per-tile GAP partials are fp32 sums of the rounded outputs."""
     from kadconv import _ext
     x, ow, ob, w, b = _inputs(2, 16, 20, 30, 30, seed=3)
     mask = _mask(2, 30, 30, seed=3)
     gap = torch.full((2, _ext.dcn_tiles(30, 30), 20), float('nan'), device='cuda')
-    out = _run_dsc(x, ow, ob, w, b, mask, torch.float32, out_layout='nhwc', gap=gap)
+    out = _run_dsc(x, ow, ob, w, b, mask, DT[dt], out_layout='nhwc', gap=gap)
     torch.cuda.synchronize()
     got = gap.sum(1).cpu().double() / 900
     ref = out.double().mean(dim=(2, 3)).cpu()
     assert torch.allclose(got, ref, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize('dt', ['f16', 'bf16'])
+def test_dsc_far_offsets(dt):
+    """Offsets of ~20 px: most samples fall outside any region that fits the
+    LDS budget (capped or 1 x 1 regions), so the pass from global memory
+    carries them; many are dead (outside the image)."""
+    dtype = DT[dt]
+    x, ow, ob, w, b = _inputs(2, 40, 48, 37, 41, seed=20, off_std=20.0)
+    mask = _mask(2, 37, 41, seed=20)
+    print(f'dsc_far_offsets dt={dt}', flush=True)
+    got = _run_dsc(x, ow, ob, w, b, mask, dtype, out_layout='nhwc')
+    torch.cuda.synchronize()
+    check_close(got, _ref(x, ow, ob, w, b, mask, dtype), dtype, f'far offsets {dt}')
 
 
 @pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
@@ -166,7 +219,8 @@ def test_dsc_rejects_stride3():
 
 
 @pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
-@pytest.mark.parametrize('C,Co,hid,H,W', [(86, 86, 86, 23, 31), (24, 130, 16, 17, 40), (40, 40, 32, 9, 9)])
+@pytest.mark.parametrize('C,Co,hid,H,W', [(86, 86, 86, 23, 31), (24, 130, 16, 17, 40), (40, 40, 32, 9, 9),
+                                           (16, 16, 16, 128, 128)])
 def test_dsc_fused_squeeze_excitation(dt, C, Co, hid, H, W):
     """kad_dsc_fwd with the SE fields set: the last block of each image turns the
     GAP partials into att = sigmoid(W2 relu(W1 mean(out) + b1) + b2)
@@ -174,7 +228,9 @@ def test_dsc_fused_squeeze_excitation(dt, C, Co, hid, H, W):
     kernel's own output (so only the reduction and the MLP are under test).
     Several calls in a row with changing batch sizes share one counter buffer,
     which every completed call must leave at zero; Co = 130 spans two column
-    blocks, whose partials the last block must both see.  att tolerance: 2e-5
+    blocks, whose partials the last block must both see; at 16 channels and
+    128 x 128 the 16-bit calls with N >= 3 run on the two-blocks-per-CU kernel
+    and the others on the 8-wave one, on the same counters.  att tolerance: 2e-5
     absolute (fp32 sums of at most H*W values, sigmoid slope <= 1/4)."""
     from kadconv import _ext
     dtype, dev = DT[dt], 'cuda'

@@ -67,7 +67,8 @@ def test_nhwc_resample(dt, mode, k, s, p):
 @pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
 @pytest.mark.parametrize('cin,cout,stride,groups,act', [(3, 40, 2, 1, 'silu'), (72, 144, 2, 1, 'silu'),
                                                         (32, 32, 1, 1, 'silu'), (64, 64, 1, 4, 'silu'),
-                                                        (144, 40, 1, 1, 'none'), (16, 24, 1, 1, 'relu')])
+                                                        (144, 40, 1, 1, 'none'), (16, 24, 1, 1, 'relu'),
+                                                        (128, 200, 2, 1, 'silu'), (24, 20, 1, 1, 'none')])
 def test_conv3x3_fwd(dt, cin, cout, stride, groups, act):
     """kad_conv_fwd (KAD-CNet's 3x3 Conv after Conv-BN fusion) against F.conv2d in
     float64 on the dtype-rounded operands; input read from a channel slice, output

@@ -334,6 +334,14 @@ int kad_se_pool(const void *x, float *partial, int n, int c, int h, int w, int l
 int kad_se_mlp(const float *partial, int tiles, float inv_count, const float *w1, const float *b1, const float *w2,
                const float *b2, float *att, int n, int c, int hid, void *stream);
 
+/* kad_se_mlp with a caller-owned workspace hidden [n][hid] fp32 (its contents on return are
+ * the hidden activations relu(W1 g + b1)): each layer runs as one launch spread over the
+ * batch's hidden units / channels instead of one block per image (C <= 1024, hid <= 64;
+ * other shapes run kad_se_mlp and leave hidden untouched).  Same result as kad_se_mlp up to
+ * fp32 summation order.  Same reference as kad_se_mlp (kadc_fused_sm75.py:1518-1542). */
+int kad_se_mlp_ws(const float *partial, int tiles, float inv_count, const float *w1, const float *b1,
+                  const float *w2, const float *b2, float *att, int n, int c, int hid, float *hidden, void *stream);
+
 /* out = x * att[n][c] (NCHW, or NHWC with channel stride x_cs).
  * Reference k_apply_tiled (acceleration/kadc_fused_sm75.py:1203-1217). */
 int kad_channel_scale(const void *x, const float *att, void *out, int n, int c, int h, int w, int layout, int x_cs,

@@ -923,6 +923,103 @@ static int grid_for(int64_t total) {
 
 using namespace kad;
 
+// ---- SE MLP over the whole batch, two launches (caller-owned hidden buffer) -------------------
+// One block per image pulls both weight matrices (2 x hid x C fp32: 512 KB at C = 1024) through
+// a single CU; here both layers are spread over (unit, 4-image group) waves:
+//  layer 1: wave (j, images 4 y .. 4 y + 3): lane l holds W1[j][l + 64 k] and the four images'
+//           tile-summed g at the same channels (every load issued before the first add), then
+//           four interleaved wave reductions; grid (ceil(hid / 4), ceil(n / 4)) x 4 waves;
+//  layer 2: block (64 channels, 4 images): the block's W2 rows, one contiguous span, are staged
+//           in LDS with an odd row stride by coalesced loads; thread (image, channel) forms
+//           att = sigmoid(W2[ch] . h[i] + b2[ch]).
+// Each output is a fixed-order sum, independent of the grid.
+constexpr int SEL_MAXC = 1024;    // layer 1: C / 64 <= 16 channels per lane
+constexpr int SEL_MAXHID = 64;    // layer 2: W2 slice [64][hid + 1] and h [4][hid] in LDS
+
+__global__ __launch_bounds__(256) void se_mlp_l1_kernel(const float* partial, int tiles, float inv_count,
+                                                        const float* w1, const float* b1, float* hbuf, int n, int c,
+                                                        int hid) {
+  constexpr int KC = SEL_MAXC / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int j = blockIdx.x * 4 + wave, i0 = blockIdx.y * 4;
+  if (j >= hid) return;  // no barrier in this kernel
+  float wv[KC];
+#pragma unroll
+  for (int k = 0; k < KC; ++k) wv[k] = lane + 64 * k < c ? w1[(int64_t)j * c + lane + 64 * k] : 0.f;
+  float gv[4][KC];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int k = 0; k < KC; ++k) gv[q][k] = 0.f;
+  for (int t = 0; t < tiles; ++t) {
+    float ld[4][KC];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        const int i = i0 + q, ch = lane + 64 * k;
+        ld[q][k] = (i < n && ch < c) ? partial[((int64_t)i * tiles + t) * c + ch] : 0.f;
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int k = 0; k < KC; ++k) gv[q][k] += ld[q][k];
+  }
+  float a[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    a[q] = 0.f;
+#pragma unroll
+    for (int k = 0; k < KC; ++k) a[q] += wv[k] * (gv[q][k] * inv_count);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] += __shfl_xor(a[q], o);
+  const float bj = b1 ? b1[j] : 0.f;
+  if (lane < 4 && i0 + lane < n) {
+    float v = a[0];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) v = lane == q ? a[q] : v;
+    hbuf[(int64_t)(i0 + lane) * hid + j] = fmaxf(v + bj, 0.f);
+  }
+}
+
+__global__ __launch_bounds__(256) void se_mlp_l2_kernel(const float* hbuf, const float* w2, const float* b2,
+                                                        float* att, int n, int c, int hid) {
+  __shared__ float ws[64 * (SEL_MAXHID + 1)];  // [64 channels][hid + 1]
+  __shared__ float hs[4 * SEL_MAXHID];         // [4 images][hid]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c0 = blockIdx.x * 64, i0 = blockIdx.y * 4, i = i0 + wave, ch = c0 + lane;
+  const int nrow = c - c0 < 64 ? c - c0 : 64, span = nrow * hid;  // W2 rows c0 .. c0 + nrow - 1
+  constexpr int PER = 64 * SEL_MAXHID / 256;
+  float wl[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) wl[u] = tid + 256 * u < span ? w2[(int64_t)c0 * hid + tid + 256 * u] : 0.f;
+  const float hv = (wave < 4 && lane < hid && i < n) ? hbuf[(int64_t)i * hid + lane] : 0.f;
+  const float bc = (b2 && ch < c) ? b2[ch] : 0.f;
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const int e = tid + 256 * u;
+    if (e < span) {
+      const int r = e / hid;
+      ws[r * (hid + 1) + e - r * hid] = wl[u];
+    }
+  }
+  if (lane < hid) hs[wave * hid + lane] = hv;
+  __syncthreads();
+  if (ch >= c || i >= n) return;  // after the only barrier
+  const float* wr = ws + lane * (hid + 1);
+  const float* hi = hs + wave * hid;
+  float a0 = 0.f, a1 = 0.f;
+  for (int k = 0; k + 1 < hid; k += 2) {
+    a0 += wr[k] * hi[k];
+    a1 += wr[k + 1] * hi[k + 1];
+  }
+  if (hid & 1) a0 += wr[hid - 1] * hi[hid - 1];
+  att[(int64_t)i * c + ch] = sigmoidf_(a0 + a1 + bc);
+}
+
 extern "C" int kad_se_pool(const void* x, float* partial, int n, int c, int h, int w, int layout, int x_cs,
                            int dtype, void* stream) {
   KAD_CHECK_ARG(x && partial, "kad_se_pool: null pointer");
@@ -998,6 +1095,23 @@ extern "C" int kad_se_mlp(const float* partial, int tiles, float inv_count, cons
     hipLaunchKernelGGL(se_mlp_kernel<1024>, dim3(n), dim3(1024), lds, (hipStream_t)stream, partial, tiles, inv_count,
                        w1, b1, w2, b2, att, c, hid);
   return check_launch("kad_se_mlp");
+}
+
+extern "C" int kad_se_mlp_ws(const float* partial, int tiles, float inv_count, const float* w1, const float* b1,
+                             const float* w2, const float* b2, float* att, int n, int c, int hid, float* hidden,
+                             void* stream) {
+  KAD_CHECK_ARG(partial && w1 && w2 && att && hidden, "kad_se_mlp_ws: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && hid > 0 && tiles > 0, "kad_se_mlp_ws: bad shape");
+  if (c > SEL_MAXC || hid > SEL_MAXHID || n > 65535 * 4)
+    return kad_se_mlp(partial, tiles, inv_count, w1, b1, w2, b2, att, n, c, hid, stream);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(se_mlp_l1_kernel, dim3(ceil_div(hid, 4), ceil_div(n, 4)), dim3(256), 0, st, partial, tiles,
+                     inv_count, w1, b1, hidden, n, c, hid);
+  int rc = check_launch("kad_se_mlp_ws");
+  if (rc) return rc;
+  hipLaunchKernelGGL(se_mlp_l2_kernel, dim3(ceil_div(c, 64), ceil_div(n, 4)), dim3(256), 0, st,
+                     (const float*)hidden, w2, b2, att, n, c, hid);
+  return check_launch("kad_se_mlp_ws");
 }
 
 extern "C" int kad_channel_scale(const void* x, const float* att, void* out, int n, int c, int h, int w, int layout,

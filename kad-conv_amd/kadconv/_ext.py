@@ -135,6 +135,8 @@ SIGNATURES = {
     'kad_se_pool_tiles': (c_int, [c_int, c_int, c_int]),
     'kad_se_pool': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_se_mlp': (c_int, [c_vp, c_int, ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    'kad_se_mlp_ws': (c_int, [c_vp, c_int, ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp,
+                              c_vp]),
     'kad_channel_scale': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_to_nhwc': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_branch_merge': (c_int, [ctypes.POINTER(MergeArgs), c_vp]),
@@ -555,6 +557,14 @@ def se_mlp(partial, tiles, inv_count, w1, b1, w2, b2, att, n, c, hid):
     _need_gpu(partial, w1, b1, w2, b2, att)
     _check(load().kad_se_mlp(_ptr(partial), tiles, inv_count, _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(att),
                              n, c, hid, _stream()), 'kad_se_mlp')
+
+
+def se_mlp_ws(partial, tiles, inv_count, w1, b1, w2, b2, att, n, c, hid, hidden):
+    """kad_se_mlp_ws: the MLP spread over the batch, hidden [n][hid] fp32 as workspace."""
+    _need_gpu(partial, w1, b1, w2, b2, att, hidden)
+    assert hidden.dtype == torch.float32 and hidden.is_contiguous() and hidden.numel() >= n * hid
+    _check(load().kad_se_mlp_ws(_ptr(partial), tiles, inv_count, _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(att),
+                                n, c, hid, _ptr(hidden), _stream()), 'kad_se_mlp_ws')
 
 
 def channel_scale(x, att, out, c, layout):

@@ -176,7 +176,8 @@ def squeeze_excitation(x, w1, b1, w2, b2):
     partial = torch.empty(N, tiles, C, dtype=torch.float32, device=x.device)
     _ext.se_pool(xv, C, layout, partial)
     att = torch.empty(N, C, dtype=torch.float32, device=x.device)
-    _ext.se_mlp(partial, tiles, 1.0 / (H * W), f32(w1), f32(b1), f32(w2), f32(b2), att, N, C, hid)
+    hidden = torch.empty(N, hid, dtype=torch.float32, device=x.device)
+    _ext.se_mlp_ws(partial, tiles, 1.0 / (H * W), f32(w1), f32(b1), f32(w2), f32(b2), att, N, C, hid, hidden)
     if nhwc:
         out = torch.empty_like(x, memory_format=torch.channels_last)
         _ext.channel_scale(xv, att, out.permute(0, 2, 3, 1), C, layout)

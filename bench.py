@@ -121,6 +121,11 @@ def cpu_baseline(shape, runs=5, warmup=2):
                       f'(os.cpu_count={os.cpu_count()}, affinity={threads}, cpu="{_cpu_model()}")'}
 
 
+# KAD-CNet-S DSC(c, c) shapes at 800 x 800: c in {12, 10, 10} at {100, 50, 25}^2, {16, 16, 16} at
+# {50, 25, 12}^2, {22, 21, 21} at {25, 12, 6}^2
+KADCNET_DSC = [(12, 100), (10, 50), (10, 25), (16, 50), (16, 25), (16, 12), (22, 25), (21, 12), (21, 6)]
+
+
 def per_op_workloads():
     """The other BASELINE configs as (name, launch, floor_us) with seeded inputs and weights."""
     import kadconv
@@ -156,6 +161,16 @@ def per_op_workloads():
     m = kadconv.SqueezeExcitation(1024, reduction=16).to('cuda', dt).eval()
     x = torch.randn(16, 1024, 25, 25, generator=g).to('cuda', dt)
     out.append(('se_1024_25', lambda m=m, x=x: m(x), 40.96e6 / PEAK_HBM * 1e6))
+    # config 5's DSC(c, c) shapes (KAD-CNet-S, bs16 at 800 x 800), channels-last as in the network
+    for C, H in KADCNET_DSC:
+        d = kadconv.DSC(C, C)
+        d.load_state_dict(S.make_dsc_state(C, C, seed=C * 7 + H, offset_std_px=2.0), strict=False)
+        d = d.to('cuda', dt).eval()
+        kadconv.enable_fast_inference(d)
+        x = torch.randn(16, C, H, H, generator=g).to('cuda', dt).contiguous(memory_format=torch.channels_last)
+        fl = 16 * H * H * (2 * 9 * C * C + 2 * 9 * 18 * C + 2 * 9 * C + 44 * C)
+        by = 2 * 16 * C * H * H * 2 + 2 * (9 * C * C + 162 * C + 9 * C)
+        out.append((f'kadcnet_dsc_{C}x{H}', lambda d=d, x=x: d(x), max(fl / PEAK_MFMA_F16, by / PEAK_HBM) * 1e6))
     return out
 
 
@@ -204,6 +219,10 @@ def per_op_cpu():
     p = [t.detach() for t in (se[0].weight, se[0].bias, se[2].weight, se[2].bias)]
     x = torch.randn(16, 1024, 25, 25, generator=g)
     out['se_1024_25'] = _cpu_time(lambda: O.se_forward(x, *p)) * 1e6
+    for C, H in KADCNET_DSC:
+        sd = S.make_dsc_state(C, C, seed=C * 7 + H, offset_std_px=2.0)
+        x = torch.randn(16, C, H, H, generator=g)
+        out[f'kadcnet_dsc_{C}x{H}'] = _cpu_time(lambda sd=sd, x=x: O.dsc_forward(sd, '', x)) * 1e6
     return out
 
 

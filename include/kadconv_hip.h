@@ -342,6 +342,21 @@ int kad_se_mlp(const float *partial, int tiles, float inv_count, const float *w1
 int kad_se_mlp_ws(const float *partial, int tiles, float inv_count, const float *w1, const float *b1,
                   const float *w2, const float *b2, float *att, int n, int c, int hid, float *hidden, void *stream);
 
+/* Layer 1 of kad_se_mlp alone: hidden[n][hid] = relu(W1 (inv_count * sum_t partial[n][t]) + b1)
+ * (C <= 1024), one wave per (hidden unit, 4 images).  With kad_se_scale it splits the SE MLP at
+ * the hidden layer (kad_conv.py:105-109: Linear, ReLU | Linear, Sigmoid, then y *= att).  Same
+ * reference as kad_se_mlp (kadc_fused_sm75.py:1518-1542). */
+int kad_se_hidden(const float *partial, int tiles, float inv_count, const float *w1, const float *b1, float *hidden,
+                  int n, int c, int hid, void *stream);
+
+/* NCHW out = x * att, att[n][c] = sigmoid(W2[c] . hidden[n] + b2[c]) (also written to att):
+ * layer 2 of the SE MLP computed by the blocks of the channel scale for the planes they touch
+ * (planes of >= 64 pixels; otherwise a layer-2 launch, then kad_channel_scale; hid <= 64).
+ * Reference: the second Linear + Sigmoid of k_se_mlp (kadc_fused_sm75.py:1518-1542) and
+ * k_apply_tiled (:1203-1217). */
+int kad_se_scale(const void *x, const float *hidden, const float *w2, const float *b2, float *att, void *out, int n,
+                 int c, int h, int w, int hid, int dtype, void *stream);
+
 /* out = x * att[n][c] (NCHW, or NHWC with channel stride x_cs).
  * Reference k_apply_tiled (acceleration/kadc_fused_sm75.py:1203-1217). */
 int kad_channel_scale(const void *x, const float *att, void *out, int n, int c, int h, int w, int layout, int x_cs,

@@ -1020,6 +1020,65 @@ __global__ __launch_bounds__(256) void se_mlp_l2_kernel(const float* hbuf, const
   att[(int64_t)i * c + ch] = sigmoidf_(a0 + a1 + bc);
 }
 
+// ---- SE layer 2 fused into the channel scale (NCHW) ---------------------------------------------
+// out = x * sigmoid(W2[c] . h[n] + b2[c]): block b scales the flat elements [2048 b, 2048 b + 2048)
+// (one 16-byte piece per thread, loaded first) and computes the attention of the planes that range
+// touches (at most 2048 / hw + 2 <= 34), four threads per plane (16 hidden units each, every load
+// issued before the first product, shuffle-reduced), into LDS; att[n][c] is also written (planes
+// shared by two blocks get the same value twice).  hw >= 64, hid <= 64.
+constexpr int SS_ELEMS = 2048, SS_MINHW = 64, SS_MAXPL = SS_ELEMS / SS_MINHW + 2;
+
+template <typename T>
+__global__ __launch_bounds__(256) void se_scale_flat_kernel(const T* x, const float* hbuf, const float* w2,
+                                                           const float* b2, float* att, T* out, int64_t total, int hw,
+                                                           int c, int hid) {
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  __shared__ float s_att[SS_MAXPL];
+  const int tid = threadIdx.x;
+  const int64_t b0 = (int64_t)blockIdx.x * SS_ELEMS, e0 = b0 + 8 * tid;
+  t8 xv;
+  if (e0 < total) xv = *(const t8*)(x + e0);
+  const int64_t blast = (b0 + SS_ELEMS < total ? b0 + SS_ELEMS : total) - 1;
+  const int p_lo = (int)(b0 / hw), npl = (int)(blast / hw) - p_lo + 1;
+  const int pt = tid >> 2, q = tid & 3;
+  if (pt < npl) {  // 4 * npl <= 136 threads: whole quads, so the shuffles stay inside live lanes
+    const int p = p_lo + pt, n = p / c, ch = p - n * c;
+    const float* wr = w2 + (int64_t)ch * hid + 16 * q;
+    const float* hr = hbuf + (int64_t)n * hid + 16 * q;
+    float wv[16], hv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const bool ok = 16 * q + j < hid;
+      wv[j] = ok ? wr[j] : 0.f;
+      hv[j] = ok ? hr[j] : 0.f;
+    }
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      a0 += wv[j] * hv[j];
+      a1 += wv[j + 1] * hv[j + 1];
+    }
+    float a = a0 + a1;
+    a += __shfl_xor(a, 1);
+    a += __shfl_xor(a, 2);
+    if (q == 0) {
+      const float v = sigmoidf_(a + (b2 ? b2[ch] : 0.f));
+      s_att[pt] = v;
+      att[p] = v;
+    }
+  }
+  __syncthreads();
+  if (e0 >= total) return;  // after the only barrier
+  const int pe = (int)(e0 / hw);
+  const int64_t off = e0 - (int64_t)pe * hw;          // position of the piece in plane pe
+  const int n0 = (int)(hw - off < 8 ? hw - off : 8);  // elements of the piece in plane pe
+  const float s0 = s_att[pe - p_lo], s1 = n0 < 8 ? s_att[pe + 1 - p_lo] : s0;
+  t8 o;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) o[k] = from_f32<T>(to_f32(xv[k]) * (k < n0 ? s0 : s1));
+  *(t8*)(out + e0) = o;
+}
+
 extern "C" int kad_se_pool(const void* x, float* partial, int n, int c, int h, int w, int layout, int x_cs,
                            int dtype, void* stream) {
   KAD_CHECK_ARG(x && partial, "kad_se_pool: null pointer");
@@ -1112,6 +1171,43 @@ extern "C" int kad_se_mlp_ws(const float* partial, int tiles, float inv_count, c
   hipLaunchKernelGGL(se_mlp_l2_kernel, dim3(ceil_div(c, 64), ceil_div(n, 4)), dim3(256), 0, st,
                      (const float*)hidden, w2, b2, att, n, c, hid);
   return check_launch("kad_se_mlp_ws");
+}
+
+extern "C" int kad_se_hidden(const float* partial, int tiles, float inv_count, const float* w1, const float* b1,
+                             float* hidden, int n, int c, int hid, void* stream) {
+  KAD_CHECK_ARG(partial && w1 && hidden, "kad_se_hidden: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && hid > 0 && tiles > 0, "kad_se_hidden: bad shape");
+  KAD_CHECK_ARG(c <= SEL_MAXC && n <= 65535 * 4, "kad_se_hidden: C = %d above %d", c, SEL_MAXC);
+  hipLaunchKernelGGL(se_mlp_l1_kernel, dim3(ceil_div(hid, 4), ceil_div(n, 4)), dim3(256), 0, (hipStream_t)stream,
+                     partial, tiles, inv_count, w1, b1, hidden, n, c, hid);
+  return check_launch("kad_se_hidden");
+}
+
+extern "C" int kad_se_scale(const void* x, const float* hidden, const float* w2, const float* b2, float* att,
+                            void* out, int n, int c, int h, int w, int hid, int dtype, void* stream) {
+  KAD_CHECK_ARG(x && hidden && w2 && att && out, "kad_se_scale: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0 && hid > 0, "kad_se_scale: bad shape");
+  const int64_t total = (int64_t)n * c * h * w;
+  const int vb = 8 * dtype_size(dtype);
+  hipStream_t st = (hipStream_t)stream;
+  if (h * w >= SS_MINHW && hid <= SEL_MAXHID && total % 8 == 0 && total / SS_ELEMS < (1ll << 31) &&
+      (uintptr_t)x % vb == 0 && (uintptr_t)out % vb == 0) {
+    const dim3 grid((unsigned)((total + SS_ELEMS - 1) / SS_ELEMS));
+    switch (dtype) {
+      case KAD_F32: hipLaunchKernelGGL(se_scale_flat_kernel<float>, grid, dim3(256), 0, st, (const float*)x, hidden, w2, b2, att, (float*)out, total, h * w, c, hid); break;
+      case KAD_F16: hipLaunchKernelGGL(se_scale_flat_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, hidden, w2, b2, att, (half_t*)out, total, h * w, c, hid); break;
+      case KAD_BF16: hipLaunchKernelGGL(se_scale_flat_kernel<bf16_t>, grid, dim3(256), 0, st, (const bf16_t*)x, hidden, w2, b2, att, (bf16_t*)out, total, h * w, c, hid); break;
+      default: return fail(KAD_EINVAL, "kad_se_scale: unknown dtype %d", dtype);
+    }
+    return check_launch("kad_se_scale");
+  }
+  // small planes or unaligned tensors: att by the layer-2 kernel, then the plain channel scale
+  KAD_CHECK_ARG(hid <= SEL_MAXHID, "kad_se_scale: hidden width %d above %d", hid, SEL_MAXHID);
+  hipLaunchKernelGGL(se_mlp_l2_kernel, dim3(ceil_div(c, 64), ceil_div(n, 4)), dim3(256), 0, st, hidden, w2, b2, att, n,
+                     c, hid);
+  int rc = check_launch("kad_se_scale");
+  if (rc) return rc;
+  return kad_channel_scale(x, att, out, n, c, h, w, KAD_NCHW, c, dtype, stream);
 }
 
 extern "C" int kad_channel_scale(const void* x, const float* att, void* out, int n, int c, int h, int w, int layout,

@@ -137,6 +137,8 @@ SIGNATURES = {
     'kad_se_mlp': (c_int, [c_vp, c_int, ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
     'kad_se_mlp_ws': (c_int, [c_vp, c_int, ctypes.c_float, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp,
                               c_vp]),
+    'kad_se_hidden': (c_int, [c_vp, c_int, ctypes.c_float, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp]),
+    'kad_se_scale': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_channel_scale': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_to_nhwc': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_branch_merge': (c_int, [ctypes.POINTER(MergeArgs), c_vp]),
@@ -565,6 +567,24 @@ def se_mlp_ws(partial, tiles, inv_count, w1, b1, w2, b2, att, n, c, hid, hidden)
     assert hidden.dtype == torch.float32 and hidden.is_contiguous() and hidden.numel() >= n * hid
     _check(load().kad_se_mlp_ws(_ptr(partial), tiles, inv_count, _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(att),
                                 n, c, hid, _ptr(hidden), _stream()), 'kad_se_mlp_ws')
+
+
+def se_hidden(partial, tiles, inv_count, w1, b1, hidden, n, c, hid):
+    """kad_se_hidden: hidden [n][hid] = relu(W1 g + b1) from the GAP partials."""
+    _need_gpu(partial, w1, b1, hidden)
+    assert hidden.dtype == torch.float32 and hidden.is_contiguous() and hidden.numel() >= n * hid
+    _check(load().kad_se_hidden(_ptr(partial), tiles, inv_count, _ptr(w1), _ptr(b1), _ptr(hidden), n, c, hid,
+                                _stream()), 'kad_se_hidden')
+
+
+def se_scale(x, hidden, w2, b2, att, out, hid):
+    """kad_se_scale: NCHW out = x * sigmoid(W2 hidden + b2) (att written too)."""
+    _need_gpu(x, hidden, w2, b2, att, out)
+    N, C, H, W = x.shape
+    assert x.is_contiguous() and out.is_contiguous() and out.dtype == x.dtype
+    assert att.dtype == torch.float32 and att.is_contiguous() and att.numel() >= N * C
+    _check(load().kad_se_scale(_ptr(x), _ptr(hidden), _ptr(w2), _ptr(b2), _ptr(att), _ptr(out), N, C, H, W, hid,
+                               kad_dtype(x.dtype), _stream()), 'kad_se_scale')
 
 
 def channel_scale(x, att, out, c, layout):

@@ -177,6 +177,12 @@ def squeeze_excitation(x, w1, b1, w2, b2):
     _ext.se_pool(xv, C, layout, partial)
     att = torch.empty(N, C, dtype=torch.float32, device=x.device)
     hidden = torch.empty(N, hid, dtype=torch.float32, device=x.device)
+    if not nhwc and C <= 1024 and hid <= 64:
+        # hidden layer, then layer 2 inside the channel scale (one launch fewer)
+        _ext.se_hidden(partial, tiles, 1.0 / (H * W), f32(w1), f32(b1), hidden, N, C, hid)
+        out = torch.empty_like(xv)
+        _ext.se_scale(xv, hidden, f32(w2), f32(b2), att, out, hid)
+        return out
     _ext.se_mlp_ws(partial, tiles, 1.0 / (H * W), f32(w1), f32(b1), f32(w2), f32(b2), att, N, C, hid, hidden)
     if nhwc:
         out = torch.empty_like(x, memory_format=torch.channels_last)

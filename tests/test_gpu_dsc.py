@@ -120,6 +120,26 @@ def test_dsc_two_blocks_per_cu(dt, shape, off_std, layout):
     check_close(got, _ref(x, ow, ob, w, b, mask, dtype), dtype, f'{dt} {shape} off_std={off_std}')
 
 
+# KAD-CNet-S at 800 x 800: the DSC(c, c) shapes of its 42 KADC4 layers,
+# c in {12, 10, 10} at {100, 50, 25}^2, {16, 16, 16} at {50, 25, 12}^2, {22, 21, 21} at {25, 12, 6}^2
+KADCNET_DSC = [(12, 100), (10, 50), (10, 25), (16, 50), (16, 25), (16, 12), (22, 25), (21, 12), (21, 6)]
+
+
+@pytest.mark.parametrize('dt', ['f16', 'f32'])
+@pytest.mark.parametrize('C,H', KADCNET_DSC)
+def test_dsc_kadcnet_shapes(dt, C, H):
+    """Every small-channel DSC shape of KAD-CNet-S, batch 16, channels-last output (the
+    network's layout), offsets ~N(0, 2) px: the fp16 launches with >= 384 tile blocks run on
+    the two-blocks-per-CU kernel, the others on the general one."""
+    dtype = DT[dt]
+    x, ow, ob, w, b = _inputs(16, C, C, H, H, seed=C * 7 + H)
+    mask = _mask(16, H, H, seed=C + H)
+    print(f'dsc_kadcnet dt={dt} C={C} H={H}', flush=True)
+    got = _run_dsc(x, ow, ob, w, b, mask, dtype, out_layout='nhwc')
+    torch.cuda.synchronize()
+    check_close(got, _ref(x, ow, ob, w, b, mask, dtype), dtype, f'{dt} C={C} H={H}')
+
+
 @pytest.mark.parametrize('dt', ['f16', 'bf16'])
 def test_dsc_two_blocks_per_cu_gap(dt):
     """GAP partials of the two-blocks-per-CU kernel: fp32 sums of the rounded outputs."""
@@ -182,7 +202,9 @@ def test_dsc_far_offsets(dt):
 
 @pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
 @pytest.mark.parametrize('shape,stride', [((2, 86, 18, 100, 100), 1), ((1, 40, 130, 13, 7), 1),
-                                          ((2, 24, 18, 15, 12), 2), ((1, 8, 3, 5, 64), 2)])
+                                          ((2, 24, 18, 15, 12), 2), ((1, 8, 3, 5, 64), 2),
+                                          ((1, 130, 18, 9, 200), 1), ((3, 8, 18, 25, 25), 1),
+                                          ((1, 3, 18, 6, 6), 1), ((2, 256, 18, 50, 50), 1)])
 def test_conv3x3(dt, shape, stride):
     """kad_conv3x3_fwd (fp32 output, NHWC and NCHW) against F.conv2d in float64."""
     from kadconv import _ext

@@ -259,6 +259,15 @@ int kad_axial_sums(const void *x, float *rows, float *cols, int n, int c, int h,
  * standalone DSC reads its NCHW input here instead of the NHWC copy. */
 int kad_axial_sums_nchw(const void *x, float *rows, float *cols, int n, int c, int h, int w, int dtype, void *stream);
 
+/* kad_axial_sums / kad_axial_sums_nchw followed by kad_lcsa_prep of that one slice, in one
+ * launch: arow[N][H][C] = row means and colm[N][W][C] = column means (each sum times 1 / W or
+ * 1 / H, the same product kad_lcsa_prep forms; bit-identical).  LCSA's pool_h / pool_w
+ * (kad_conv.py:26-27) for a standalone DSC, whose input has no pyramid partial sums. */
+int kad_axial_means(const void *x, float *arow, float *colm, int n, int c, int h, int w, int x_cs, int dtype,
+                    void *stream);
+int kad_axial_means_nchw(const void *x, float *arow, float *colm, int n, int c, int h, int w, int dtype,
+                         void *stream);
+
 /* E[j][k][c] = w4[j][c] * w3[c][k] (j < 9, else 0) and ebias[16] = b4 + w4 . b3:
  * the 11x1 depthwise conv and the 1x1 projection of LCSA (kad_conv.py:33-35)
  * fused into one matrix.  emat_dtype KAD_F16 (fp16/bf16 runs) or KAD_F32. */

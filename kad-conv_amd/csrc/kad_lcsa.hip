@@ -31,9 +31,11 @@ constexpr int HALF_BAND = 5;
 // ---- axial sums of an NHWC map ---------------------------------------------------------------
 // grid.x = H + W lines, grid.y = N.  Line l < H is row l (sum over w);
 // otherwise column l - H (sum over h).  Threads stride over channels.
+// Each sum is multiplied by rsc (rows) / csc (columns) before it is stored: 1 for sums, 1 / W and
+// 1 / H for the means kad_lcsa_mask reads (the same product kad_lcsa_prep forms from one slice).
 template <typename T>
 __global__ __launch_bounds__(256) void axial_sums_kernel(const T* x, float* rows, float* cols, int c, int h, int w,
-                                                        int cs) {
+                                                        int cs, float rsc, float csc) {
   const int n = blockIdx.y;
   const int l = blockIdx.x;
   const T* base = x + (int64_t)n * h * w * cs;
@@ -42,7 +44,7 @@ __global__ __launch_bounds__(256) void axial_sums_kernel(const T* x, float* rows
       float acc = 0.f;
       const T* p = base + (int64_t)l * w * cs + ch;
       for (int j = 0; j < w; ++j) acc += to_f32(p[(int64_t)j * cs]);
-      rows[((int64_t)n * h + l) * c + ch] = acc;
+      rows[((int64_t)n * h + l) * c + ch] = acc * rsc;
     }
   } else {
     const int col = l - h;
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(256) void axial_sums_kernel(const T* x, float* rows
       float acc = 0.f;
       const T* p = base + (int64_t)col * cs + ch;
       for (int i = 0; i < h; ++i) acc += to_f32(p[(int64_t)i * w * cs]);
-      cols[((int64_t)n * w + col) * c + ch] = acc;
+      cols[((int64_t)n * w + col) * c + ch] = acc * csc;
     }
   }
 }
@@ -64,7 +66,7 @@ constexpr int AX_MAX_PX = 12288;
 
 template <typename T>
 __global__ __launch_bounds__(256) void axial_sums_nchw_kernel(const T* x, float* rows, float* cols, int c, int h,
-                                                             int w) {
+                                                             int w, float rsc, float csc) {
   extern __shared__ float pl[];  // [h][w + 1]
   const int plane = blockIdx.x, n = plane / c, ch = plane - n * c;
   const int P = h * w, ws = w + 1;
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256) void axial_sums_nchw_kernel(const T* x, float*
         a1 += r[j + 1];
       }
       if (j < w) a0 += r[j];
-      rows[((int64_t)n * h + i) * c + ch] = a0 + a1;
+      rows[((int64_t)n * h + i) * c + ch] = (a0 + a1) * rsc;
     } else {
       const int xx = i - h;
       int j = 0;
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(256) void axial_sums_nchw_kernel(const T* x, float*
         a1 += pl[(j + 1) * ws + xx];
       }
       if (j < h) a0 += pl[j * ws + xx];
-      cols[((int64_t)n * w + xx) * c + ch] = a0 + a1;
+      cols[((int64_t)n * w + xx) * c + ch] = (a0 + a1) * csc;
     }
   }
 }
@@ -480,38 +482,62 @@ extern "C" int64_t kad_lcsa_params_elems(int c) { return c > 0 ? 35 * (int64_t)c
 
 extern "C" int64_t kad_lcsa_emat_elems(int c) { return c > 0 ? (int64_t)16 * BAND * round_up(c, 32) : 0; }
 
+namespace kad {
+static int launch_axial_nhwc(const void* x, float* rows, float* cols, int n, int c, int h, int w, int x_cs,
+                             int dtype, float rsc, float csc, hipStream_t st, const char* who) {
+  KAD_CHECK_ARG(x && rows && cols, "%s: null pointer", who);
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0 && x_cs >= c, "%s: bad shape", who);
+  dim3 grid(h + w, n);
+  switch (dtype) {
+    case KAD_F32: hipLaunchKernelGGL(axial_sums_kernel<float>, grid, dim3(256), 0, st, (const float*)x, rows, cols, c, h, w, x_cs, rsc, csc); break;
+    case KAD_F16: hipLaunchKernelGGL(axial_sums_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, rows, cols, c, h, w, x_cs, rsc, csc); break;
+    case KAD_BF16: hipLaunchKernelGGL(axial_sums_kernel<bf16_t>, grid, dim3(256), 0, st, (const bf16_t*)x, rows, cols, c, h, w, x_cs, rsc, csc); break;
+    default: return fail(KAD_EINVAL, "%s: unknown dtype %d", who, dtype);
+  }
+  return check_launch(who);
+}
+
+static int launch_axial_nchw(const void* x, float* rows, float* cols, int n, int c, int h, int w, int dtype,
+                             float rsc, float csc, hipStream_t st, const char* who) {
+  KAD_CHECK_ARG(x && rows && cols, "%s: null pointer", who);
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0, "%s: bad shape", who);
+  KAD_CHECK_ARG((int64_t)h * w <= AX_MAX_PX, "%s: %dx%d plane exceeds %d pixels", who, h, w, AX_MAX_PX);
+  KAD_CHECK_ARG((int64_t)n * c < (1ll << 31), "%s: too many planes", who);
+  KAD_CHECK_ARG(((uintptr_t)x) % (4 * dtype_size(dtype)) == 0, "%s: x must be aligned to 4 elements", who);
+  const size_t lds = (size_t)h * (w + 1) * sizeof(float);
+  const dim3 grid(n * c);
+  switch (dtype) {
+    case KAD_F32: allow_lds(axial_sums_nchw_kernel<float>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<float>, grid, dim3(256), lds, st, (const float*)x, rows, cols, c, h, w, rsc, csc); break;
+    case KAD_F16: allow_lds(axial_sums_nchw_kernel<half_t>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<half_t>, grid, dim3(256), lds, st, (const half_t*)x, rows, cols, c, h, w, rsc, csc); break;
+    case KAD_BF16: allow_lds(axial_sums_nchw_kernel<bf16_t>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<bf16_t>, grid, dim3(256), lds, st, (const bf16_t*)x, rows, cols, c, h, w, rsc, csc); break;
+    default: return fail(KAD_EINVAL, "%s: unknown dtype %d", who, dtype);
+  }
+  return check_launch(who);
+}
+}  // namespace kad
+
 extern "C" int kad_axial_sums(const void* x, float* rows, float* cols, int n, int c, int h, int w, int x_cs,
                               int dtype, void* stream) {
-  KAD_CHECK_ARG(x && rows && cols, "kad_axial_sums: null pointer");
-  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0 && x_cs >= c, "kad_axial_sums: bad shape");
-  dim3 grid(h + w, n);
-  hipStream_t st = (hipStream_t)stream;
-  switch (dtype) {
-    case KAD_F32: hipLaunchKernelGGL(axial_sums_kernel<float>, grid, dim3(256), 0, st, (const float*)x, rows, cols, c, h, w, x_cs); break;
-    case KAD_F16: hipLaunchKernelGGL(axial_sums_kernel<half_t>, grid, dim3(256), 0, st, (const half_t*)x, rows, cols, c, h, w, x_cs); break;
-    case KAD_BF16: hipLaunchKernelGGL(axial_sums_kernel<bf16_t>, grid, dim3(256), 0, st, (const bf16_t*)x, rows, cols, c, h, w, x_cs); break;
-    default: return fail(KAD_EINVAL, "kad_axial_sums: unknown dtype %d", dtype);
-  }
-  return check_launch("kad_axial_sums");
+  return launch_axial_nhwc(x, rows, cols, n, c, h, w, x_cs, dtype, 1.f, 1.f, (hipStream_t)stream, "kad_axial_sums");
 }
 
 extern "C" int kad_axial_sums_nchw(const void* x, float* rows, float* cols, int n, int c, int h, int w, int dtype,
                                    void* stream) {
-  KAD_CHECK_ARG(x && rows && cols, "kad_axial_sums_nchw: null pointer");
-  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0, "kad_axial_sums_nchw: bad shape");
-  KAD_CHECK_ARG((int64_t)h * w <= AX_MAX_PX, "kad_axial_sums_nchw: %dx%d plane exceeds %d pixels", h, w, AX_MAX_PX);
-  KAD_CHECK_ARG((int64_t)n * c < (1ll << 31), "kad_axial_sums_nchw: too many planes");
-  KAD_CHECK_ARG(((uintptr_t)x) % (4 * dtype_size(dtype)) == 0, "kad_axial_sums_nchw: x must be aligned to 4 elements");
-  const size_t lds = (size_t)h * (w + 1) * sizeof(float);
-  const dim3 grid(n * c);
-  hipStream_t st = (hipStream_t)stream;
-  switch (dtype) {
-    case KAD_F32: allow_lds(axial_sums_nchw_kernel<float>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<float>, grid, dim3(256), lds, st, (const float*)x, rows, cols, c, h, w); break;
-    case KAD_F16: allow_lds(axial_sums_nchw_kernel<half_t>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<half_t>, grid, dim3(256), lds, st, (const half_t*)x, rows, cols, c, h, w); break;
-    case KAD_BF16: allow_lds(axial_sums_nchw_kernel<bf16_t>, lds); hipLaunchKernelGGL(axial_sums_nchw_kernel<bf16_t>, grid, dim3(256), lds, st, (const bf16_t*)x, rows, cols, c, h, w); break;
-    default: return fail(KAD_EINVAL, "kad_axial_sums_nchw: unknown dtype %d", dtype);
-  }
-  return check_launch("kad_axial_sums_nchw");
+  return launch_axial_nchw(x, rows, cols, n, c, h, w, dtype, 1.f, 1.f, (hipStream_t)stream, "kad_axial_sums_nchw");
+}
+
+extern "C" int kad_axial_means(const void* x, float* arow, float* colm, int n, int c, int h, int w, int x_cs,
+                               int dtype, void* stream) {
+  if (h <= 0 || w <= 0) return fail(KAD_EINVAL, "kad_axial_means: bad shape");
+  return launch_axial_nhwc(x, arow, colm, n, c, h, w, x_cs, dtype, 1.f / (float)w, 1.f / (float)h,
+                           (hipStream_t)stream, "kad_axial_means");
+}
+
+extern "C" int kad_axial_means_nchw(const void* x, float* arow, float* colm, int n, int c, int h, int w, int dtype,
+                                    void* stream) {
+  if (h <= 0 || w <= 0) return fail(KAD_EINVAL, "kad_axial_means_nchw: bad shape");
+  return launch_axial_nchw(x, arow, colm, n, c, h, w, dtype, 1.f / (float)w, 1.f / (float)h, (hipStream_t)stream,
+                           "kad_axial_means_nchw");
 }
 
 extern "C" int kad_lcsa_pack(const float* params, void* emat, float* ebias, int c, int emat_dtype, void* stream) {

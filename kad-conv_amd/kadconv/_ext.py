@@ -125,6 +125,8 @@ SIGNATURES = {
     'kad_lcsa_emat_elems': (c_i64, [c_int]),
     'kad_axial_sums': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_axial_sums_nchw': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_axial_means': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_axial_means_nchw': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_lcsa_pack': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_vp]),
     'kad_lcsa_prep': (c_int, [c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp]),
     'kad_lcsa_mask': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_vp]),
@@ -508,6 +510,24 @@ def axial_sums_nchw(x, rows, cols):
         raise ValueError('axial_sums_nchw: x must be contiguous NCHW')
     _check(load().kad_axial_sums_nchw(_ptr(x), _ptr(rows), _ptr(cols), N, C, H, W, kad_dtype(x.dtype), _stream()),
            'kad_axial_sums_nchw')
+
+
+def axial_means(x_nhwc, c, arow, colm):
+    """Row / column means of an NHWC map straight into LCSA's arow / colm (no partial slices)."""
+    _need_gpu(x_nhwc, arow, colm)
+    N, H, W, cs = x_nhwc.shape
+    _check(load().kad_axial_means(_ptr(x_nhwc), _ptr(arow), _ptr(colm), N, c, H, W, cs, kad_dtype(x_nhwc.dtype),
+                                  _stream()), 'kad_axial_means')
+
+
+def axial_means_nchw(x, arow, colm):
+    """Row / column means of a contiguous NCHW map (planes of at most AXIAL_NCHW_MAX_PX pixels)."""
+    _need_gpu(x, arow, colm)
+    N, C, H, W = x.shape
+    if not x.is_contiguous():
+        raise ValueError('axial_means_nchw: x must be contiguous NCHW')
+    _check(load().kad_axial_means_nchw(_ptr(x), _ptr(arow), _ptr(colm), N, C, H, W, kad_dtype(x.dtype), _stream()),
+           'kad_axial_means_nchw')
 
 
 def lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, c, h, w):

@@ -110,26 +110,26 @@ class DSCPlan:
         st = []
         mask = None
         if self.use_mask:
-            if sums is None:
-                rows = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
-                cols = torch.empty(n, w, self.cin, dtype=torch.float32, device=dev)
-                nrp = ncp = 1
-                if x_nchw is not None and h * w <= _ext.AXIAL_NCHW_MAX_PX and x_nchw.data_ptr() % 16 == 0:
-                    # the NCHW input itself: contiguous planes, one block each
-                    st.append(('axial_sums' + tag, lambda: _ext.axial_sums_nchw(x_nchw, rows, cols)))
-                else:
-                    st.append(('axial_sums' + tag, lambda: _ext.axial_sums(y, self.cin, rows, cols)))
-            else:
-                rows, nrp, cols, ncp = sums
             arow = torch.empty(n, h, self.cin, dtype=torch.float32, device=dev)
             colm = torch.empty(n, w, self.cin, dtype=torch.float32, device=dev)
+            if sums is None:
+                # no partial slices to reduce: the axial means in one launch (sums + prep)
+                if x_nchw is not None and h * w <= _ext.AXIAL_NCHW_MAX_PX and x_nchw.data_ptr() % 16 == 0:
+                    # the NCHW input itself: contiguous planes, one block each
+                    st.append(('axial_means' + tag, lambda: _ext.axial_means_nchw(x_nchw, arow, colm)))
+                else:
+                    st.append(('axial_means' + tag, lambda: _ext.axial_means(y, self.cin, arow, colm)))
+            else:
+                rows, nrp, cols, ncp = sums
             mask = torch.empty(n, h, w, 9, dtype=torch.float32, device=dev)
             # split the mask's channel contraction over blocks when the image has few tiles (standalone
             # DSC); KADConv's coarse branches run beside the full-resolution chain and stay unsplit
             ks = _ext.lcsa_mask_splits(n, self.cin, h, w) if mask_split else 1
             work = torch.empty(_ext.lcsa_mask_work_elems(n, h, w, ks), dtype=torch.float32, device=dev) \
                 if ks > 1 else None
-            st.append(('lcsa_prep' + tag, lambda: _ext.lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, self.cin, h, w)))
+            if sums is not None:
+                st.append(('lcsa_prep' + tag, lambda: _ext.lcsa_prep(rows, nrp, cols, ncp, arow, colm, n, self.cin,
+                                                                     h, w)))
             st.append(('lcsa_mask' + tag, lambda: _ext.lcsa_mask(arow, colm, self.lcsa, emat, ebias, mask, n,
                                                                  self.cin, h, w, ks, work)))
         b = self.bias if bias is None else bias

@@ -170,3 +170,18 @@ def test_oracle_nms_matches_pairwise_definition():
         else:
             assert any(iou(boxes[i], boxes[j]) > 0.45 and rank[j] < rank[i] for j in kept)
     assert [rank[i] for i in kept] == sorted(rank[i] for i in kept)
+
+
+def test_kadc4_state_dict_loads_into_kadconv():
+    """Checkpoint interop (KAD-Conv/README.md:39-55): a KAD-CNet KADC4_m layer's state dict
+    loads strictly into kadconv.KADConv of the same width and hidden size, and both modules
+    then compute the same plain forward."""
+    import kadconv
+    from kadcnet.kadc import KADC4_m
+    torch.manual_seed(3)
+    src = KADC4_m(48).eval()
+    dst = kadconv.KADConv(48, se_min_hidden=64).eval()
+    assert dst.load_state_dict(src.state_dict(), strict=True).missing_keys == []
+    x = torch.randn(1, 48, 12, 10, generator=torch.Generator().manual_seed(4))
+    with torch.no_grad():
+        assert torch.equal(src(x), dst(x))

@@ -39,6 +39,14 @@ def _f32(t):
     return None if t is None else t.detach().to(torch.float32).contiguous()
 
 
+def _emat_dtype(dtype):
+    """Precision of the LCSA mask GEMM (E matrix and strip activation u) for a run in `dtype`:
+    fp16 for fp16 runs (packed-fp16 u, fp16 MFMA); fp32 for fp32 and bf16 runs, whose
+    activations may exceed fp16's range (65504), where an fp16 u would turn the mask to NaN.
+    The mask reads fp32 means whatever the input dtype, so bf16 loses nothing by this."""
+    return torch.float16 if dtype == torch.float16 else torch.float32
+
+
 def _fold_bn(bn):
     a = bn.weight.detach().double() / torch.sqrt(bn.running_var.detach().double() + bn.eps)
     b = bn.bias.detach().double() - bn.running_mean.detach().double() * a
@@ -81,12 +89,11 @@ class DSCPlan:
 
     def packed(self, dtype):
         """(DCN weights, offset-conv weights, LCSA E matrix, LCSA bias) for `dtype`;
-        the LCSA matrix is fp16 for fp16/bf16 runs and fp32 for fp32 runs."""
+        the LCSA matrix is fp16 for fp16 runs and fp32 otherwise (see _emat_dtype)."""
         if dtype not in self._packed:
             emat = ebias = None
             if self.use_mask:
-                emat, ebias = _ext.lcsa_pack(self.lcsa, self.cin,
-                                             torch.float32 if dtype == torch.float32 else torch.float16)
+                emat, ebias = _ext.lcsa_pack(self.lcsa, self.cin, _emat_dtype(dtype))
             self._packed[dtype] = (_ext.dcn_pack_weights(self.weight, dtype),
                                    _ext.dcn_pack_weights(self.off_w, dtype), emat, ebias)
         return self._packed[dtype]
@@ -263,7 +270,7 @@ class KADConvPlan:
         xin, in_layout, out, out_v, out_layout = self._io(x)
         ntx, nty = _ext.pyramid_tiles(H, W)
         pyr, lcsa, dcn, keep, merges = [], [], {}, [], []
-        edt = torch.float32 if dtype == torch.float32 else torch.float16
+        edt = _emat_dtype(dtype)
         st = []
         for i, br in enumerate(self.branches):
             h, w = H >> i, W >> i

@@ -22,7 +22,7 @@ from oracle import kadconv_oracle as O
 pytestmark = pytest.mark.gpu
 
 DT = {'f32': torch.float32, 'f16': torch.float16, 'bf16': torch.bfloat16}
-TOL = {'f32': 1e-5, 'f16': 2e-3, 'bf16': 2e-3}
+TOL = {'f32': 1e-5, 'f16': 2e-3, 'bf16': 1e-5}  # bf16 runs form the mask GEMM in fp32 (fused._emat_dtype)
 
 
 def _wide_bn(sd, c, seed):
@@ -74,3 +74,37 @@ def test_lcsa_mask_matches_oracle(dt, n, c, h, w, split):
     err = (got - ref).abs().max().item()
     print(f'  max|d| = {err:.3e} (ksplit={ks})', flush=True)
     assert err <= TOL[dt], f'mask max|d| = {err:.3e} > {TOL[dt]}'
+
+
+def test_lcsa_mask_bf16_beyond_fp16_range():
+    """A bf16 map whose axial means exceed fp16's 65504: the mask GEMM of a bf16 run is fp32, so
+    the mask stays finite (an fp16 strip activation would be inf and the mask NaN) and matches
+    the oracle.  Tolerance 2e-3: most logits are saturated, and the fp32 sums of terms of
+    ~1e5 leave ~1e-3 on the few logits near 0 (sigmoid slope <= 1/4)."""
+    import kadconv
+    from kadconv import _ext
+    from kadconv.fused import DSCPlan
+    dtype, dev = torch.bfloat16, 'cuda'
+    n, c, h, w = 2, 86, 30, 30
+    d = kadconv.DSC(c, c)
+    d.load_state_dict(_wide_bn(S.make_dsc_state(c, c, seed=5), c, seed=6), strict=False)
+    d = d.to(dev, dtype).eval()
+    plan = DSCPlan(d)
+    _, _, emat, ebias = plan.packed(dtype)
+    assert emat.dtype == torch.float32
+    x = (torch.randn(n, c, h, w, generator=torch.Generator().manual_seed(7)) * 1e5).to(dtype)
+    y = torch.zeros(n, h, w, 88, dtype=dtype)
+    y[..., :c] = x.permute(0, 2, 3, 1)
+    y = y.to(dev)
+    arow = torch.empty(n, h, c, device=dev)
+    colm = torch.empty(n, w, c, device=dev)
+    mask = torch.full((n, h, w, 9), float('nan'), device=dev)
+    _ext.axial_means(y, c, arow, colm)
+    _ext.lcsa_mask(arow, colm, plan.lcsa, emat, ebias, mask, n, c, h, w, 1, None)
+    torch.cuda.synchronize()
+    sd = {k: v.detach().double().cpu() for k, v in d.state_dict().items()}
+    ref = torch.sigmoid(O.lcsa_forward(sd, 'RCA_mask.', x.double())).permute(0, 2, 3, 1)
+    got = mask.cpu().double()
+    assert x.double().mean(3).abs().max().item() > 65504
+    assert torch.isfinite(got).all()
+    assert (got - ref).abs().max().item() <= 2e-3

@@ -111,6 +111,10 @@ inline void allow_lds(F* kernel, size_t bytes) {
     (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
 }
 
+// kad_conv_fwd's 16-bit NHWC-output path (kad_conv3.hip): returns 1 when the launch is not one it
+// handles (the caller then runs its general path), else 0 or a KAD_E* code.
+int convolution_igemm(const kad_dcn_args& a, int ho, int wo, hipStream_t st);
+
 inline int dtype_size(int dtype) {
   return dtype == KAD_F32 ? 4 : 2;
 }

@@ -56,6 +56,7 @@
 // layout (lane -> column lane & 15, rows 4 * (lane >> 4) + i) is the MFMA
 // output layout.
 #include <mutex>
+#include <type_traits>
 
 #include "kad_common.h"
 
@@ -1102,27 +1103,35 @@ __device__ __forceinline__ void dcn_block(const kad_dcn_args& a, const DcnGeom& 
       pix_ok[m][i] = pl < npx && ty0 + oyl < g.ho && tx0 + pl - oyl * g.tw < g.wo;
     }
   float gsum[NBF];
+  // the activation as a template argument: a per-value branch would put every value's chain in a
+  // basic block of its own, and the scheduler could not interleave the independent chains
+  auto epilogue = [&](auto act) {
+    constexpr int ACT = decltype(act)::value;
 #pragma unroll
-  for (int b = 0; b < NBF; ++b) {
-    gsum[b] = 0.f;
-    const int col = b * 16 + row;
-    const bool co_ok = co0 + col < a.cout;
-    const float shift = s_par[0][col], mul = s_par[1][col], scl = s_par[3][col];
+    for (int b = 0; b < NBF; ++b) {
+      gsum[b] = 0.f;
+      const int col = b * 16 + row;
+      const bool co_ok = co0 + col < a.cout;
+      const float shift = s_par[0][col], mul = s_par[1][col], scl = s_par[3][col];
 #pragma unroll
-    for (int m = 0; m < DCN_WM; ++m) {
+      for (int m = 0; m < DCN_WM; ++m) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pl = wave * (16 * DCN_WM) + m * 16 + grp * 4 + i;
-        float v = fmaf(acc[m][b][i], mul, shift);
-        if (a.relu == KAD_ACT_SILU) v = v * sigmoidf_(v);
-        else if (a.relu) v = fmaxf(v, 0.f);
-        v *= scl;
-        const OutT o = from_f32<OutT>(v);
-        ost[pl * SROW + col] = o;
-        if (co_ok && pix_ok[m][i]) gsum[b] += to_f32(o);
+        for (int i = 0; i < 4; ++i) {
+          const int pl = wave * (16 * DCN_WM) + m * 16 + grp * 4 + i;
+          float v = fmaf(acc[m][b][i], mul, shift);
+          if constexpr (ACT == KAD_ACT_SILU) v = v * sigmoidf_(v);
+          else if constexpr (ACT == KAD_ACT_RELU) v = fmaxf(v, 0.f);
+          v *= scl;
+          const OutT o = from_f32<OutT>(v);
+          ost[pl * SROW + col] = o;
+          if (co_ok && pix_ok[m][i]) gsum[b] += to_f32(o);
+        }
       }
     }
-  }
+  };
+  if (a.relu == KAD_ACT_SILU) epilogue(std::integral_constant<int, KAD_ACT_SILU>{});
+  else if (a.relu) epilogue(std::integral_constant<int, KAD_ACT_RELU>{});
+  else epilogue(std::integral_constant<int, KAD_ACT_NONE>{});
   if (a.gap_partial) {
 #pragma unroll
     for (int b = 0; b < NBF; ++b) {
@@ -1793,26 +1802,32 @@ __device__ __forceinline__ void dsc2_block(const kad_dcn_args& a, const DcnGeom&
       pix_ok[m][i] = pl < npx && ty0 + oyl < g.ho && tx0 + pl - oyl * g.tw < g.wo;
     }
   float gsum[NBF];
+  auto epilogue = [&](auto act) {  // activation as a template argument, as in dcn_block
+    constexpr int ACT = decltype(act)::value;
 #pragma unroll
-  for (int f = 0; f < NBF; ++f) {
-    gsum[f] = 0.f;
-    const int col = f * 16 + row;
-    const bool co_ok = co0 + col < a.cout;
-    const float shift = s_par[0][col], mul = s_par[1][col], scl = s_par[2][col];
+    for (int f = 0; f < NBF; ++f) {
+      gsum[f] = 0.f;
+      const int col = f * 16 + row;
+      const bool co_ok = co0 + col < a.cout;
+      const float shift = s_par[0][col], mul = s_par[1][col], scl = s_par[2][col];
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
+      for (int m = 0; m < 2; ++m)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pl = wave * 32 + m * 16 + grp * 4 + i;
-        float v = fmaf(acc[m][f][i], mul, shift);
-        if (a.relu == KAD_ACT_SILU) v = v * sigmoidf_(v);
-        else if (a.relu) v = fmaxf(v, 0.f);
-        v *= scl;
-        const OutT o = from_f32<OutT>(v);
-        ost[pl * SROW + col] = o;
-        if (co_ok && pix_ok[m][i]) gsum[f] += to_f32(o);
-      }
-  }
+        for (int i = 0; i < 4; ++i) {
+          const int pl = wave * 32 + m * 16 + grp * 4 + i;
+          float v = fmaf(acc[m][f][i], mul, shift);
+          if constexpr (ACT == KAD_ACT_SILU) v = v * sigmoidf_(v);
+          else if constexpr (ACT == KAD_ACT_RELU) v = fmaxf(v, 0.f);
+          v *= scl;
+          const OutT o = from_f32<OutT>(v);
+          ost[pl * SROW + col] = o;
+          if (co_ok && pix_ok[m][i]) gsum[f] += to_f32(o);
+        }
+    }
+  };
+  if (a.relu == KAD_ACT_SILU) epilogue(std::integral_constant<int, KAD_ACT_SILU>{});
+  else if (a.relu) epilogue(std::integral_constant<int, KAD_ACT_RELU>{});
+  else epilogue(std::integral_constant<int, KAD_ACT_NONE>{});
   if (a.gap_partial) {
 #pragma unroll
     for (int f = 0; f < NBF; ++f) {
@@ -2117,6 +2132,8 @@ extern "C" int kad_conv_fwd(const kad_dcn_args* a, void* stream) {
   if (rc) return fail(rc, "kad_conv_fwd: %s", kad_last_error());
   KAD_CHECK_ARG(a->relu >= KAD_ACT_NONE && a->relu <= KAD_ACT_SILU, "kad_conv_fwd: unknown activation %d", a->relu);
   hipStream_t st = (hipStream_t)stream;
+  rc = convolution_igemm(*a, g.ho, g.wo, st);  // 16-bit, NHWC output: implicit-GEMM kernel
+  if (rc != 1) return rc;
   switch (a->dtype) {
     case KAD_F32: return dispatch_dcn<float, float, MODE_PLAIN>(*a, st, g);
     case KAD_F16: return dispatch_dcn<half_t, half_t, MODE_PLAIN>(*a, st, g);

@@ -20,6 +20,8 @@
 // (transposed on the way in for NCHW input, so every lane's MFMA A fragment is
 // 8 K-contiguous halves); the B fragment (weights, packed [Cout_pad][Cin_pad]
 // with Cin_pad = roundup(Cin, 32)) is one 16-byte load per lane.
+#include <type_traits>
+
 #include "kad_common.h"
 
 namespace kad {
@@ -146,33 +148,38 @@ __global__ __launch_bounds__(GM_THREADS) void gemm1x1_kernel(kad_gemm_args a, in
   }
 
   // ---- epilogue: bias, activation, store; zero the NHWC padding channels -------------
+  auto epilogue = [&](auto act_tag) {  // activation as a template argument: no per-value branch
+    constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-  for (int b = 0; b < NBF; ++b) {
-    const int co = co0 + b * 16 + row;
-    const bool co_ok = co < a.cout;
-    // NHWC: channels [cout, roundup(cout, 8)) are the output's zero padding; the rest of a
-    // wider channel stride (other slices of a concat buffer) is left untouched
-    const bool pad_ch = !co_ok && a.out_layout == KAD_NHWC && co < a.out_cs && co < round_up(a.cout, 8);
-    const float bias = (co_ok && a.bias) ? a.bias[co] : 0.f;
+    for (int b = 0; b < NBF; ++b) {
+      const int co = co0 + b * 16 + row;
+      const bool co_ok = co < a.cout;
+      // NHWC: channels [cout, roundup(cout, 8)) are the output's zero padding; the rest of a
+      // wider channel stride (other slices of a concat buffer) is left untouched
+      const bool pad_ch = !co_ok && a.out_layout == KAD_NHWC && co < a.out_cs && co < round_up(a.cout, 8);
+      const float bias = (co_ok && a.bias) ? a.bias[co] : 0.f;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
+      for (int m = 0; m < 2; ++m) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = p0 + wave * 32 + m * 16 + grp * 4 + i;
-        if (p >= P) continue;
-        float v = acc[m][b][i] + bias;
-        if (a.act == 1) v = v * sigmoidf_(v);
-        if (co_ok) {
-          if (a.out_layout == KAD_NHWC)
-            ((T*)a.out)[((int64_t)n * P + p) * a.out_cs + co] = from_f32<T>(v);
-          else
-            ((T*)a.out)[((int64_t)n * a.cout + co) * P + p] = from_f32<T>(v);
-        } else if (pad_ch) {
-          ((T*)a.out)[((int64_t)n * P + p) * a.out_cs + co] = from_f32<T>(0.f);
+        for (int i = 0; i < 4; ++i) {
+          const int p = p0 + wave * 32 + m * 16 + grp * 4 + i;
+          if (p >= P) continue;
+          float v = acc[m][b][i] + bias;
+          if constexpr (ACT == 1) v = v * sigmoidf_(v);
+          if (co_ok) {
+            if (a.out_layout == KAD_NHWC)
+              ((T*)a.out)[((int64_t)n * P + p) * a.out_cs + co] = from_f32<T>(v);
+            else
+              ((T*)a.out)[((int64_t)n * a.cout + co) * P + p] = from_f32<T>(v);
+          } else if (pad_ch) {
+            ((T*)a.out)[((int64_t)n * P + p) * a.out_cs + co] = from_f32<T>(0.f);
+          }
         }
       }
     }
-  }
+  };
+  if (a.act == 1) epilogue(std::integral_constant<int, 1>{});
+  else epilogue(std::integral_constant<int, 0>{});
 }
 
 // ---- NCHW fast path -------------------------------------------------------------------------
@@ -331,36 +338,41 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_arg
       const int co = co_w + 16 * m + 4 * g + i;
       bias[m][i] = (a.bias && co < a.cout) ? a.bias[co] : 0.f;
     }
+  auto epilogue = [&](auto act_tag) {  // activation as a template argument: no per-value branch
+    constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < 4; ++m) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int co = co_w + 16 * m + 4 * g + i;
-      if (co >= a.cout || nvalid <= 0) continue;
-      raw_t o;
+      for (int i = 0; i < 4; ++i) {
+        const int co = co_w + 16 * m + 4 * g + i;
+        if (co >= a.cout || nvalid <= 0) continue;
+        raw_t o;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float v = acc[m][j][i] + bias[m][i];
-        if (a.act == 1) v = v * __builtin_amdgcn_rcpf(1.f + __expf(-v));  // SiLU; 16-bit output
-        o[j] = from_f32<T>(v);
-      }
-      T* dst = (T*)a.out + ((int64_t)n * a.cout + co) * P + px;
-      if (nvalid >= 8) {
-        if constexpr (V16) {
-          *(intx4*)dst = __builtin_bit_cast(intx4, o);
-        } else {
-          typedef int intx2 __attribute__((ext_vector_type(2)));
-          const intx4 q = __builtin_bit_cast(intx4, o);
-          *(intx2*)dst = intx2{q[0], q[1]};
-          *(intx2*)(dst + 4) = intx2{q[2], q[3]};
+        for (int j = 0; j < 8; ++j) {
+          float v = acc[m][j][i] + bias[m][i];
+          if constexpr (ACT == 1) v = v * __builtin_amdgcn_rcpf(1.f + __expf(-v));  // SiLU; 16-bit output
+          o[j] = from_f32<T>(v);
         }
-      } else {
+        T* dst = (T*)a.out + ((int64_t)n * a.cout + co) * P + px;
+        if (nvalid >= 8) {
+          if constexpr (V16) {
+            *(intx4*)dst = __builtin_bit_cast(intx4, o);
+          } else {
+            typedef int intx2 __attribute__((ext_vector_type(2)));
+            const intx4 q = __builtin_bit_cast(intx4, o);
+            *(intx2*)dst = intx2{q[0], q[1]};
+            *(intx2*)(dst + 4) = intx2{q[2], q[3]};
+          }
+        } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (j < nvalid) dst[j] = o[j];
+          for (int j = 0; j < 8; ++j)
+            if (j < nvalid) dst[j] = o[j];
+        }
       }
     }
-  }
+  };
+  if (a.act == 1) epilogue(std::integral_constant<int, 1>{});
+  else epilogue(std::integral_constant<int, 0>{});
 }
 
 // Packed weights: rows [Cout_pad][Cin_pad] (the general kernel, the pyramid),
@@ -456,33 +468,38 @@ __global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args 
   // ---- epilogue: bias, activation, 8-byte stores of 4 channels; zero the pad channels ----------
   const int cpad = round_up(a.cout, 8) < a.out_cs ? round_up(a.cout, 8) : a.out_cs;
   T* out = (T*)a.out + (int64_t)n * P * a.out_cs;
+  auto epilogue = [&](auto act_tag) {  // activation as a template argument: no per-value branch
+    constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
-  for (int f = 0; f < NB; ++f) {
-    const int co = co0 + 16 * f + 4 * g;
-    if (co >= cpad) continue;
-    float b[4];
+    for (int f = 0; f < NB; ++f) {
+      const int co = co0 + 16 * f + 4 * g;
+      if (co >= cpad) continue;
+      float b[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) b[i] = (a.bias && co + i < a.cout) ? a.bias[co + i] : 0.f;
+      for (int i = 0; i < 4; ++i) b[i] = (a.bias && co + i < a.cout) ? a.bias[co + i] : 0.f;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      if (!pok[m]) continue;
-      T o[4];
+      for (int m = 0; m < 4; ++m) {
+        if (!pok[m]) continue;
+        T o[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = acc[m][f][i] + b[i];
-        if (a.act == 1) v = v * sigmoidf_(v);
-        o[i] = from_f32<T>(co + i < a.cout ? v : 0.f);
-      }
-      T* dst = out + (int64_t)(p0 + 16 * m + c) * a.out_cs + co;
-      if (co + 4 <= cpad) {
-        *(half4_t*)dst = __builtin_bit_cast(half4_t, o);
-      } else {
+        for (int i = 0; i < 4; ++i) {
+          float v = acc[m][f][i] + b[i];
+          if constexpr (ACT == 1) v = v * sigmoidf_(v);
+          o[i] = from_f32<T>(co + i < a.cout ? v : 0.f);
+        }
+        T* dst = out + (int64_t)(p0 + 16 * m + c) * a.out_cs + co;
+        if (co + 4 <= cpad) {
+          *(half4_t*)dst = __builtin_bit_cast(half4_t, o);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (co + i < cpad) dst[i] = o[i];
+          for (int i = 0; i < 4; ++i)
+            if (co + i < cpad) dst[i] = o[i];
+        }
       }
     }
-  }
+  };
+  if (a.act == 1) epilogue(std::integral_constant<int, 1>{});
+  else epilogue(std::integral_constant<int, 0>{});
 }
 
 // The NHWC fast path covers 16-bit NHWC -> NHWC without pooling when Cin and the input channel

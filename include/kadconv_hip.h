@@ -424,6 +424,15 @@ int kad_scale_residual(void *out, const float *att, const void *residual, int n,
  * cuDNN (KAD-CNet/inference/acceleration/kadc_fused_sm75.py:616-629). */
 int kad_conv_fwd(const kad_dcn_args *a, void *stream);
 
+/* The network's stem: the same 3x3 Conv for an NCHW image with 1-3 channels,
+ * read as it is (x: [N][Cin][H][W] contiguous, 16-bit; x_cs ignored) and written
+ * NHWC (out_cs), so the input needs no channels-last copy.  pad 1, stride 1 or 2,
+ * Cout <= 64, W a multiple of 8; bias and activation only (post_* NULL).
+ * Weights packed by kad_dcn_pack_weights.  Stands in for the first Conv of
+ * KAD-CNet (models/common.py:43-57, `Conv(3, c, 3, 2)` of the yaml's first
+ * row), run by cuDNN in the reference (kadc_fused_sm75.py:616-629). */
+int kad_stem_conv_fwd(const kad_dcn_args *a, void *stream);
+
 #define KAD_RS_AVG 0      /* average pool, zero padding counted (count_include_pad=True) */
 #define KAD_RS_MAX 1      /* max pool, padding ignored */
 #define KAD_RS_NEAREST 2  /* nearest upsample by the integer factor s: out[y][x] = in[y / s][x / s] */

@@ -27,7 +27,9 @@
 //    (consecutive output columns) read consecutive 80-byte rows for every tap, as
 //    with stride 1.
 //  * Taps are software-pipelined (fully unrolled, fragments of tap k + 1 read while
-//    tap k multiplies).  Accumulation is fp32, chunk-major then tap order.
+//    tap k multiplies).  Accumulation is fp32, chunk-major then tap order.  The MFMA
+//    takes the weights as its row operand, so a lane's accumulator holds 4 consecutive
+//    output channels of one pixel: the epilogue writes them as one 8-byte piece.
 //  * Epilogue: parameters applied in registers, the tile staged in LDS (the weight
 //    buffer) and written with 16-byte row-contiguous stores.
 //  * Blocks over (image, patch) flattened in XCD-aware order: each XCD takes a
@@ -89,7 +91,7 @@ struct CvGeom {
 };
 
 template <typename T, int NBW, int S>
-__global__ __launch_bounds__(CV_THREADS, 1) void conv3x3_ig_kernel(kad_dcn_args a, CvGeom g) {
+__global__ __launch_bounds__(CV_THREADS, NBW <= 2 ? 2 : 1) void conv3x3_ig_kernel(kad_dcn_args a, CvGeom g) {
   typedef CvFrag<T> Ops;
   typedef typename Ops::frag frag;
   constexpr int BN = 32 * NBW;                                  // block columns
@@ -99,6 +101,7 @@ __global__ __launch_bounds__(CV_THREADS, 1) void conv3x3_ig_kernel(kad_dcn_args 
   static_assert(CV_PX * SROW * 2 <= 9 * BN * 64, "epilogue tile must fit the weight buffer");
   __shared__ __align__(16) char region[CvCap<S>::SLOTS * CV_PXB];
   __shared__ __align__(16) char wsm[9 * BN * 64];
+  __shared__ __align__(16) float s_par[3][BN];  // shift (bias * mul + add), mul, post_scale per column
 
   const int q = (blockIdx.x & 7) * (g.grid_x >> 3) + (blockIdx.x >> 3);
   if (q >= a.n * g.tiles) return;  // whole block, before any barrier
@@ -114,21 +117,14 @@ __global__ __launch_bounds__(CV_THREADS, 1) void conv3x3_ig_kernel(kad_dcn_args 
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(xb, (uint32_t)(a.h * a.w * a.x_cs * 2));
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.wpack, (uint32_t)(g.cout_pad * g.nchunk * 9 * 32 * 2));
 
-  // epilogue parameters of this lane's columns (loaded first, used last)
-  float shift[NBW], mul[NBW], scl[NBW];
-#pragma unroll
-  for (int b = 0; b < NBW; ++b) {
-    const int co = co0 + wn * 16 * NBW + b * 16 + row;
-    float bi = 0.f, m = 1.f, ad = 0.f, sc = 1.f;
-    if (co < a.cout) {
-      if (a.bias) bi = a.bias[co];
-      if (a.post_mul) m = a.post_mul[co];
-      if (a.post_add) ad = a.post_add[co];
-      if (a.post_scale) sc = a.post_scale[co];
-    }
-    shift[b] = bi * m + ad;
-    mul[b] = m;
-    scl[b] = sc;
+  // epilogue parameters: requested first, staged in LDS with chunk 0
+  float par[4] = {0.f, 1.f, 0.f, 1.f};
+  if (tid < BN && co0 + tid < a.cout) {
+    const int co = co0 + tid;
+    if (a.bias) par[0] = a.bias[co];
+    if (a.post_mul) par[1] = a.post_mul[co];
+    if (a.post_add) par[2] = a.post_add[co];
+    if (a.post_scale) par[3] = a.post_scale[co];
   }
 
   // ---- staging, walked in LDS order so every store is at a fixed offset from the thread's base -------
@@ -205,6 +201,11 @@ __global__ __launch_bounds__(CV_THREADS, 1) void conv3x3_ig_kernel(kad_dcn_args 
 
   stage_load(0);
   stage_store();
+  if (tid < BN) {
+    s_par[0][tid] = par[0] * par[1] + par[2];
+    s_par[1][tid] = par[1];
+    s_par[2][tid] = par[3];
+  }
   for (int c = 0; c < g.nchunk; ++c) {
     __syncthreads();  // chunk c staged
     const bool next = c + 1 < g.nchunk;
@@ -229,7 +230,7 @@ __global__ __launch_bounds__(CV_THREADS, 1) void conv3x3_ig_kernel(kad_dcn_args 
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int b = 0; b < NBW; ++b) acc[m][b] = Ops::mma(af[k & 1][m], bf[k & 1][b], acc[m][b]);
+        for (int b = 0; b < NBW; ++b) acc[m][b] = Ops::mma(bf[k & 1][b], af[k & 1][m], acc[m][b]);
     }
     if (next) {
       __syncthreads();  // every wave is done with chunk c
@@ -246,17 +247,21 @@ __global__ __launch_bounds__(CV_THREADS, 1) void conv3x3_ig_kernel(kad_dcn_args 
     constexpr int ACT = decltype(act)::value;
 #pragma unroll
     for (int b = 0; b < NBW; ++b) {
-      const int col = wn * 16 * NBW + b * 16 + row;
+      const int col = wn * 16 * NBW + b * 16 + grp * 4;  // this lane's 4 channels
+      const floatx4 sh = *(const floatx4*)&s_par[0][col], mu = *(const floatx4*)&s_par[1][col],
+                    sc = *(const floatx4*)&s_par[2][col];
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
+      for (int m = 0; m < 4; ++m) {
+        T o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float v = fmaf(acc[m][b][i], mul[b], shift[b]);
+          float v = fmaf(acc[m][b][i], mu[i], sh[i]);
           if constexpr (ACT == KAD_ACT_SILU) v = v * sigmoidf_(v);
           else if constexpr (ACT == KAD_ACT_RELU) v = fmaxf(v, 0.f);
-          v *= scl[b];
-          ost[(wm * 64 + m * 16 + grp * 4 + i) * SROW + col] = from_f32<T>(v);
+          o[i] = from_f32<T>(v * sc[i]);
         }
+        *(uint2*)(ost + (wm * 64 + m * 16 + row) * SROW + col) = __builtin_bit_cast(uint2, o);
+      }
     }
   };
   if (a.relu == KAD_ACT_SILU) epilogue(std::integral_constant<int, KAD_ACT_SILU>{});
@@ -267,17 +272,26 @@ __global__ __launch_bounds__(CV_THREADS, 1) void conv3x3_ig_kernel(kad_dcn_args 
   const int64_t P = (int64_t)g.ho * g.wo;
   const bool vec_ok = (a.out_cs % 8) == 0 && ((uintptr_t)a.out & 15) == 0;
   constexpr int VPP = BN / 8;  // 16-byte vectors per pixel row of the tile
-  for (int j = tid; j < CV_PX * VPP; j += CV_THREADS) {
-    const int pl = j / VPP, v = j - pl * VPP;
+  constexpr int NIT = CV_PX * VPP / CV_THREADS;
+  static_assert(NIT * CV_THREADS == CV_PX * VPP, "whole copy rounds");
+  intx4 vv[NIT];
+#pragma unroll
+  for (int t = 0; t < NIT; ++t) {  // every LDS read first, then the stores
+    const int j = tid + t * CV_THREADS, pl = j / VPP, v = j - pl * VPP;
+    vv[t] = *(const intx4*)(ost + pl * SROW + v * 8);
+  }
+#pragma unroll
+  for (int t = 0; t < NIT; ++t) {
+    const int j = tid + t * CV_THREADS, pl = j / VPP, v = j - pl * VPP;
     const int oyl = (int)(((float)pl + 0.5f) * g.inv_tw);
     const int oy = ty0 + oyl, ox = tx0 + pl - oyl * g.tw;
     const int co = co0 + v * 8;
     if (pl >= g.th * g.tw || oy >= g.ho || ox >= g.wo || co >= a.cout) continue;
-    const T* src = ost + pl * SROW + v * 8;
     T* dst = out + ((int64_t)n * P + (int64_t)oy * g.wo + ox) * a.out_cs + co;
     if (vec_ok && co + 8 <= a.cout) {
-      *(intx4*)dst = *(const intx4*)src;
+      *(intx4*)dst = vv[t];
     } else {
+      const T* src = ost + pl * SROW + v * 8;
       for (int e = 0; e < 8 && co + e < a.cout; ++e) dst[e] = src[e];
     }
   }
@@ -330,6 +344,155 @@ int launch_nbw(const kad_dcn_args& a, const CvGeom& g, int nbw, hipStream_t st) 
   return check_launch("kad_conv_fwd");
 }
 
+// ---- stem: 3x3 convolution of an NCHW image with at most 3 channels -----------------------------------
+// The network's first Conv (3 -> C, stride 2) has K = 9 Cin <= 27: the whole reduction is one
+// v_mfma_f32_16x16x32 step with k = 9 c + 3 ky + kx (k >= 9 Cin zero), instead of nine 32-channel taps
+// of which 29 / 32 are padding.  The image is read as it comes (NCHW, no channels-last copy): a block
+// (8 x 32 output pixels, 4 waves of two rows) stages its footprint as [Cin][FH][FWP] rows of 16-byte
+// pieces (W % 8 == 0, so every piece is wholly inside or outside the image), each lane gathers the 8
+// taps of its k-group from LDS, and the weights [co][k] form the MFMA's row operand, so a lane ends
+// with 4 consecutive output channels of one pixel (one 8-byte NHWC store).
+constexpr int ST_TH = 8, ST_TW = 32;
+
+template <int S> struct StGeo {
+  static constexpr int FH = (ST_TH - 1) * S + 3;          // footprint rows
+  static constexpr int FWP = ((ST_TW - 1) * S + 3 + 7 + 7) / 8 * 8;  // from 8 before the first column
+  static constexpr int PIECES = 3 * FH * (FWP / 8);       // at most 3 channels
+  static constexpr int PPT = (PIECES + CV_THREADS - 1) / CV_THREADS;
+};
+
+template <typename T, int S, int NB>
+__global__ __launch_bounds__(CV_THREADS) void stem_conv_kernel(kad_dcn_args a, int ho, int wo, int tiles_x,
+                                                             int tiles) {
+  typedef CvFrag<T> Ops;
+  typedef typename Ops::frag frag;
+  typedef StGeo<S> G;
+  __shared__ __align__(16) T fp[3 * G::FH * G::FWP];
+  const int q = blockIdx.x;
+  const int n = q / tiles, tile = q - n * tiles;
+  const int tyi = tile / tiles_x;
+  const int ty0 = tyi * ST_TH, tx0 = (tile - tyi * tiles_x) * ST_TW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = lane & 15, grp = lane >> 4;
+  const int y0 = ty0 * S - a.pad, xa = tx0 * S - 8;  // footprint row 0; column 0 of the staged rows
+  const int cin = a.cin;
+  const T* xb = (const T*)a.x + (int64_t)n * cin * a.h * a.w;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xb, (uint32_t)(cin * a.h * a.w * 2));
+
+  // footprint pieces: (channel, row, 8 columns); outside the image -> zeros
+  frag v[G::PPT];
+  const int np = cin * G::FH * (G::FWP / 8);
+#pragma unroll
+  for (int u = 0; u < G::PPT; ++u) {
+    const int e = tid + u * CV_THREADS;
+    uint32_t o = KAD_OOB;
+    if (e < np) {
+      const int c = e / (G::FH * (G::FWP / 8)), r = e - c * (G::FH * (G::FWP / 8));
+      const int fy = r / (G::FWP / 8), pc = r - fy * (G::FWP / 8);
+      const int gy = y0 + fy, gx = xa + 8 * pc;
+      if (gy >= 0 && gy < a.h && gx >= 0 && gx < a.w) o = (uint32_t)(((c * a.h + gy) * a.w + gx) * 2);
+    }
+    v[u] = gld8<T>(rx, o, 0);
+  }
+  // weights as the row operand: lane -> output channel 16 b + row, k = 8 grp + j (packed [co][9][32])
+  frag wa[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int co = 16 * b + row;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int k = 8 * grp + j;
+      T w = from_f32<T>(0.f);
+      if (k < 9 * cin && co < a.cout) w = ((const T*)a.wpack)[co * 288 + (k % 9) * 32 + k / 9];
+      wa[b][j] = w;
+    }
+  }
+  float shift[NB][4], scl[NB][4];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int co = 16 * b + 4 * grp + i;
+      shift[b][i] = (a.bias && co < a.cout) ? a.bias[co] : 0.f;
+      scl[b][i] = 1.f;
+    }
+  // this lane's tap offsets in the footprint (element units), -1: k past 9 Cin
+  int koff[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int k = 8 * grp + j;
+    const int c = k / 9, t = k - 9 * c, ky = t / 3, kx = t - 3 * ky;
+    koff[j] = k < 9 * cin ? (c * G::FH + ky) * G::FWP + kx + 7 : -1;
+  }
+#pragma unroll
+  for (int u = 0; u < G::PPT; ++u) {
+    const int e = tid + u * CV_THREADS;
+    if (e < np) {
+      const int c = e / (G::FH * (G::FWP / 8)), r = e - c * (G::FH * (G::FWP / 8));
+      *(frag*)(fp + (c * G::FH) * G::FWP + r * 8) = v[u];
+    }
+  }
+  __syncthreads();
+
+  floatx4 acc[4][NB];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int py = 2 * wave + (m >> 1), px = 16 * (m & 1) + row;  // output pixel of this lane's column
+    const T* base = fp + (py * S) * G::FWP + px * S;
+    frag bm;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) bm[j] = koff[j] >= 0 ? base[koff[j]] : from_f32<T>(0.f);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[m][b] = Ops::mma(wa[b], bm, floatx4{0.f, 0.f, 0.f, 0.f});
+  }
+
+  T* out = (T*)a.out;
+  const bool vec_ok = (a.out_cs % 4) == 0 && ((uintptr_t)a.out & 7) == 0;
+  auto epilogue = [&](auto act) {
+    constexpr int ACT = decltype(act)::value;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int oy = ty0 + 2 * wave + (m >> 1), ox = tx0 + 16 * (m & 1) + row;
+      if (oy >= ho || ox >= wo) continue;
+      T* dst = out + (((int64_t)n * ho + oy) * wo + ox) * a.out_cs;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int co = 16 * b + 4 * grp;
+        if (co >= a.cout) continue;
+        T o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float val = acc[m][b][i] + shift[b][i];
+          if constexpr (ACT == KAD_ACT_SILU) val = val * sigmoidf_(val);
+          else if constexpr (ACT == KAD_ACT_RELU) val = fmaxf(val, 0.f);
+          o[i] = from_f32<T>(val * scl[b][i]);
+        }
+        if (vec_ok && co + 4 <= a.cout) {
+          *(uint2*)(dst + co) = __builtin_bit_cast(uint2, o);
+        } else {
+          for (int i = 0; i < 4 && co + i < a.cout; ++i) dst[co + i] = o[i];
+        }
+      }
+    }
+  };
+  if (a.relu == KAD_ACT_SILU) epilogue(std::integral_constant<int, KAD_ACT_SILU>{});
+  else if (a.relu) epilogue(std::integral_constant<int, KAD_ACT_RELU>{});
+  else epilogue(std::integral_constant<int, KAD_ACT_NONE>{});
+}
+
+template <typename T, int S>
+int launch_stem(const kad_dcn_args& a, int ho, int wo, hipStream_t st) {
+  const int tiles_x = ceil_div(wo, ST_TW), tiles = ceil_div(ho, ST_TH) * tiles_x;
+  const dim3 grid(a.n * tiles), block(CV_THREADS);
+  const int nb = ceil_div(a.cout, 16);
+  switch (nb) {
+    case 1: hipLaunchKernelGGL((stem_conv_kernel<T, S, 1>), grid, block, 0, st, a, ho, wo, tiles_x, tiles); break;
+    case 2: hipLaunchKernelGGL((stem_conv_kernel<T, S, 2>), grid, block, 0, st, a, ho, wo, tiles_x, tiles); break;
+    case 3: hipLaunchKernelGGL((stem_conv_kernel<T, S, 3>), grid, block, 0, st, a, ho, wo, tiles_x, tiles); break;
+    default: hipLaunchKernelGGL((stem_conv_kernel<T, S, 4>), grid, block, 0, st, a, ho, wo, tiles_x, tiles); break;
+  }
+  return check_launch("kad_stem_conv_fwd");
+}
+
 }  // namespace
 
 // 16-bit NHWC-output 3x3 convolution on the implicit-GEMM kernel; 1 = not handled here
@@ -363,3 +526,26 @@ int convolution_igemm(const kad_dcn_args& a, int ho, int wo, hipStream_t st) {
 }
 
 }  // namespace kad
+
+extern "C" int kad_stem_conv_fwd(const kad_dcn_args* a, void* stream) {
+  using namespace kad;
+  KAD_CHECK_ARG(a && a->x && a->wpack && a->out, "kad_stem_conv_fwd: null pointer");
+  KAD_CHECK_ARG(a->dtype == KAD_F16 || a->dtype == KAD_BF16, "kad_stem_conv_fwd: 16-bit dtypes only (got %d)", a->dtype);
+  KAD_CHECK_ARG(a->n > 0 && a->cin >= 1 && a->cin <= 3 && a->cout >= 1 && a->cout <= 64,
+                "kad_stem_conv_fwd: n=%d cin=%d cout=%d (cin in [1, 3], cout in [1, 64])", a->n, a->cin, a->cout);
+  KAD_CHECK_ARG((a->stride == 1 || a->stride == 2) && a->pad == 1, "kad_stem_conv_fwd: stride %d pad %d (stride 1 or 2, pad 1)",
+                a->stride, a->pad);
+  KAD_CHECK_ARG(a->h > 0 && a->w > 0 && a->w % 8 == 0 && (int64_t)a->cin * a->h * a->w * 2 < ((int64_t)1 << 31),
+                "kad_stem_conv_fwd: image %dx%d (W a multiple of 8, one image below 2 GB)", a->h, a->w);
+  KAD_CHECK_ARG(a->out_layout == KAD_NHWC && a->out_cs >= a->cout, "kad_stem_conv_fwd: NHWC output with out_cs >= cout");
+  KAD_CHECK_ARG(!a->post_mul && !a->post_add && !a->post_scale && !a->gap_partial && !a->se_att,
+                "kad_stem_conv_fwd: bias and activation only");
+  KAD_CHECK_ARG(a->relu >= KAD_ACT_NONE && a->relu <= KAD_ACT_SILU, "kad_stem_conv_fwd: unknown activation %d", a->relu);
+  KAD_CHECK_ARG(((uintptr_t)a->x & 15) == 0, "kad_stem_conv_fwd: x must be 16-byte aligned");
+  const int ho = (a->h - 1) / a->stride + 1, wo = (a->w - 1) / a->stride + 1;
+  KAD_CHECK_ARG((int64_t)a->n * ceil_div(ho, ST_TH) * ceil_div(wo, ST_TW) < (1ll << 31), "kad_stem_conv_fwd: grid too large");
+  hipStream_t st = (hipStream_t)stream;
+  if (a->stride == 1)
+    return a->dtype == KAD_F16 ? launch_stem<half_t, 1>(*a, ho, wo, st) : launch_stem<bf16_t, 1>(*a, ho, wo, st);
+  return a->dtype == KAD_F16 ? launch_stem<half_t, 2>(*a, ho, wo, st) : launch_stem<bf16_t, 2>(*a, ho, wo, st);
+}

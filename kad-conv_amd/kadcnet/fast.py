@@ -7,7 +7,8 @@ tree, found by class name, so a model built by the reference's own
 KAD-CNet/models/yolo.py works too) and runs every layer on the gfx950 kernels:
 
   Conv k=1 (+SiLU)          kad_gemm1x1_fwd, NHWC in / out
-  Conv k=3 (+SiLU), s 1/2   kad_conv_fwd (plain 3x3 conv on the DCN machinery)
+  Conv k=3 (+SiLU), s 1/2   kad_conv_fwd (implicit-GEMM 3x3 conv); the first layer on a
+                            1-3 channel image: kad_stem_conv_fwd, reading the NCHW input
   AConv                     kad_nhwc_resample (2x2 / s1 average) + kad_conv_fwd s2
   ELAN1, SPPELAN, GELAN     the convs write their channel slice of one concat
                             buffer; chunks are slices of it (no copies)
@@ -122,6 +123,20 @@ class _ConvOp:
         else:
             _ext.conv_fwd(x, self.cin, wp, self.cout, out, stride=self.stride, pad=1, bias=self.b, act=self.act)
         return out
+
+
+def _stem_ok(op, x):
+    """The first layer can read the NCHW image directly (kad_stem_conv_fwd)."""
+    return (isinstance(op, _ConvOp) and op.k == 3 and op.pad == 1 and op.stride in (1, 2) and op.cin <= 3
+            and op.cout <= 64 and x.dtype in (torch.float16, torch.bfloat16) and x.shape[3] % 8 == 0)
+
+
+def _stem(op, x):
+    N, _, H, W = x.shape
+    ho, wo = op.out_hw(H, W)
+    out = x.new_empty(N, ho, wo, op.cout)
+    _ext.stem_conv_fwd(x, op.packed(x.dtype), op.cout, out, stride=op.stride, bias=op.b, act=op.act)
+    return out
 
 
 def _copy(src, dst):
@@ -322,12 +337,19 @@ class KADCNetPlan:
         """(y, heads); with keep_layers, also every layer's output (NHWC maps; the
         last entry is (y, heads))."""
         N, C, H, W = x.shape
-        cs = (C + 7) // 8 * 8
-        xin = torch.empty(N, H, W, cs, dtype=x.dtype, device=x.device)
-        _ext.to_nhwc(x.contiguous(), xin)
-        cur = xin[..., :C]
         ys = []
-        for f, op in self.layers:
+        layers = self.layers
+        f0, op0 = layers[0]
+        if f0 == -1 and _stem_ok(op0, x):  # the stem reads the NCHW image itself
+            cur = _stem(op0, x.contiguous())
+            ys.append(cur)
+            layers = layers[1:]
+        else:
+            cs = (C + 7) // 8 * 8
+            xin = torch.empty(N, H, W, cs, dtype=x.dtype, device=x.device)
+            _ext.to_nhwc(x.contiguous(), xin)
+            cur = xin[..., :C]
+        for f, op in layers:
             if f != -1:
                 cur = ys[f] if isinstance(f, int) else [cur if j == -1 else ys[j] for j in f]
             cur = op(cur)

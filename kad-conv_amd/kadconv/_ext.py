@@ -145,6 +145,7 @@ SIGNATURES = {
     'kad_to_nhwc': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_branch_merge': (c_int, [ctypes.POINTER(MergeArgs), c_vp]),
     'kad_conv_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
+    'kad_stem_conv_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_nhwc_resample': (c_int, [ctypes.POINTER(ResampleArgs), c_vp]),
     'kad_ddetect_decode': (c_int, [ctypes.POINTER(DecodeArgs), c_vp]),
     'kad_nms_mask_words': (c_i64, [c_int]),
@@ -711,6 +712,30 @@ def conv_fwd(x_nhwc, cin, wpack, cout, out_nhwc, *, stride=1, pad=1, bias=None, 
     a.dtype = kad_dtype(x_nhwc.dtype)
     a.relu = act
     _check(load().kad_conv_fwd(ctypes.byref(a), _stream()), 'kad_conv_fwd')
+    return out_nhwc
+
+
+def stem_conv_fwd(x_nchw, wpack, cout, out_nhwc, *, stride=2, bias=None, act=KAD_ACT_SILU):
+    """act(conv3x3(x) + bias), pad 1, of a contiguous 16-bit NCHW image with 1-3 channels,
+    written into the NHWC view out (channel slices allowed)."""
+    _need_gpu(x_nchw, wpack, out_nhwc, bias)
+    if x_nchw.dim() != 4 or not x_nchw.is_contiguous():
+        raise ValueError('stem_conv_fwd: x must be a contiguous NCHW tensor')
+    N, C, H, W = x_nchw.shape
+    No, Ho, Wo, ocs = _nhwc_cs(out_nhwc)
+    if (No, Ho, Wo) != (N, (H - 1) // stride + 1, (W - 1) // stride + 1) or out_nhwc.shape[3] < cout:
+        raise ValueError('stem_conv_fwd: output shape does not match the convolution')
+    if wpack.dtype != x_nchw.dtype or out_nhwc.dtype != x_nchw.dtype:
+        raise TypeError('x, packed weights and out must share a dtype')
+    if bias is not None and bias.dtype != torch.float32:
+        raise TypeError('bias must be float32')
+    a = DcnArgs()
+    a.x, a.wpack, a.bias, a.out = _ptr(x_nchw), _ptr(wpack), _ptr(bias), _ptr(out_nhwc)
+    a.n, a.cin, a.cout, a.h, a.w, a.stride, a.pad = N, C, cout, H, W, stride, 1
+    a.x_cs, a.out_layout, a.out_cs = 0, KAD_NHWC, ocs
+    a.dtype = kad_dtype(x_nchw.dtype)
+    a.relu = act
+    _check(load().kad_stem_conv_fwd(ctypes.byref(a), _stream()), 'kad_stem_conv_fwd')
     return out_nhwc
 
 

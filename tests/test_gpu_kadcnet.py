@@ -103,6 +103,47 @@ def test_conv3x3_fwd(dt, cin, cout, stride, groups, act):
     check_close(got[..., 8:8 + cout].permute(0, 3, 1, 2), ref, dtype, f'conv3x3 {dt} {cin}->{cout}')
 
 
+@pytest.mark.parametrize('dt', ['f16', 'bf16'])
+@pytest.mark.parametrize('cin,cout,stride,H,W,act', [(3, 40, 2, 19, 40, 'silu'), (3, 40, 2, 64, 96, 'silu'),
+                                                     (1, 8, 1, 9, 16, 'none'), (2, 24, 2, 33, 24, 'relu'),
+                                                     (3, 64, 1, 17, 32, 'silu'), (3, 33, 2, 8, 8, 'silu')])
+def test_stem_conv_fwd(dt, cin, cout, stride, H, W, act):
+    """kad_stem_conv_fwd (the first Conv, NCHW image in, NHWC out) against F.conv2d in float64
+    on the dtype-rounded operands, written into a channel slice of a wider buffer."""
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(cin * 100 + cout + H)
+    N = 3
+    w = torch.randn(cout, cin, 3, 3, generator=g) / (9 * cin) ** 0.5
+    b = torch.randn(cout, generator=g) * 0.1
+    xq = torch.rand(N, cin, H, W, generator=g).to(dtype)
+    code = {'silu': _ext.KAD_ACT_SILU, 'none': _ext.KAD_ACT_NONE, 'relu': _ext.KAD_ACT_RELU}[act]
+    Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
+    out = torch.full((N, Ho, Wo, cout + 12), 5.0, dtype=dtype, device=dev)
+    wp = _ext.dcn_pack_weights(w.to(dev, dtype), dtype)
+    print(f'stem {dt} {cin}->{cout} s{stride} {H}x{W} {act}', flush=True)
+    _ext.stem_conv_fwd(xq.to(dev), wp, cout, out[..., 4:4 + cout], stride=stride, bias=b.to(dev), act=code)
+    torch.cuda.synchronize()
+    ref = F.conv2d(xq.double(), w.to(dtype).double(), b.double(), stride, 1)
+    ref = {'silu': F.silu, 'none': lambda t: t, 'relu': torch.relu}[act](ref)
+    got = out.cpu().double()
+    assert (got[..., :4] == 5.0).all() and (got[..., 4 + cout:] == 5.0).all()
+    check_close(got[..., 4:4 + cout].permute(0, 3, 1, 2), ref, dtype, f'stem {dt} {cin}->{cout}')
+
+
+def test_stem_conv_rejects_bad_args():
+    from kadconv import _ext
+    x = torch.zeros(1, 4, 16, 16, dtype=torch.float16, device='cuda')
+    wp = _ext.dcn_pack_weights(torch.zeros(8, 4, 3, 3, device='cuda', dtype=torch.float16), torch.float16)
+    out = torch.zeros(1, 8, 8, 8, dtype=torch.float16, device='cuda')
+    with pytest.raises(RuntimeError, match='cin'):
+        _ext.stem_conv_fwd(x, wp, 8, out, stride=2)
+    x3 = torch.zeros(1, 3, 16, 12, dtype=torch.float16, device='cuda')
+    out3 = torch.zeros(1, 8, 6, 8, dtype=torch.float16, device='cuda')
+    with pytest.raises(RuntimeError, match='multiple of 8'):
+        _ext.stem_conv_fwd(x3, wp, 8, out3, stride=2)
+
+
 @pytest.mark.parametrize('dt', ['f16', 'f32'])
 def test_gemm1x1_into_slice(dt):
     """kad_gemm1x1_fwd NHWC into a channel slice of a wider buffer: channels

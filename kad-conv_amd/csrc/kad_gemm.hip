@@ -433,8 +433,12 @@ __global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args 
     xp[m] = x + (int64_t)(pok[m] ? p : 0) * a.x_cs + 8 * g;
   }
   const T* wr[NB];
+  const int wrows = round_up(round_up(a.cout, 8), 128);  // rows of the packed [Cout_pad][Cin_pad] part
 #pragma unroll
-  for (int f = 0; f < NB; ++f) wr[f] = wt + (int64_t)(co0 + 16 * f + c) * cin_pad + 8 * g;
+  for (int f = 0; f < NB; ++f) {
+    const int co = co0 + 16 * f + c;  // rows past the packing (discarded columns) read row 0
+    wr[f] = wt + (int64_t)(co < wrows ? co : 0) * cin_pad + 8 * g;
+  }
   floatx4 acc[4][NB];
 #pragma unroll
   for (int m = 0; m < 4; ++m)
@@ -519,13 +523,35 @@ static void launch_gemm_nhwc_nb(const kad_gemm_args& a, hipStream_t st) {
                      tiles_px, co_blocks, total, round_up(a.cin, 32));
 }
 
+// Output-channel fragments per wave: the fewest padded columns plus 16 per channel block (each
+// re-reads the pixel fragments), ties to the larger NB.  NB <= 5: from NB = 6 the accumulators and
+// the prefetched fragments take more than 256 registers, one wave per SIMD, and the loads' latency
+// is no longer hidden (NB = 8 measured 1.1-1.8x slower than NB = 4 or 5 at the KAD-CNet-S shapes).
+static int nhwc_pick_nb(int cout) {
+  static const int cand[] = {1, 2, 3, 4, 5};
+  const int c8 = round_up(cout, 8);
+  int best = 1;
+  long best_cost = -1;
+  for (int nb : cand) {
+    const int blocks = ceil_div(c8, nb * 16);
+    const long cost = (long)blocks * nb * 16 + 16L * blocks;
+    if (best_cost < 0 || cost <= best_cost) {
+      best_cost = cost;
+      best = nb;
+    }
+  }
+  return best;
+}
+
 template <typename T>
 static int launch_gemm_nhwc(const kad_gemm_args& a, hipStream_t st) {
-  const int nf = ceil_div(round_up(a.cout, 8), 16);  // 16-channel fragments of the output
-  if (nf <= 1) launch_gemm_nhwc_nb<T, 1>(a, st);
-  else if (nf <= 2) launch_gemm_nhwc_nb<T, 2>(a, st);
-  else if (nf <= 4) launch_gemm_nhwc_nb<T, 4>(a, st);
-  else launch_gemm_nhwc_nb<T, 8>(a, st);
+  switch (nhwc_pick_nb(a.cout)) {
+    case 1: launch_gemm_nhwc_nb<T, 1>(a, st); break;
+    case 2: launch_gemm_nhwc_nb<T, 2>(a, st); break;
+    case 3: launch_gemm_nhwc_nb<T, 3>(a, st); break;
+    case 4: launch_gemm_nhwc_nb<T, 4>(a, st); break;
+    default: launch_gemm_nhwc_nb<T, 5>(a, st); break;
+  }
   return check_launch("kad_gemm1x1_fwd");
 }
 

@@ -104,6 +104,36 @@ def test_conv3x3_fwd(dt, cin, cout, stride, groups, act):
 
 
 @pytest.mark.parametrize('dt', ['f16', 'bf16'])
+@pytest.mark.parametrize('cin,cout,stride,H,W', [(144, 208, 1, 50, 50), (72, 144, 2, 64, 72), (40, 72, 1, 37, 101),
+                                                 (216, 96, 2, 26, 30), (64, 36, 1, 100, 9)])
+def test_conv3x3_fwd_many_tiles(dt, cin, cout, stride, H, W):
+    """kad_conv_fwd's implicit-GEMM kernel over many patches and both column-block counts,
+    against F.conv2d in float64; the output's channel stride (cout + 4) is not a multiple of 8
+    for cout = 36 / 72 ... so the element-store path runs too."""
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(cin + cout + H)
+    N = 2
+    w = torch.randn(cout, cin, 3, 3, generator=g) / (9 * cin) ** 0.5
+    b = torch.randn(cout, generator=g) * 0.1
+    xq = torch.randn(N, H, W, cin, generator=g).to(dtype)
+    cs = (cin + 7) // 8 * 8
+    x = torch.zeros(N, H, W, cs, dtype=dtype)
+    x[..., :cin] = xq
+    Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
+    out = torch.full((N, Ho, Wo, cout + 4), 3.0, dtype=dtype, device=dev)
+    wp = _ext.dcn_pack_weights(w.to(dev, dtype), dtype)
+    print(f'conv3x3 tiles {dt} {cin}->{cout} s{stride} {H}x{W}', flush=True)
+    _ext.conv_fwd(x.to(dev)[..., :cin], cin, wp, cout, out[..., :cout], stride=stride, bias=b.to(dev),
+                  act=_ext.KAD_ACT_SILU)
+    torch.cuda.synchronize()
+    ref = F.silu(F.conv2d(xq.permute(0, 3, 1, 2).double(), w.to(dtype).double(), b.double(), stride, 1))
+    got = out.cpu().double()
+    assert (got[..., cout:] == 3.0).all()
+    check_close(got[..., :cout].permute(0, 3, 1, 2), ref, dtype, f'conv3x3 tiles {dt} {cin}->{cout}')
+
+
+@pytest.mark.parametrize('dt', ['f16', 'bf16'])
 @pytest.mark.parametrize('cin,cout,stride,H,W,act', [(3, 40, 2, 19, 40, 'silu'), (3, 40, 2, 64, 96, 'silu'),
                                                      (1, 8, 1, 9, 16, 'none'), (2, 24, 2, 33, 24, 'relu'),
                                                      (3, 64, 1, 17, 32, 'silu'), (3, 33, 2, 8, 8, 'silu')])

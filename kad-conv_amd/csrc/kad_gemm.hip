@@ -527,7 +527,7 @@ static void launch_gemm_nhwc_nb(const kad_gemm_args& a, hipStream_t st) {
 // re-reads the pixel fragments), ties to the larger NB.  NB <= 5: from NB = 6 the accumulators and
 // the prefetched fragments take more than 256 registers, one wave per SIMD, and the loads' latency
 // is no longer hidden (NB = 8 measured 1.1-1.8x slower than NB = 4 or 5 at the KAD-CNet-S shapes).
-static int nhwc_pick_nb(int cout) {
+static int nhwc_pick_nb(int cout, long tiles) {
   static const int cand[] = {1, 2, 3, 4, 5};
   const int c8 = round_up(cout, 8);
   int best = 1;
@@ -540,12 +540,15 @@ static int nhwc_pick_nb(int cout) {
       best = nb;
     }
   }
+  // a launch of fewer than 2048 wave items (512 blocks) narrows its channel blocks: the 25^2 / 50^2
+  // layers of KAD-CNet-S otherwise leave most CUs idle (whole network 7.13 -> 7.05 ms)
+  while (best > 1 && tiles * ceil_div(c8, best * 16) < 2048) --best;
   return best;
 }
 
 template <typename T>
 static int launch_gemm_nhwc(const kad_gemm_args& a, hipStream_t st) {
-  switch (nhwc_pick_nb(a.cout)) {
+  switch (nhwc_pick_nb(a.cout, (long)a.n * ceil_div(a.h * a.w, GH_PXW))) {
     case 1: launch_gemm_nhwc_nb<T, 1>(a, st); break;
     case 2: launch_gemm_nhwc_nb<T, 2>(a, st); break;
     case 3: launch_gemm_nhwc_nb<T, 3>(a, st); break;

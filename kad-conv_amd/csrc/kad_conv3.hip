@@ -411,14 +411,13 @@ __global__ __launch_bounds__(CV_THREADS) void stem_conv_kernel(kad_dcn_args a, i
       wa[b][j] = w;
     }
   }
-  float shift[NB][4], scl[NB][4];
+  float shift[NB][4];  // bias of this lane's output channels
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int co = 16 * b + 4 * grp + i;
       shift[b][i] = (a.bias && co < a.cout) ? a.bias[co] : 0.f;
-      scl[b][i] = 1.f;
     }
   // this lane's tap offsets in the footprint (element units), -1: k past 9 Cin
   int koff[8];
@@ -469,7 +468,7 @@ __global__ __launch_bounds__(CV_THREADS) void stem_conv_kernel(kad_dcn_args a, i
           float val = acc[m][b][i] + shift[b][i];
           if constexpr (ACT == KAD_ACT_SILU) val = val * sigmoidf_(val);
           else if constexpr (ACT == KAD_ACT_RELU) val = fmaxf(val, 0.f);
-          o[i] = from_f32<T>(val * scl[b][i]);
+          o[i] = from_f32<T>(val);
         }
         if (vec_ok && co + 4 <= a.cout) {
           *(uint2*)(dst + co) = __builtin_bit_cast(uint2, o);

@@ -410,15 +410,54 @@ __global__ void gemm_pack_kernel(const float* w, T* out, int cin, int cout, int 
 constexpr int GH_PXW = 64;    // pixels per wave
 constexpr int GH_WAVES = 4;   // waves per block (independent work items)
 
-template <typename T, int NB>
+// WLDS: the block's four waves share one channel block and take four pixel tiles; the block first
+// copies its weight fragments (the packing's fragment-ordered part: NB x Cin_pad / 32 chunks of
+// 1 KB, contiguous) into LDS, so per k-step a wave loads only its pixel fragments from memory and
+// reads the weights from LDS (without it every wave fetched the same weights through the vector
+// memory path, which bounded the big launches).
+template <typename T, int NB, bool WLDS>
 __global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args a, int P, int tiles_px, int co_blocks,
                                                                  int total, int cin_pad) {
   typedef typename GemmOps<T>::frag frag;
+  extern __shared__ __align__(16) char gh_smem[];  // WLDS: [NB][nk][64 lanes][16 bytes]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int item = blockIdx.x * GH_WAVES + wave;
-  if (item >= total) return;
-  const int cb = item % co_blocks;  // the channel blocks of a pixel tile run in neighbouring waves
-  const int t = item / co_blocks;
+  const int nk = cin_pad / 32;
+  int cb, t;
+  if constexpr (WLDS) {
+    // Blocks are dealt to the 8 XCDs round robin (block b to XCD b % 8), each with its own L2:
+    // blocks b, b + 8, ... b + 8 (co_blocks - 1) take the same four pixel tiles with each channel
+    // block, so a tile's pixels are fetched into one L2 only.
+    const int ntg = ceil_div(total / co_blocks, GH_WAVES), b = blockIdx.x;
+    const int tg = (b / (8 * co_blocks)) * 8 + (b & 7);
+    if (tg >= ntg) return;  // the whole block, before its barrier
+    cb = (b >> 3) % co_blocks;
+    t = tg * GH_WAVES + wave;
+    const int cpad16 = round_up(round_up(a.cout, 8), 128) / 16;  // 16-column blocks in the packing
+    const T* frags = (const T*)a.wpack + (int64_t)cpad16 * 16 * cin_pad;
+    const int nchunk = NB * nk * 64;  // 16-byte pieces
+    for (int e0 = 0; e0 < nchunk; e0 += 8 * 64 * GH_WAVES) {
+      intx4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u * 64 * GH_WAVES + threadIdx.x, ch = e >> 6, f = ch / nk, cb16 = cb * NB + f;
+        v[u] = intx4{0, 0, 0, 0};
+        if (e < nchunk && cb16 < cpad16)
+          v[u] = *(const intx4*)(frags + ((int64_t)(cb16 * nk + (ch - f * nk)) * 64 + (e & 63)) * 8);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int e = e0 + u * 64 * GH_WAVES + threadIdx.x;
+        if (e < nchunk) *(intx4*)(gh_smem + (size_t)e * 16) = v[u];
+      }
+    }
+    __syncthreads();
+    if (t * co_blocks >= total) return;  // no tile for this wave (after the block's only barrier)
+  } else {
+    const int item = blockIdx.x * GH_WAVES + wave;
+    if (item >= total) return;
+    cb = item % co_blocks;  // the channel blocks of a pixel tile run in neighbouring waves
+    t = item / co_blocks;
+  }
   const int n = t / tiles_px, p0 = (t - n * tiles_px) * GH_PXW;
   const int co0 = cb * NB * 16;
   const int c = lane & 15, g = lane >> 4;
@@ -450,14 +489,20 @@ __global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args 
     const bool kok = k0 + 8 * g < a.cin;
 #pragma unroll
     for (int m = 0; m < 4; ++m) xv[m] = (pok[m] && kok) ? *(const frag*)(xp[m] + k0) : zero;
+    if constexpr (!WLDS) {
 #pragma unroll
-    for (int f = 0; f < NB; ++f) wv[f] = *(const frag*)(wr[f] + k0);
+      for (int f = 0; f < NB; ++f) wv[f] = *(const frag*)(wr[f] + k0);
+    }
   };
   load(0, xa, wa);
   for (int k0 = 0; k0 < cin_pad; k0 += 32) {
     frag xn[4], wn[NB];
     const bool more = k0 + 32 < cin_pad;
     if (more) load(k0 + 32, xn, wn);
+    if constexpr (WLDS) {
+#pragma unroll
+      for (int f = 0; f < NB; ++f) wa[f] = *(const frag*)(gh_smem + ((f * nk + (k0 >> 5)) * 64 + lane) * 16);
+    }
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -465,8 +510,10 @@ __global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args 
     if (more) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) xa[m] = xn[m];
+      if constexpr (!WLDS) {
 #pragma unroll
-      for (int f = 0; f < NB; ++f) wa[f] = wn[f];
+        for (int f = 0; f < NB; ++f) wa[f] = wn[f];
+      }
     }
   }
   // ---- epilogue: bias, activation, 8-byte stores of 4 channels; zero the pad channels ----------
@@ -514,13 +561,23 @@ static bool nhwc_fast_ok(const kad_gemm_args& a) {
          ((uintptr_t)a.out % 8) == 0;
 }
 
+#ifndef KAD_GH_WLDS_KB
+#define KAD_GH_WLDS_KB 64
+#endif
 template <typename T, int NB>
 static void launch_gemm_nhwc_nb(const kad_gemm_args& a, hipStream_t st) {
-  const int P = a.h * a.w;
+  const int P = a.h * a.w, cin_pad = round_up(a.cin, 32);
   const int tiles_px = ceil_div(P, GH_PXW), co_blocks = ceil_div(round_up(a.cout, 8), NB * 16);
   const int total = a.n * tiles_px * co_blocks;
-  hipLaunchKernelGGL((gemm_nhwc_kernel<T, NB>), dim3(ceil_div(total, GH_WAVES)), dim3(64 * GH_WAVES), 0, st, a, P,
-                     tiles_px, co_blocks, total, round_up(a.cin, 32));
+  const size_t wlds = (size_t)NB * (cin_pad / 32) * 1024;  // the block's weight fragments
+  if (wlds <= (size_t)KAD_GH_WLDS_KB * 1024) {
+    allow_lds(gemm_nhwc_kernel<T, NB, true>, wlds);
+    hipLaunchKernelGGL((gemm_nhwc_kernel<T, NB, true>), dim3(co_blocks * round_up(ceil_div(a.n * tiles_px, GH_WAVES), 8)),
+                       dim3(64 * GH_WAVES), wlds, st, a, P, tiles_px, co_blocks, total, cin_pad);
+  } else {
+    hipLaunchKernelGGL((gemm_nhwc_kernel<T, NB, false>), dim3(ceil_div(total, GH_WAVES)), dim3(64 * GH_WAVES), 0, st,
+                       a, P, tiles_px, co_blocks, total, cin_pad);
+  }
 }
 
 // Output-channel fragments per wave: the fewest padded columns plus 16 per channel block (each

@@ -136,6 +136,73 @@ __global__ __launch_bounds__(256) void ddetect_decode_kernel(kad_decode_args a, 
   for (int k = 0; k < a.nc; ++k) y[(4 + k) * A] = from_f32<T>(sigmoidf_(to_f32(h[a.box_ch + k])));
 }
 
+// The same decode when reg_max is 16 and every level's anchor records are whole 16-byte pieces
+// (head_cs and box_ch multiples of 16 bytes, 16-byte aligned maps): the thread fetches its anchor's
+// box logits with 4 * 16 / V 16-byte loads issued together and its class logits up to 4 pieces
+// at a time, instead of one element per load (records are head_cs elements apart, so an
+// element-wise load touches a different cache line in every lane).  Arithmetic as above, in the
+// same order.
+template <typename T>
+__global__ __launch_bounds__(256) void ddetect_decode_vec_kernel(kad_decode_args a, int total_anchors) {
+  constexpr int V = 16 / (int)sizeof(T), REG = 16, NBV = 4 * REG / V, CU = 4;
+  typedef T piece[V];
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= (int64_t)a.n * total_anchors) return;
+  const int n = (int)(i / total_anchors);
+  int anc = (int)(i - (int64_t)n * total_anchors);
+  int l = 0;
+  while (l + 1 < a.nl && anc >= a.anchor_off[l + 1]) ++l;
+  const int cell = anc - a.anchor_off[l];
+  const int cx = cell % a.lw[l], cy = cell / a.lw[l];
+  const T* h = (const T*)a.head[l] + ((int64_t)n * a.lh[l] * a.lw[l] + cell) * a.head_cs[l];
+  intx4 bv[NBV];
+#pragma unroll
+  for (int q = 0; q < NBV; ++q) bv[q] = *(const intx4*)(h + q * V);
+  float d[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float x[REG];
+#pragma unroll
+    for (int b = 0; b < REG; ++b) x[b] = to_f32(__builtin_bit_cast(piece, bv[(j * REG + b) / V])[(j * REG + b) % V]);
+    float m = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < REG; ++b) m = fmaxf(m, x[b]);
+    float s = 0.f, e = 0.f;
+#pragma unroll
+    for (int b = 0; b < REG; ++b) {
+      const float p = __expf(x[b] - m);
+      s += p;
+      e += p * (float)b;
+    }
+    d[j] = e / s;
+  }
+  const float st = a.stride[l];
+  const float ax = (float)cx + 0.5f, ay = (float)cy + 0.5f;
+  const float x1 = ax - d[0], y1 = ay - d[1], x2 = ax + d[2], y2 = ay + d[3];
+  T* y = (T*)a.out + (int64_t)n * (4 + a.nc) * total_anchors + anc;
+  const int64_t A = total_anchors;
+  y[0] = from_f32<T>((x1 + x2) * 0.5f * st);
+  y[A] = from_f32<T>((y1 + y2) * 0.5f * st);
+  y[2 * A] = from_f32<T>((x2 - x1) * st);
+  y[3 * A] = from_f32<T>((y2 - y1) * st);
+  const T* hc = h + a.box_ch;
+  const int ncv = a.nc - a.nc % V;  // classes in whole pieces
+  for (int k0 = 0; k0 < ncv; k0 += CU * V) {
+    intx4 cv[CU];
+#pragma unroll
+    for (int u = 0; u < CU; ++u)
+      if (k0 + u * V < ncv) cv[u] = *(const intx4*)(hc + k0 + u * V);
+#pragma unroll
+    for (int u = 0; u < CU; ++u) {
+      if (k0 + u * V >= ncv) break;
+      const auto pc = __builtin_bit_cast(piece, cv[u]);
+#pragma unroll
+      for (int e = 0; e < V; ++e) y[(4 + k0 + u * V + e) * A] = from_f32<T>(sigmoidf_(to_f32(pc[e])));
+    }
+  }
+  for (int k = ncv; k < a.nc; ++k) y[(4 + k) * A] = from_f32<T>(sigmoidf_(to_f32(hc[k])));
+}
+
 // ---- NMS --------------------------------------------------------------------------------------
 // boxes [n][4] fp32 (x1, y1, x2, y2), sorted by descending score.  Block (col block
 // cb, row block rb) with cb >= rb: thread t owns row i = 64 rb + t and sets bit j
@@ -247,10 +314,22 @@ extern "C" int kad_ddetect_decode(const kad_decode_args* a, void* stream) {
   KAD_CHECK_ARG(threads < (1ll << 31), "kad_ddetect_decode: too many anchors");
   hipStream_t st = (hipStream_t)stream;
   const int blocks = (int)((threads + 255) / 256);
+  const int V = a->dtype == KAD_F32 ? 4 : 8;  // elements per 16-byte piece
+  bool vec = a->reg_max == 16 && a->box_ch % V == 0;
+  for (int l = 0; l < a->nl; ++l) vec = vec && a->head_cs[l] % V == 0 && ((uintptr_t)a->head[l] & 15) == 0;
   switch (a->dtype) {
-    case KAD_F32: hipLaunchKernelGGL(ddetect_decode_kernel<float>, dim3(blocks), dim3(256), 0, st, *a, total); break;
-    case KAD_F16: hipLaunchKernelGGL(ddetect_decode_kernel<half_t>, dim3(blocks), dim3(256), 0, st, *a, total); break;
-    case KAD_BF16: hipLaunchKernelGGL(ddetect_decode_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, *a, total); break;
+    case KAD_F32:
+      if (vec) hipLaunchKernelGGL(ddetect_decode_vec_kernel<float>, dim3(blocks), dim3(256), 0, st, *a, total);
+      else hipLaunchKernelGGL(ddetect_decode_kernel<float>, dim3(blocks), dim3(256), 0, st, *a, total);
+      break;
+    case KAD_F16:
+      if (vec) hipLaunchKernelGGL(ddetect_decode_vec_kernel<half_t>, dim3(blocks), dim3(256), 0, st, *a, total);
+      else hipLaunchKernelGGL(ddetect_decode_kernel<half_t>, dim3(blocks), dim3(256), 0, st, *a, total);
+      break;
+    case KAD_BF16:
+      if (vec) hipLaunchKernelGGL(ddetect_decode_vec_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, *a, total);
+      else hipLaunchKernelGGL(ddetect_decode_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, *a, total);
+      break;
     default: return fail(KAD_EINVAL, "kad_ddetect_decode: unknown dtype %d", a->dtype);
   }
   return check_launch("kad_ddetect_decode");

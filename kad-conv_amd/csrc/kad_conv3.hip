@@ -315,24 +315,38 @@ void cv_pick_tile(int ho, int wo, int* th_out, int* tw_out) {
   *tw_out = btw;
 }
 
-// Output-channel fragments per wave: the fewest padded columns (ceil(Cout / 32 NBW) blocks of 32 NBW),
-// ties to the larger NBW (fewer column blocks, each re-staging the footprint).  A stride-1 launch of
-// fewer than 1024 blocks then narrows its column blocks until it has 1024 (or NBW = 1): at 50^2 and
-// 25^2 the patches alone leave most CUs idle (96 -> 96 at 50^2: 24.3 -> 20.2 us; 144 -> 144 at 25^2:
-// 23.1 -> 16.7 us).  Stride 2 keeps its blocks: each would re-stage a footprint four times the patch
-// (216 -> 288 at 50^2: 25.9 -> 37.3 us narrowed).
+// Output-channel fragments per wave (column blocks of 32 NBW channels).  Measured at batch 16, fp16
+// (us for NBW = 1 .. 5):
+//  * stride 1: NBW <= 2 keeps two blocks per CU, wider blocks one, so NBW = 2 wins broadly
+//    (144 -> 208 at 100^2: 214 162 224 182 218; 216 -> 208 at 50^2: 79 61 80 72 85; 144 -> 144 at
+//    25^2: 17.0 13.7 16.7 20.2 23.0).  Exceptions: Cout <= 96 where NBW = 2 pads more columns than
+//    NBW = 1 (96 -> 96 at 50^2: 20.5 21.9; 32 -> 32 at 200^2: 41 70); one column block of 3 - 5
+//    fragments on a launch of >= 1024 patches (144 -> 144 at 100^2: 163 135 154 180 116); and a small
+//    launch that NBW = 3 fits in one block per CU where NBW = 2 would not (288 -> 208 at 25^2:
+//    35.7 30.9 24.7 29.4 34.1).
+//  * stride 2: every column block re-stages a footprint four times its patch, so the cost counts the
+//    padded columns plus 32 per column block, ties to the narrower block, and a launch of fewer than
+//    200 blocks narrows its column blocks (144 -> 216 at 100^2: 91 87 80 67.5 79; 216 -> 144 at 50^2:
+//    25.0 20.5 22.8 26.8 30.3).
 int cv_pick_nbw(int cout, long tiles, int stride) {
-  int best = 1;
-  long best_cost = -1;
-  for (int nbw = 1; nbw <= 5; ++nbw) {
-    const long cost = (long)ceil_div(cout, 32 * nbw) * 32 * nbw;
-    if (best_cost < 0 || cost <= best_cost) {
-      best_cost = cost;
-      best = nbw;
+  if (stride != 1) {
+    int best = 1;
+    long best_cost = -1;
+    for (int nbw = 1; nbw <= 5; ++nbw) {
+      const long cb = ceil_div(cout, 32 * nbw), cost = cb * 32 * nbw + 32 * cb;
+      if (best_cost < 0 || cost < best_cost) {
+        best_cost = cost;
+        best = nbw;
+      }
     }
+    while (best > 1 && tiles * ceil_div(cout, 32 * best) < 200) --best;
+    return best;
   }
-  while (stride == 1 && best > 1 && tiles * ceil_div(cout, 32 * best) < 1024) --best;
-  return best;
+  if (cout <= 96 && round_up(cout, 64) > round_up(cout, 32)) return 1;
+  const int nb1 = ceil_div(cout, 32);
+  if (nb1 >= 3 && nb1 <= 5 && tiles >= 1024) return nb1;
+  if (tiles * ceil_div(cout, 64) > 256 && tiles * ceil_div(cout, 96) <= 256) return 3;
+  return 2;
 }
 
 template <typename T, int S>

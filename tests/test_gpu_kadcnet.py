@@ -104,16 +104,20 @@ def test_conv3x3_fwd(dt, cin, cout, stride, groups, act):
 
 
 @pytest.mark.parametrize('dt', ['f16', 'bf16'])
-@pytest.mark.parametrize('cin,cout,stride,H,W', [(144, 208, 1, 50, 50), (72, 144, 2, 64, 72), (40, 72, 1, 37, 101),
-                                                 (216, 96, 2, 26, 30), (64, 36, 1, 100, 9)])
-def test_conv3x3_fwd_many_tiles(dt, cin, cout, stride, H, W):
-    """kad_conv_fwd's implicit-GEMM kernel over many patches and both column-block counts,
+@pytest.mark.parametrize('cin,cout,stride,N,H,W', [
+    (144, 208, 1, 2, 50, 50), (72, 144, 2, 2, 64, 72), (40, 72, 1, 2, 37, 101), (216, 96, 2, 2, 26, 30),
+    (64, 36, 1, 2, 100, 9),
+    # launches whose column blocks are 3, 4 and 5 fragments wide (stride 1: 1024 patches with one
+    # column block, a 100-patch launch; stride 2: 100 - 200 patches)
+    (32, 144, 1, 8, 128, 128), (32, 112, 1, 8, 128, 128), (32, 192, 1, 20, 25, 25), (64, 216, 2, 5, 100, 100),
+    (64, 144, 2, 10, 100, 100), (64, 288, 2, 14, 50, 50)])
+def test_conv3x3_fwd_many_tiles(dt, cin, cout, stride, N, H, W):
+    """kad_conv_fwd's implicit-GEMM kernel over many patches and every column-block width,
     against F.conv2d in float64; the output's channel stride (cout + 4) is not a multiple of 8
     for cout = 36 / 72 ... so the element-store path runs too."""
     from kadconv import _ext
     dtype, dev = DT[dt], 'cuda'
     g = torch.Generator().manual_seed(cin + cout + H)
-    N = 2
     w = torch.randn(cout, cin, 3, 3, generator=g) / (9 * cin) ** 0.5
     b = torch.randn(cout, generator=g) * 0.1
     xq = torch.randn(N, H, W, cin, generator=g).to(dtype)
@@ -123,7 +127,7 @@ def test_conv3x3_fwd_many_tiles(dt, cin, cout, stride, H, W):
     Ho, Wo = (H - 1) // stride + 1, (W - 1) // stride + 1
     out = torch.full((N, Ho, Wo, cout + 4), 3.0, dtype=dtype, device=dev)
     wp = _ext.dcn_pack_weights(w.to(dev, dtype), dtype)
-    print(f'conv3x3 tiles {dt} {cin}->{cout} s{stride} {H}x{W}', flush=True)
+    print(f'conv3x3 tiles {dt} {cin}->{cout} s{stride} {N}x{H}x{W}', flush=True)
     _ext.conv_fwd(x.to(dev)[..., :cin], cin, wp, cout, out[..., :cout], stride=stride, bias=b.to(dev),
                   act=_ext.KAD_ACT_SILU)
     torch.cuda.synchronize()

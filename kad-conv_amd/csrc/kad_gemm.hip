@@ -580,32 +580,34 @@ static void launch_gemm_nhwc_nb(const kad_gemm_args& a, hipStream_t st) {
   }
 }
 
-// Output-channel fragments per wave: the fewest padded columns plus 16 per channel block (each
-// re-reads the pixel fragments), ties to the larger NB.  NB <= 5: from NB = 6 the accumulators and
-// the prefetched fragments take more than 256 registers, one wave per SIMD, and the loads' latency
-// is no longer hidden (NB = 8 measured 1.1-1.8x slower than NB = 4 or 5 at the KAD-CNet-S shapes).
-static int nhwc_pick_nb(int cout, long tiles) {
-  static const int cand[] = {1, 2, 3, 4, 5};
-  const int c8 = round_up(cout, 8);
+// Output-channel fragments per wave (channel blocks of 16 NB): the fewest padded columns plus 16
+// per channel block, among the widths whose weight fragments fit the LDS staging (NB x Cin_pad / 32
+// KB <= 64), ties to the narrower block; then a launch of fewer than 200 blocks narrows its channel
+// blocks.  Measured at batch 16, fp16 (us for NB = 1 .. 5): 512 -> 288 at 25^2: 28.7 23.2 18.3 19.6
+// 28.5 (NB = 5 does not fit the staging); 384 -> 216 at 50^2: 59.7 43.7 37.2 33.9 28.9; 256 -> 144
+// at 100^2: 104.9 73.4 53.8 61.5 57.9; 432 -> 256 at 25^2: 21.1 16.5 15.8 16.8 20.9.  NB <= 5: from
+// NB = 6 the accumulators and the prefetched fragments take more than 256 registers, one wave per
+// SIMD, and the loads' latency is no longer hidden (NB = 8 measured 1.1-1.8x slower than 4 or 5).
+static int nhwc_pick_nb(int cout, int cin_pad, long tiles) {
+  const int c8 = round_up(cout, 8), nk = cin_pad / 32;
   int best = 1;
   long best_cost = -1;
-  for (int nb : cand) {
+  for (int nb = 1; nb <= 5; ++nb) {
+    if (nb > 1 && (long)nb * nk * 1024 > (long)KAD_GH_WLDS_KB * 1024) break;
     const int blocks = ceil_div(c8, nb * 16);
     const long cost = (long)blocks * nb * 16 + 16L * blocks;
-    if (best_cost < 0 || cost <= best_cost) {
+    if (best_cost < 0 || cost < best_cost) {
       best_cost = cost;
       best = nb;
     }
   }
-  // a launch of fewer than 2048 wave items (512 blocks) narrows its channel blocks: the 25^2 / 50^2
-  // layers of KAD-CNet-S otherwise leave most CUs idle (whole network 7.13 -> 7.05 ms)
-  while (best > 1 && tiles * ceil_div(c8, best * 16) < 2048) --best;
+  while (best > 1 && ceil_div(tiles, GH_WAVES) * ceil_div(c8, best * 16) < 200) --best;
   return best;
 }
 
 template <typename T>
 static int launch_gemm_nhwc(const kad_gemm_args& a, hipStream_t st) {
-  switch (nhwc_pick_nb(a.cout, (long)a.n * ceil_div(a.h * a.w, GH_PXW))) {
+  switch (nhwc_pick_nb(a.cout, round_up(a.cin, 32), (long)a.n * ceil_div(a.h * a.w, GH_PXW))) {
     case 1: launch_gemm_nhwc_nb<T, 1>(a, st); break;
     case 2: launch_gemm_nhwc_nb<T, 2>(a, st); break;
     case 3: launch_gemm_nhwc_nb<T, 3>(a, st); break;

@@ -205,12 +205,18 @@ def test_gemm1x1_into_slice(dt):
 @pytest.mark.parametrize('dt', ['f16', 'bf16'])
 @pytest.mark.parametrize('n,p,cin,cout,act', [(2, 1000, 8, 20, 'silu'), (1, 4096, 72, 64, 'silu'),
                                               (3, 130, 360, 300, 'none'), (2, 77, 504, 192, 'silu'),
-                                              (1, 64, 64, 84, 'none')])
+                                              (1, 64, 64, 84, 'none'),
+                                              # channel blocks of 2, 3, 4 and 5 fragments; weights too
+                                              # large for the LDS staging (Cin 2080)
+                                              (16, 4096, 64, 32, 'silu'), (8, 4096, 256, 144, 'silu'),
+                                              (8, 4096, 144, 128, 'none'), (16, 4096, 128, 72, 'silu'),
+                                              (1, 256, 2080, 40, 'silu')])
 def test_gemm1x1_nhwc_fast_path(dt, n, p, cin, cout, act):
     """The NHWC MFMA path of kad_gemm1x1_fwd: input read from a slice whose
     neighbouring channels hold NaN (channels past Cin inside a k-step must not be
     used), ragged pixel counts, Cout not a multiple of 16, several 128-channel
-    blocks; output into a slice, its pad channels zeroed and the rest untouched."""
+    blocks, every channel-block width; output into a slice, its pad channels zeroed
+    and the rest untouched."""
     from kadconv import _ext
     dtype, dev = DT[dt], 'cuda'
     g = torch.Generator().manual_seed(p + cin + cout)

@@ -791,17 +791,33 @@ __global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
 // whose window holds it; a branch at the output's resolution is read at the pixel itself (it may be
 // the output's own channel slice: the thread reads it before writing the same 16 bytes), an
 // upsampled one through its four bilinear corners, whose row / column indices are computed once
-// per thread and branch.  Lets a channels-last KAD-Conv merge all its branches in one launch.
+// per thread and branch.  Lets a channels-last KAD-Conv merge all its branches in one launch.  A
+// branch whose window covers the thread's 8 channels as one aligned 16-byte piece of its map
+// (channel offset and stride multiples of 8) is read with one vector load per corner; others
+// element by element.  Index arithmetic in 32 bits when the launch has fewer than 2^32 items.
 template <typename T>
 __global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, int64_t npix, int ngroups) {
   typedef Vec8<T> V;
   const int64_t total = npix * ngroups;
+  const bool i32 = total < ((int64_t)1 << 32);
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int grp = (int)(i % ngroups);
-    const int64_t p = i / ngroups;
-    const int x = (int)(p % a.w);
-    const int64_t t = p / a.w;
-    const int y = (int)(t % a.h), n = (int)(t / a.h);
+    int grp, x, y, n;
+    int64_t p;
+    if (i32) {
+      const uint32_t ii = (uint32_t)i, pp = ii / (uint32_t)ngroups, tt = pp / (uint32_t)a.w;
+      grp = (int)(ii - pp * (uint32_t)ngroups);
+      x = (int)(pp - tt * (uint32_t)a.w);
+      n = (int)(tt / (uint32_t)a.h);
+      y = (int)(tt - (uint32_t)n * (uint32_t)a.h);
+      p = pp;
+    } else {
+      grp = (int)(i % ngroups);
+      p = i / ngroups;
+      x = (int)(p % a.w);
+      const int64_t t = p / a.w;
+      y = (int)(t % a.h);
+      n = (int)(t / a.h);
+    }
     const int c0 = a.c_begin + 8 * grp;
     const int64_t oi = p * a.c + c0;
     float v[8];
@@ -827,6 +843,30 @@ __global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, i
       const int cs = a.br_cs[b], bw = a.br_w[b];
       const T* r0 = z + (int64_t)y0 * bw * cs;
       const T* r1 = z + (int64_t)y1 * bw * cs;
+      if (lo <= c0 && c0 + 8 <= hi && ((c0 - lo) & 7) == 0 && (cs & 7) == 0 && ((uintptr_t)a.br_z[b] & 15) == 0) {
+        const int cb = c0 - lo;
+        float s[8];
+        if (same) {
+          const V q = *(const V*)(r0 + (int64_t)x * cs + cb);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s[e] = to_f32(q.v[e]);
+        } else {
+          const V q00 = *(const V*)(r0 + (int64_t)x0 * cs + cb), q01 = *(const V*)(r0 + (int64_t)x1 * cs + cb);
+          const V q10 = *(const V*)(r1 + (int64_t)x0 * cs + cb), q11 = *(const V*)(r1 + (int64_t)x1 * cs + cb);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float v00 = to_f32(q00.v[e]), v01 = to_f32(q01.v[e]);
+            const float v10 = to_f32(q10.v[e]), v11 = to_f32(q11.v[e]);
+            s[e] = (1.f - ly) * ((1.f - lx) * v00 + lx * v01) + ly * ((1.f - lx) * v10 + lx * v11);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (att) s[e] *= att[cb + e];
+          v[e] += coeff * s[e];
+        }
+        continue;
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int c = c0 + e;

@@ -16,6 +16,8 @@
 // computes the builder-defined KADDown mixture.
 #include "kad_common.h"
 
+#include <type_traits>
+
 namespace kad {
 
 // ---- SE pool: per-(n, c) plane means, one wave per plane (NCHW) ----------------------------
@@ -786,40 +788,28 @@ __global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
   }
 }
 
-// NHWC output, window and channel count multiples of 8: one thread per (pixel, 8-channel group),
-// 16-byte loads of the residual and 16-byte stores.  Each channel takes its value from the branch
-// whose window holds it; a branch at the output's resolution is read at the pixel itself (it may be
-// the output's own channel slice: the thread reads it before writing the same 16 bytes), an
-// upsampled one through its four bilinear corners, whose row / column indices are computed once
-// per thread and branch.  Lets a channels-last KAD-Conv merge all its branches in one launch.  A
-// branch whose window covers the thread's 8 channels as one aligned 16-byte piece of its map
-// (channel offset and stride multiples of 8) is read with one vector load per corner; others
-// element by element.  Index arithmetic in 32 bits when the launch has fewer than 2^32 items.
+// NHWC output, window and channel count multiples of 8.  A block takes 64 pixels; its wave w the
+// 8-channel groups w, w + 4, ... of them, a lane per pixel, so the group -- which branches cover it,
+// at which channel offset -- is the same across the wave (scalar branches, no divergence), while
+// the block's other waves read the other groups of the same pixels' lines.  16-byte loads of the
+// residual and 16-byte stores.  Each channel takes its value from the branch whose window holds it;
+// a branch at the output's resolution is read at the pixel itself (it may be the output's own
+// channel slice: the wave reads it before writing the same 16 bytes), an upsampled one through its
+// four bilinear corners.  A branch map whose channel stride is a multiple of 8 is read in aligned
+// 8-element pieces (one or two vector loads per corner, whatever the window's offset; a piece is
+// read only when it holds a channel of the window, so it lies in a mapped page); others element by
+// element.  Lets a channels-last KAD-Conv merge all its branches in one launch.
 template <typename T>
-__global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, int64_t npix, int ngroups) {
+__global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, int npix, int ngroups) {
   typedef Vec8<T> V;
-  const int64_t total = npix * ngroups;
-  const bool i32 = total < ((int64_t)1 << 32);
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    int grp, x, y, n;
-    int64_t p;
-    if (i32) {
-      const uint32_t ii = (uint32_t)i, pp = ii / (uint32_t)ngroups, tt = pp / (uint32_t)a.w;
-      grp = (int)(ii - pp * (uint32_t)ngroups);
-      x = (int)(pp - tt * (uint32_t)a.w);
-      n = (int)(tt / (uint32_t)a.h);
-      y = (int)(tt - (uint32_t)n * (uint32_t)a.h);
-      p = pp;
-    } else {
-      grp = (int)(i % ngroups);
-      p = i / ngroups;
-      x = (int)(p % a.w);
-      const int64_t t = p / a.w;
-      y = (int)(t % a.h);
-      n = (int)(t / a.h);
-    }
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int p = blockIdx.x * 64 + (int)(threadIdx.x & 63);
+  if (p >= npix) return;
+  const int x = p % a.w, t = p / a.w;
+  const int y = t % a.h, n = t / a.h;
+  for (int grp = wave; grp < ngroups; grp += 4) {
     const int c0 = a.c_begin + 8 * grp;
-    const int64_t oi = p * a.c + c0;
+    const int64_t oi = (int64_t)p * a.c + c0;
     float v[8];
     if (a.residual) {
       const V r = *(const V*)((const T*)a.residual + oi);
@@ -843,45 +833,70 @@ __global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, i
       const int cs = a.br_cs[b], bw = a.br_w[b];
       const T* r0 = z + (int64_t)y0 * bw * cs;
       const T* r1 = z + (int64_t)y1 * bw * cs;
-      if (lo <= c0 && c0 + 8 <= hi && ((c0 - lo) & 7) == 0 && (cs & 7) == 0 && ((uintptr_t)a.br_z[b] & 15) == 0) {
-        const int cb = c0 - lo;
-        float s[8];
-        if (same) {
-          const V q = *(const V*)(r0 + (int64_t)x * cs + cb);
+      const int d = c0 - lo;  // branch channel of the group's first channel (may be negative)
+      const int ea = lo > c0 ? lo - c0 : 0, eb = hi < c0 + 8 ? hi - c0 : 8;  // valid e: [ea, eb)
+      if ((cs & 7) == 0 && ((uintptr_t)a.br_z[b] % sizeof(T)) == 0) {
+        // channels d .. d + 7 sit OFF elements into an aligned 8-element piece of the map, the same
+        // OFF for every pixel
+        const int mis = (int)(((uintptr_t)a.br_z[b] / sizeof(T) + (uintptr_t)(int64_t)d) & 7);
+        auto body = [&](auto off_tag) {
+          constexpr int OFF = decltype(off_tag)::value;
+          const bool need0 = ea < 8 - OFF, need1 = OFF > 0 && eb > 8 - OFF;
+          auto corner = [&](const T* px, float* r) {  // px: branch channel d of the corner pixel
+            const T* al = px - OFF;
+            V q0{}, q1{};
+            if (need0) q0 = *(const V*)al;
+            if (need1) q1 = *(const V*)(al + 8);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) s[e] = to_f32(q.v[e]);
-        } else {
-          const V q00 = *(const V*)(r0 + (int64_t)x0 * cs + cb), q01 = *(const V*)(r0 + (int64_t)x1 * cs + cb);
-          const V q10 = *(const V*)(r1 + (int64_t)x0 * cs + cb), q11 = *(const V*)(r1 + (int64_t)x1 * cs + cb);
+            for (int e = 0; e < 8; ++e) r[e] = to_f32(OFF + e < 8 ? q0.v[(OFF + e) & 7] : q1.v[(OFF + e) & 7]);
+          };
+          float sv[8];
+          if (same) {
+            corner(r0 + (int64_t)x * cs + d, sv);
+          } else {
+            float c00[8], c01[8], c10[8], c11[8];
+            corner(r0 + (int64_t)x0 * cs + d, c00);
+            corner(r0 + (int64_t)x1 * cs + d, c01);
+            corner(r1 + (int64_t)x0 * cs + d, c10);
+            corner(r1 + (int64_t)x1 * cs + d, c11);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              sv[e] = (1.f - ly) * ((1.f - lx) * c00[e] + lx * c01[e]) + ly * ((1.f - lx) * c10[e] + lx * c11[e]);
+          }
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            const float v00 = to_f32(q00.v[e]), v01 = to_f32(q01.v[e]);
-            const float v10 = to_f32(q10.v[e]), v11 = to_f32(q11.v[e]);
-            s[e] = (1.f - ly) * ((1.f - lx) * v00 + lx * v01) + ly * ((1.f - lx) * v10 + lx * v11);
+            if (e < ea || e >= eb) continue;
+            float se = sv[e];
+            if (att) se *= att[d + e];
+            v[e] += coeff * se;
           }
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (att) s[e] *= att[cb + e];
-          v[e] += coeff * s[e];
+        };
+        switch (mis) {
+          case 0: body(std::integral_constant<int, 0>{}); break;
+          case 1: body(std::integral_constant<int, 1>{}); break;
+          case 2: body(std::integral_constant<int, 2>{}); break;
+          case 3: body(std::integral_constant<int, 3>{}); break;
+          case 4: body(std::integral_constant<int, 4>{}); break;
+          case 5: body(std::integral_constant<int, 5>{}); break;
+          case 6: body(std::integral_constant<int, 6>{}); break;
+          default: body(std::integral_constant<int, 7>{}); break;
         }
         continue;
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int c = c0 + e;
-        if (c < lo || c >= hi) continue;
-        const int cb = c - lo;
-        float s;
+        if (e < ea || e >= eb) continue;
+        const int cb = d + e;
+        float sv;
         if (same) {
-          s = to_f32(r0[(int64_t)x * cs + cb]);
+          sv = to_f32(r0[(int64_t)x * cs + cb]);
         } else {
           const float v00 = to_f32(r0[(int64_t)x0 * cs + cb]), v01 = to_f32(r0[(int64_t)x1 * cs + cb]);
           const float v10 = to_f32(r1[(int64_t)x0 * cs + cb]), v11 = to_f32(r1[(int64_t)x1 * cs + cb]);
-          s = (1.f - ly) * ((1.f - lx) * v00 + lx * v01) + ly * ((1.f - lx) * v10 + lx * v11);
+          sv = (1.f - ly) * ((1.f - lx) * v00 + lx * v01) + ly * ((1.f - lx) * v10 + lx * v11);
         }
-        if (att) s *= att[cb];
-        v[e] += coeff * s;
+        if (att) sv *= att[cb];
+        v[e] += coeff * sv;
       }
     }
     V o;
@@ -1437,11 +1452,10 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
       default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
     }
   } else if (a->c % 8 == 0 && a->c_begin % 8 == 0 && a->c_end % 8 == 0 && ((uintptr_t)a->out % 16) == 0 &&
-             ((uintptr_t)a->residual % 16) == 0) {
-    const int64_t npix = (int64_t)a->n * a->h * a->w;
+             ((uintptr_t)a->residual % 16) == 0 && (int64_t)a->n * a->h * a->w < ((int64_t)1 << 31) - 64) {
+    const int npix = a->n * a->h * a->w;
     const int ngroups = (a->c_end - a->c_begin) / 8;
-    const int64_t total = npix * ngroups;
-    const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+    const int blocks = ceil_div(npix, 64);
     switch (a->dtype) {
       case KAD_F32: hipLaunchKernelGGL(merge_nhwc_vec_kernel<float>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;
       case KAD_F16: hipLaunchKernelGGL(merge_nhwc_vec_kernel<half_t>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;

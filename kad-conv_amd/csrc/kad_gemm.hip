@@ -396,19 +396,20 @@ __global__ void gemm_pack_kernel(const float* w, T* out, int cin, int cout, int 
 
 // ---- NHWC fast path ---------------------------------------------------------------------------------
 // 16-bit NHWC input and output, no pooling, Cin a multiple of 8 (whole 16-byte channel pieces).
-// In NHWC both MFMA operands are contiguous 16-byte runs, so a wave loads them straight from
-// memory into registers, with no LDS staging and no barriers:
-//  * A = weights, 16 output channels x 32 input channels: lane (r, g) reads row r's input
-//    channels 8g .. 8g + 7 of the packed [Cout_pad][Cin_pad] rows (L2-resident, shared by all waves);
-//  * B = input, 32 input channels x 16 pixels: lane (c, g) reads pixel c's channels 8g .. 8g + 7
-//    (four lanes cover a pixel's 64 contiguous bytes of the k-step).
+// In NHWC both MFMA operands are contiguous 16-byte runs:
+//  * A = weights, 16 output channels x 32 input channels: lane (r, g) holds row r's input
+//    channels 8g .. 8g + 7, from the block's copy of its fragment-ordered weights in LDS (WLDS:
+//    one copy per block, one barrier), else straight from the packed [Cout_pad][Cin_pad] rows;
+//  * B = input, 32 input channels x 16 pixels: lane (c, g) loads pixel c's channels 8g .. 8g + 7
+//    straight from memory into registers (four lanes cover a pixel's 64 contiguous bytes of the
+//    k-step).
 // A wave owns 64 pixels (4 pixel fragments) x 16 NB output channels.  The accumulator of
 // (pixel fragment m, channel fragment f) in lane (c, g) holds output channels 16 f + 4 g .. + 3
 // of pixel 16 m + c: one 8-byte store.  The next k-step's operands are loaded before this step's
 // MFMAs.  Input channels past Cin inside a k-step are read as 0 (they may belong to another slice
 // of a concat buffer); weight rows past Cout are zero in the packing.
 constexpr int GH_PXW = 64;    // pixels per wave
-constexpr int GH_WAVES = 4;   // waves per block (independent work items)
+constexpr int GH_WAVES = 4;   // waves per block
 
 // WLDS: the block's four waves share one channel block and take four pixel tiles; the block first
 // copies its weight fragments (the packing's fragment-ordered part: NB x Cin_pad / 32 chunks of

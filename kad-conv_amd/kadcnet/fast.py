@@ -192,7 +192,7 @@ class _GELAN:
         self.c4 = self.stages[0][1].cout
         self.cv4 = _ConvOp.from_conv_module(m.cv4)
 
-    def __call__(self, x):
+    def __call__(self, x, out=None):
         N, H, W = x.shape[:3]
         ctot = self.c3 + 2 * self.c4
         cat = x.new_empty(N, H, W, ctot)
@@ -205,18 +205,18 @@ class _GELAN:
             conv(t, dst)
             src = dst
             off += self.c4
-        return self.cv4(cat)
+        return self.cv4(cat, out)
 
 
 class _AConv:
     def __init__(self, m):
         self.cv1 = _ConvOp.from_conv_module(m.cv1)
 
-    def __call__(self, x):
+    def __call__(self, x, out=None):
         N, H, W, C = x.shape
         p = x.new_empty(N, H - 1, W - 1, C)
         _ext.nhwc_resample(x, p, C, _ext.KAD_RS_AVG, k=2, s=1, p=0)
-        return self.cv1(p)
+        return self.cv1(p, out)
 
 
 class _SPPELAN:
@@ -225,7 +225,7 @@ class _SPPELAN:
         self.k = [sp.m.kernel_size for sp in (m.cv2, m.cv3, m.cv4)]
         self.cv5 = _ConvOp.from_conv_module(m.cv5)
 
-    def __call__(self, x):
+    def __call__(self, x, out=None):
         N, H, W = x.shape[:3]
         c = self.cv1.cout
         cat = x.new_empty(N, H, W, 4 * c)
@@ -234,7 +234,7 @@ class _SPPELAN:
             k = k if isinstance(k, int) else k[0]
             _ext.nhwc_resample(cat[..., i * c:(i + 1) * c], cat[..., (i + 1) * c:(i + 2) * c], c, _ext.KAD_RS_MAX,
                                k=k, s=1, p=k // 2)
-        return self.cv5(cat)
+        return self.cv5(cat, out)
 
 
 class _Upsample:
@@ -247,9 +247,10 @@ class _Upsample:
             raise NotImplementedError('nn.Upsample: integer scale factors only')
         self.s = int(sf)
 
-    def __call__(self, x):
+    def __call__(self, x, out=None):
         N, H, W, C = x.shape
-        out = x.new_empty(N, H * self.s, W * self.s, C)
+        if out is None:
+            out = x.new_empty(N, H * self.s, W * self.s, C)
         _ext.nhwc_resample(x, out, C, _ext.KAD_RS_NEAREST, s=self.s)
         return out
 
@@ -327,6 +328,7 @@ class KADCNetPlan:
         self.in_ch = None
         first = self.layers[0][1]
         self.in_ch = first.cin if isinstance(first, _ConvOp) else None
+        self._elide = {}
 
     def eligible(self, x):
         return (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.float16, torch.bfloat16)
@@ -349,12 +351,48 @@ class KADCNetPlan:
             xin = torch.empty(N, H, W, cs, dtype=x.dtype, device=x.device)
             _ext.to_nhwc(x.contiguous(), xin)
             cur = xin[..., :C]
+        key = (tuple(x.shape), x.dtype, x.device)
+        el = self._elide.get(key)
+        bufs = {}
         for f, op in layers:
+            i = len(ys)  # this layer's index in the model
             if f != -1:
                 cur = ys[f] if isinstance(f, int) else [cur if j == -1 else ys[j] for j in f]
-            cur = op(cur)
+            if el is not None and i in el[0]:   # writes its slice of a later Concat's buffer
+                k, off, c = el[0][i]
+                if k not in bufs:
+                    bufs[k] = x.new_empty(el[1][k])
+                cur = op(cur, out=bufs[k][..., off:off + c])
+            elif el is not None and i in el[1]:  # a Concat whose inputs are already in place
+                cur = bufs.pop(i)
+            else:
+                cur = op(cur)
             ys.append(cur)
+        if el is None:
+            self._elide[key] = self._concat_slots(ys)
         return (cur, ys) if keep_layers else cur
+
+    def _concat_slots(self, ys):
+        """From one forward's layer outputs: ({layer i: (Concat layer k, channel offset, channels)},
+        {k: buffer shape}) for every Concat whose inputs can all be written straight into its buffer
+        (each input layer feeding no other Concat), so that later forwards of the same input shape
+        skip the copies.  Other consumers of such an input read its channel slice of the buffer."""
+        slots, shapes = {}, {}
+        for k, (f, op) in enumerate(self.layers):
+            if not isinstance(op, _Concat) or not isinstance(f, (list, tuple)):
+                continue
+            ins = [k - 1 if j == -1 else j for j in f]
+            if (len(set(ins)) != len(ins) or any(j in slots or j == 0 for j in ins)
+                    or not all(isinstance(self.layers[j][1], (_ConvOp, _GELAN, _AConv, _SPPELAN, _Upsample))
+                               for j in ins)):
+                continue
+            off = 0
+            for j in ins:
+                c = ys[j].shape[3]
+                slots[j] = (k, off, c)
+                off += c
+            shapes[k] = tuple(ys[k].shape)
+        return slots, shapes
 
 
 def enable_fast_inference(model, allow_untested_gpu=False):

@@ -307,15 +307,22 @@ def _rel(got, ref):
 def test_kadcnet_plan_matches_oracle(dt, fuse):
     """Whole network, layer by layer, at [2, 3, 256, 192] (non-square; 4 x 3 cells at
     stride 64 under the deepest KAD-Conv branch), unfused (BN folded by the plan)
-    and fused models."""
+    and fused models.  The first forward of an input shape copies Concat inputs into
+    the Concat's buffer; later ones write them there directly: bit-identical."""
     import kadcnet
     dtype = DT[dt]
     m, sd = _model(dtype, seed=1, fuse=fuse)
     x = torch.rand(2, 3, 256, 192, generator=torch.Generator().manual_seed(2)).to(dtype)
     plan = kadcnet.KADCNetPlan(m)
     with torch.no_grad():
+        (y1, heads1), layers1 = plan.forward(x.cuda(), keep_layers=True)
+        y1, heads1, layers1 = y1.clone(), [h.clone() for h in heads1], [t.clone() for t in layers1[:-1]]
         (y, heads), layers = plan.forward(x.cuda(), keep_layers=True)
     torch.cuda.synchronize()
+    slots, bufs = next(iter(plan._elide.values()))
+    assert sorted(bufs) == [11, 14, 17, 20] and sorted(slots) == [4, 6, 9, 10, 12, 13, 16, 19]
+    assert torch.equal(y, y1) and all(torch.equal(a, b) for a, b in zip(heads, heads1))
+    assert all(torch.equal(a, b) for a, b in zip(layers[:-1], layers1))
     ref_layers = []
     yo, ho = KO.kadcnet_forward(sd, kadcnet.DIOR_S_BASE, x.double(), layers=ref_layers)
     tol = {'f32': 1e-4, 'f16': 1e-2, 'bf16': 5e-2}[dt]

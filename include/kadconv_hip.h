@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KAD_ABI_VERSION 3
+#define KAD_ABI_VERSION 4
 
 /* element types */
 #define KAD_F32 0
@@ -392,6 +392,8 @@ typedef struct kad_merge_args {
   int br_c[KAD_MAX_BRANCHES], br_c_off[KAD_MAX_BRANCHES];
   int br_h[KAD_MAX_BRANCHES], br_w[KAD_MAX_BRANCHES], br_cs[KAD_MAX_BRANCHES];
   float br_coeff[KAD_MAX_BRANCHES];
+  int out_cs, res_cs;      /* NHWC only: pixel strides (elements) of out and residual; 0 = c.  Lets
+                              the output be a channel slice of a wider buffer (a concat).  NCHW: 0 */
 } kad_merge_args;
 
 /* out[n, c] = gate[c] * (residual + sum over branches b with c in [c_off_b, c_off_b + c_b):

@@ -765,8 +765,9 @@ __global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
   const int cw = a.c_end - a.c_begin;
   for (int e = threadIdx.x; e < a.w * cw; e += 256) {
     const int c = a.c_begin + e % cw, x = e / cw;
-    const int64_t oi = (((int64_t)n * a.h + y) * a.w + x) * a.c + c;
-    float v = a.residual ? to_f32(((const T*)a.residual)[oi]) : 0.f;
+    const int64_t pix = ((int64_t)n * a.h + y) * a.w + x;
+    const int64_t oi = pix * a.out_cs + c;
+    float v = a.residual ? to_f32(((const T*)a.residual)[pix * a.res_cs + c]) : 0.f;
     for (int b = 0; b < a.nbranch; ++b) {
       const int cb = c - a.br_c_off[b];
       if (cb < 0 || cb >= a.br_c[b]) continue;
@@ -788,7 +789,7 @@ __global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
   }
 }
 
-// NHWC output, window and channel count multiples of 8.  A block takes 64 pixels; its wave w the
+// NHWC output, channel window and pixel strides multiples of 8.  A block takes 64 pixels; its wave w the
 // 8-channel groups w, w + 4, ... of them, a lane per pixel, so the group -- which branches cover it,
 // at which channel offset -- is the same across the wave (scalar branches, no divergence), while
 // the block's other waves read the other groups of the same pixels' lines.  16-byte loads of the
@@ -809,10 +810,10 @@ __global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, i
   const int y = t % a.h, n = t / a.h;
   for (int grp = wave; grp < ngroups; grp += 4) {
     const int c0 = a.c_begin + 8 * grp;
-    const int64_t oi = (int64_t)p * a.c + c0;
+    const int64_t oi = (int64_t)p * a.out_cs + c0;
     float v[8];
     if (a.residual) {
-      const V r = *(const V*)((const T*)a.residual + oi);
+      const V r = *(const V*)((const T*)a.residual + (int64_t)p * a.res_cs + c0);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = to_f32(r.v[e]);
     } else {
@@ -1383,6 +1384,12 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
   KAD_CHECK_ARG(a_in && a_in->out, "kad_branch_merge: null pointer");
   kad_merge_args win = *a_in;
   if (win.c_begin == 0 && win.c_end == 0) win.c_end = win.c;
+  KAD_CHECK_ARG(win.layout == KAD_NHWC || (win.out_cs == 0 && win.res_cs == 0),
+                "kad_branch_merge: out_cs / res_cs apply to NHWC only");
+  if (win.out_cs == 0) win.out_cs = win.c;
+  if (win.res_cs == 0) win.res_cs = win.c;
+  KAD_CHECK_ARG(win.out_cs >= win.c && win.res_cs >= win.c, "kad_branch_merge: out_cs %d / res_cs %d < c=%d",
+                win.out_cs, win.res_cs, win.c);
   const kad_merge_args* a = &win;
   KAD_CHECK_ARG(a->c_begin >= 0 && a->c_begin < a->c_end && a->c_end <= a->c,
                 "kad_branch_merge: channel window [%d, %d) outside [0, %d)", a->c_begin, a->c_end, a->c);
@@ -1451,8 +1458,9 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
       case KAD_BF16: hipLaunchKernelGGL(merge_nchw_kernel<bf16_t>, grid, dim3(256), 0, st, *a); break;
       default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
     }
-  } else if (a->c % 8 == 0 && a->c_begin % 8 == 0 && a->c_end % 8 == 0 && ((uintptr_t)a->out % 16) == 0 &&
-             ((uintptr_t)a->residual % 16) == 0 && (int64_t)a->n * a->h * a->w < ((int64_t)1 << 31) - 64) {
+  } else if (a->layout == KAD_NHWC && a->out_cs % 8 == 0 && a->res_cs % 8 == 0 && a->c_begin % 8 == 0 &&
+             a->c_end % 8 == 0 && ((uintptr_t)a->out % 16) == 0 && ((uintptr_t)a->residual % 16) == 0 &&
+             (int64_t)a->n * a->h * a->w < ((int64_t)1 << 31) - 64) {
     const int npix = a->n * a->h * a->w;
     const int ngroups = (a->c_end - a->c_begin) / 8;
     const int blocks = ceil_div(npix, 64);

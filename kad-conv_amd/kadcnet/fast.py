@@ -150,9 +150,10 @@ class _KADConvOp:
         self.plan = KADConvPlan(layer)
         self.dim = self.plan.dim
 
-    def __call__(self, x):
-        """x: dense NHWC [N, H, W, dim] -> dense NHWC [N, H, W, dim]."""
-        y = self.plan.forward(x.permute(0, 3, 1, 2))
+    def __call__(self, x, out=None):
+        """x: dense NHWC [N, H, W, dim] -> NHWC [N, H, W, dim] (dense, or out: an NHWC channel
+        slice of a wider buffer)."""
+        y = self.plan.forward(x.permute(0, 3, 1, 2), None if out is None else out.permute(0, 3, 1, 2))
         return y.permute(0, 2, 3, 1)
 
 
@@ -171,9 +172,10 @@ class _RepNCSP:
         cat = x.new_empty(N, H, W, 2 * self.c_)
         self.cv2(x, cat[..., self.c_:])
         y = self.cv1(x)
-        for blk in self.m:
-            y = blk(y)
-        _copy(y, cat)
+        if not self.m:
+            _copy(y, cat)
+        for i, blk in enumerate(self.m):  # the last block writes the concat's first half itself
+            y = blk(y, cat[..., :self.c_] if i == len(self.m) - 1 else None)
         return self.cv3(cat, out)
 
 

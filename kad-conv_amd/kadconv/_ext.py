@@ -19,7 +19,7 @@ _LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libkadconv
 
 KAD_F32, KAD_F16, KAD_BF16 = 0, 1, 2
 KAD_NHWC, KAD_NCHW = 0, 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _DTYPES = {torch.float32: KAD_F32, torch.float16: KAD_F16, torch.bfloat16: KAD_BF16}
 
@@ -82,6 +82,7 @@ class MergeArgs(ctypes.Structure):
         ('br_c', c_int * MAX_BRANCHES), ('br_c_off', c_int * MAX_BRANCHES),
         ('br_h', c_int * MAX_BRANCHES), ('br_w', c_int * MAX_BRANCHES), ('br_cs', c_int * MAX_BRANCHES),
         ('br_coeff', ctypes.c_float * MAX_BRANCHES),
+        ('out_cs', c_int), ('res_cs', c_int),
     ]
 
 
@@ -657,6 +658,10 @@ def branch_merge(out, layout, branches, residual=None, gate=None, channels=None)
         N, C, H, W = out.shape
     else:
         N, H, W, C = out.shape
+        # out / residual may be channel slices of wider NHWC buffers (pixel strides >= C)
+        a.out_cs = _nhwc_cs(out)[3]
+        if residual is not None:
+            a.res_cs = _nhwc_cs(residual)[3]
     a.out, a.residual, a.gate = _ptr(out), _ptr(residual), _ptr(gate)
     a.n, a.c, a.h, a.w, a.layout, a.dtype, a.nbranch = N, C, H, W, layout, kad_dtype(out.dtype), len(branches)
     if channels is not None:

@@ -250,24 +250,32 @@ class KADConvPlan:
         pre, branches, post, out = self.schedule(x)
         return pre + [s for b in branches for s in b] + post, out
 
-    def _io(self, x):
-        """(x view for the kernels, its layout, out, out view, out layout)."""
+    def _io(self, x, out=None):
+        """(x view for the kernels, its layout, out, out view, out layout).  out: for a channels-last
+        x, an NCHW-shaped view of channels-last memory whose pixel stride may exceed C (a channel
+        slice of a wider buffer, e.g. a concat), written in place."""
         nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
         if nhwc:
-            out = torch.empty_like(x, memory_format=torch.channels_last)
+            if out is None:
+                out = torch.empty_like(x, memory_format=torch.channels_last)
+            elif (out.shape != x.shape or out.dtype != x.dtype or out.device != x.device or out.stride(1) != 1
+                  or out.stride(3) < x.shape[1] or out.stride(2) != out.stride(3) * x.shape[3]):
+                raise ValueError('out must be a channels-last view shaped like x (channel stride 1)')
             return x.permute(0, 2, 3, 1), _ext.KAD_NHWC, out, out.permute(0, 2, 3, 1), _ext.KAD_NHWC
+        if out is not None:
+            raise ValueError('out= needs a channels-last input')
         x = x.contiguous()
         out = torch.empty_like(x)
         return x, _ext.KAD_NCHW, out, out, _ext.KAD_NCHW
 
-    def schedule_grouped(self, x):
+    def schedule_grouped(self, x, out=None):
         """The forward as one chain of launches on one stream: the pyramid, then the LCSA
         means, the LCSA masks and the fused DSCs (+ SE) of all branches as one launch each
         (kad_lcsa_prep_group, kad_lcsa_mask_group, kad_dsc_fwd_group), then the merges.
         Returns (stages, out)."""
         N, C, H, W = x.shape
         dev, dtype = x.device, x.dtype
-        xin, in_layout, out, out_v, out_layout = self._io(x)
+        xin, in_layout, out, out_v, out_layout = self._io(x, out)
         ntx, nty = _ext.pyramid_tiles(H, W)
         pyr, lcsa, dcn, keep, merges = [], [], {}, [], []
         edt = _emat_dtype(dtype)
@@ -322,22 +330,14 @@ class KADConvPlan:
                 st.append(('merge', lambda: _ext.branch_merge(out_v, out_layout, up, residual=xin, channels=(lo, hi))))
         return st, out
 
-    def schedule(self, x):
+    def schedule(self, x, out=None):
         """(pre, [per-branch stages], post, out): the branch chains (LCSA, DSC,
         SE, and the merge of the branch's own output channels) only depend on
         `pre` (the pyramid), so forward() runs them on side streams concurrently."""
         N, C, H, W = x.shape
         dev, dtype = x.device, x.dtype
-        nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
-        if nhwc:
-            xin, in_layout = x.permute(0, 2, 3, 1), _ext.KAD_NHWC
-            out = torch.empty_like(x, memory_format=torch.channels_last)
-            out_v, out_layout = out.permute(0, 2, 3, 1), _ext.KAD_NHWC
-        else:
-            x = x.contiguous()
-            xin, in_layout = x, _ext.KAD_NCHW
-            out = torch.empty_like(x)
-            out_v, out_layout = out, _ext.KAD_NCHW
+        xin, in_layout, out, out_v, out_layout = self._io(x, out)
+        x = xin if in_layout == _ext.KAD_NCHW else x
         st = []
         ys, sums = [], []
         pyr = []
@@ -418,16 +418,17 @@ class KADConvPlan:
             self._side = streams
         return streams[key]
 
-    def forward(self, x):
+    def forward(self, x, out=None):
         """Grouped: every stage on the caller's stream.  Else the pyramid on the caller's
         stream, the branch chains forked onto side streams (concurrent on the GPU;
-        HIP-graph capture records the fork/join as graph edges), merge after the join."""
+        HIP-graph capture records the fork/join as graph edges), merge after the join.
+        out: see _io (channels-last input only)."""
         if self._grouped(x):
-            st, out = self.schedule_grouped(x)
+            st, out = self.schedule_grouped(x, out)
             for _, fn in st:
                 fn()
             return out
-        pre, chains, post, out = self.schedule(x)
+        pre, chains, post, out = self.schedule(x, out)
         for _, fn in pre:
             fn()
         main = torch.cuda.current_stream(x.device)

@@ -110,7 +110,9 @@ def test_conv3x3_fwd(dt, cin, cout, stride, groups, act):
     # launches whose column blocks are 3, 4 and 5 fragments wide (stride 1: 1024 patches with one
     # column block, a 100-patch launch; stride 2: 100 - 200 patches)
     (32, 144, 1, 8, 128, 128), (32, 112, 1, 8, 128, 128), (32, 192, 1, 20, 25, 25), (64, 216, 2, 5, 100, 100),
-    (64, 144, 2, 10, 100, 100), (64, 288, 2, 14, 50, 50)])
+    (64, 144, 2, 10, 100, 100), (64, 288, 2, 14, 50, 50),
+    # stride 2 over fewer than 64 channels (the general path), ragged patches
+    (40, 72, 2, 2, 45, 71), (8, 20, 2, 3, 33, 30), (56, 80, 2, 2, 40, 50), (16, 33, 2, 1, 17, 17)])
 def test_conv3x3_fwd_many_tiles(dt, cin, cout, stride, N, H, W):
     """kad_conv_fwd's implicit-GEMM kernel over many patches and every column-block width,
     against F.conv2d in float64; the output's channel stride (cout + 4) is not a multiple of 8

@@ -1290,7 +1290,7 @@ constexpr int D2_TILE = 128;                   // pixels per block: wave w owns 
 constexpr int D2_PPT = 5;                      // samples per thread: pixel tid % 128, taps tid / 128 + 2 u
 constexpr int D2_RCAP = 1024;                  // region pixels per half-chunk buffer
 constexpr int D2_RBUF = D2_RCAP * 32;          // bytes per region buffer
-constexpr int D2_U = 2 * D2_RBUF;              // shared area: conv_offset staging, offsets, regions, epilogue
+// shared area (conv_offset staging, offsets, region buffers, epilogue, SE): NRB * D2_RBUF bytes
 constexpr int D2_RINST = D2_RCAP * 2 / 64 / D2_WAVES;  // direct loads per wave per half-chunk
 constexpr int D2_NBF_MAX = 4;
 constexpr unsigned D2_SLOW = 0x80000000u;      // record flag: sample outside the region (read from memory)
@@ -1310,7 +1310,8 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds_b
 // straight into LDS, then 9 G k-steps of 2 x 2 MFMA.  oacc[m][b]: offset channel 16 b + row.
 template <typename T>
 __device__ __forceinline__ void d2_offset_conv(floatx4 (&oacc)[2][2], __amdgpu_buffer_rsrc_t rx, const kad_dcn_args& a,
-                                               const DcnGeom& g, int fy0, int fx0, int cin8, unsigned char* su) {
+                                               const DcnGeom& g, int fy0, int fx0, int cin8, unsigned char* su,
+                                               int su_bytes) {
   typedef DcnFrag<T> Ops;
   typedef typename Ops::frag frag;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = lane & 15, grp = lane >> 4;
@@ -1326,7 +1327,7 @@ __device__ __forceinline__ void d2_offset_conv(floatx4 (&oacc)[2][2], __amdgpu_b
   }
   for (int c0 = 0; c0 < g.nchunk;) {
     int G = g.nchunk - c0 < 3 ? g.nchunk - c0 : 3;
-    while (G > 1 && (ceil_div(fpix * (4 * G + 1), 64) + ceil_div(9 * DCN_NOFF * (4 * G + 1), 64)) * 1024 > D2_U) --G;
+    while (G > 1 && (ceil_div(fpix * (4 * G + 1), 64) + ceil_div(9 * DCN_NOFF * (4 * G + 1), 64)) * 1024 > su_bytes) --G;
     const int R = 4 * G + 1, GS = 8 * R;
     const float inv_r = 1.f / (float)R;
     const int nif = ceil_div(fpix * R, 64), niw = ceil_div(9 * DCN_NOFF * R, 64);
@@ -1377,14 +1378,19 @@ __device__ __forceinline__ void d2_offset_conv(floatx4 (&oacc)[2][2], __amdgpu_b
   }
 }
 
-template <typename T, int NBF, int MODE>
+// NRB: region buffers.  One suffices when Cin <= 16 (a single half-chunk, nothing to prefetch): the
+// block then needs ~46 KB of LDS instead of ~78 KB, three blocks per CU instead of two (the host
+// checks that the conv_offset staging and the SE scratch fit the smaller shared area).
+template <typename T, int NBF, int MODE, int NRB>
 __device__ __forceinline__ void dsc2_block(const kad_dcn_args& a, const DcnGeom& g, const int bx, const int by,
                                            const int ny) {
   static_assert(sizeof(T) == 2 && NBF <= D2_NBF_MAX && MODE != MODE_PLAIN, "16-bit DCN / DSC only");
+  static_assert(NRB == 1 || NRB == 2, "one or two region buffers");
   typedef DcnFrag<T> Ops;
   typedef typename Ops::frag frag;
   constexpr int NB = NBF * 16;
-  __shared__ __align__(16) unsigned char s_u[D2_U];  // staging / offsets / region buffers / epilogue / SE
+  constexpr int SU = NRB * D2_RBUF;
+  __shared__ __align__(16) unsigned char s_u[SU];  // staging / offsets / region buffers / epilogue / SE
   __shared__ unsigned s_ia[9 * D2_TILE];            // [tap][pixel] record: region offset + steps, or D2_SLOW
   __shared__ uint2 s_iw[9 * D2_TILE];               // [tap][pixel] corner weights (2 x half2)
   __shared__ float s_par[3][NB];                    // shift, mul, scale
@@ -1450,7 +1456,7 @@ __device__ __forceinline__ void dsc2_block(const kad_dcn_args& a, const DcnGeom&
     floatx4 oacc[2][2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) oacc[m][0] = oacc[m][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-    d2_offset_conv<T>(oacc, rx, a, g, fy0, fx0, cin8, s_u);
+    d2_offset_conv<T>(oacc, rx, a, g, fy0, fx0, cin8, s_u, SU);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int ch = b * 16 + row;
@@ -1783,7 +1789,7 @@ __device__ __forceinline__ void dsc2_block(const kad_dcn_args& a, const DcnGeom&
   typedef T OutT;
   constexpr int SROW = NB + 16 / (int)sizeof(OutT);
   constexpr int STAGE_BYTES = D2_TILE * SROW * (int)sizeof(OutT);
-  static_assert(STAGE_BYTES + D2_WAVES * NB * 4 <= D2_U, "epilogue tile must fit the shared area");
+  static_assert(STAGE_BYTES + D2_WAVES * NB * 4 <= SU, "epilogue tile must fit the shared area");
   OutT* ost = (OutT*)s_u;
   float(*gap_red)[NB] = (float(*)[NB])(s_u + STAGE_BYTES);
   if (tid < NB) {  // v = acc * mul + (bias * mul + add)
@@ -1917,12 +1923,12 @@ __device__ __forceinline__ void dsc2_block(const kad_dcn_args& a, const DcnGeom&
   }
 }
 
-template <typename T, int NBF, int MODE>
+template <typename T, int NBF, int MODE, int NRB>
 __global__ __launch_bounds__(D2_THREADS, 2) void dsc2_kernel(kad_dcn_args a, DcnGeom g) {
-  dsc2_block<T, NBF, MODE>(a, g, blockIdx.x, blockIdx.y, gridDim.y);
+  dsc2_block<T, NBF, MODE, NRB>(a, g, blockIdx.x, blockIdx.y, gridDim.y);
 }
 
-template <typename T, int NBF>
+template <typename T, int NBF, int NRB>
 __global__ __launch_bounds__(D2_THREADS, 2) void dsc2_group_kernel(DcnGroup grp) {
   const int id = blockIdx.x;
   int p = 0;
@@ -1932,7 +1938,7 @@ __global__ __launch_bounds__(D2_THREADS, 2) void dsc2_group_kernel(DcnGroup grp)
   if (id >= grp.start[p + 1]) return;
   const int local = id - grp.start[p];
   const int gx = grp.g[p].grid_x;
-  dsc2_block<T, NBF, MODE_FUSED>(grp.a[p], grp.g[p], local % gx, local / gx, grp.ny[p]);
+  dsc2_block<T, NBF, MODE_FUSED, NRB>(grp.a[p], grp.g[p], local % gx, local / gx, grp.ny[p]);
 }
 
 // ---- weight packing ------------------------------------------------------------------------------
@@ -2046,10 +2052,20 @@ static bool d2_shape_ok(const kad_dcn_args& a) {
 static bool d2_ok(const kad_dcn_args& a, const DcnGeom& g) {
   return d2_shape_ok(a) && (int64_t)a.n * g.tiles >= D2_MIN_BLOCKS;
 }
+// One region buffer (NRB = 1): a single 16-channel half-chunk, and the conv_offset staging of one
+// 32-channel chunk (footprint and filters, 5 slots per row) and the SE scratch within D2_RBUF.
+static bool d2_single(const kad_dcn_args& a, const DcnGeom& g) {
+  const int fpix = g.fh * g.fw;
+  return a.cin <= 16 && (ceil_div(fpix * 5, 64) + ceil_div(9 * DCN_NOFF * 5, 64)) * 1024 <= D2_RBUF &&
+         (a.cout + a.se_hid + D2_THREADS) * 4 <= D2_RBUF;
+}
 
 template <typename T, int NBF, int MODE>
 static int launch_d2(const kad_dcn_args& a, hipStream_t st, const DcnGeom& g) {
-  hipLaunchKernelGGL((dsc2_kernel<T, NBF, MODE>), dim3(g.grid_x, 1, 1), dim3(D2_THREADS), 0, st, a, g);
+  if (d2_single(a, g))
+    hipLaunchKernelGGL((dsc2_kernel<T, NBF, MODE, 1>), dim3(g.grid_x, 1, 1), dim3(D2_THREADS), 0, st, a, g);
+  else
+    hipLaunchKernelGGL((dsc2_kernel<T, NBF, MODE, 2>), dim3(g.grid_x, 1, 1), dim3(D2_THREADS), 0, st, a, g);
   return check_launch(MODE == MODE_FUSED ? "kad_dsc_fwd" : "kad_dcn_fwd");
 }
 
@@ -2070,7 +2086,12 @@ static int dispatch_d2_dtype(const kad_dcn_args& a, hipStream_t st, const DcnGeo
 
 template <typename T, int NBF>
 static int launch_group_d2(const DcnGroup& grp, hipStream_t st) {
-  hipLaunchKernelGGL((dsc2_group_kernel<T, NBF>), dim3(grp.start[grp.count]), dim3(D2_THREADS), 0, st, grp);
+  bool single = true;
+  for (int p = 0; p < grp.count; ++p) single = single && d2_single(grp.a[p], grp.g[p]);
+  if (single)
+    hipLaunchKernelGGL((dsc2_group_kernel<T, NBF, 1>), dim3(grp.start[grp.count]), dim3(D2_THREADS), 0, st, grp);
+  else
+    hipLaunchKernelGGL((dsc2_group_kernel<T, NBF, 2>), dim3(grp.start[grp.count]), dim3(D2_THREADS), 0, st, grp);
   return check_launch("kad_dsc_fwd_group");
 }
 

@@ -212,17 +212,21 @@ constexpr int LM_SCS = LM_SC + 4;                       // fp32 row stride of th
 // formed there once.  Per 32-channel chunk: the lanes' E fragments (11 taps) are
 // requested first, u = relu(alpha a + beta) is written to LDS meanwhile, then
 // 11 x 4 MFMAs.
-template <typename ET>
+// SC: channels per staged group (LM_SC; 32 when every problem has one 32-channel chunk, which cuts
+// the block's LDS from ~71 KB to ~46 KB: three blocks per CU instead of two).
+template <typename ET, int SC = LM_SC>
 __device__ __forceinline__ void lcsa_mask_block(const float* arow, const float* colm, const float* params,
                                                 const ET* emat, const float* ebias, float* mask, int c, int h, int w,
                                                 int cp, int ksplit, float* part, const int bx, const int by,
                                                 const int bz, const int nz) {
   constexpr int LDU = LmCfg<ET>::ldu;
+  constexpr int SCS = SC + 4;
+  static_assert(SC % 32 == 0 && SC <= LM_SC, "whole 32-channel chunks");
   __shared__ __align__(16) ET us[LM_UR * LM_TW * LDU];
-  __shared__ __align__(16) float s_col[LM_UR][LM_SCS];   // column means, columns w0 - 5 .. w0 + 20
-  __shared__ __align__(16) float s_a[LM_UR][LM_SCS];     // row means, rows h0 - 5 .. h0 + 20
-  __shared__ float s_w1[LM_SC * BAND], s_b1[LM_SC], s_bna[LM_SC], s_bnb[LM_SC];
-  __shared__ __align__(16) float s_alpha[LM_TW][LM_SCS], s_beta[LM_TW][LM_SCS];
+  __shared__ __align__(16) float s_col[LM_UR][SCS];   // column means, columns w0 - 5 .. w0 + 20
+  __shared__ __align__(16) float s_a[LM_UR][SCS];     // row means, rows h0 - 5 .. h0 + 20
+  __shared__ float s_w1[SC * BAND], s_b1[SC], s_bna[SC], s_bnb[SC];
+  __shared__ __align__(16) float s_alpha[LM_TW][SCS], s_beta[LM_TW][SCS];
   __shared__ float s_eb[16];  // logit biases, staged with the first group
   const float* w1 = params;
   const float* b1 = params + 11 * c;
@@ -239,28 +243,28 @@ __device__ __forceinline__ void lcsa_mask_block(const float* arow, const float* 
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Flat loop over 32-channel chunks kc; groups of LM_SC / 32 = 3 chunks share the
+  // Flat loop over 32-channel chunks kc; groups of SC / 32 = 3 chunks share the
   // staged means / parameters.  Loads run ahead: the next group's means and
   // parameters are requested as soon as the current group is in LDS, the next
   // chunk's E fragments as soon as the current chunk's MFMAs are issued.  The
   // barriers inside the loop wait for LDS traffic only (a workgroup barrier
   // would also drain those loads).
-  constexpr int NW = (LM_UR * LM_SC + LM_THREADS - 1) / LM_THREADS;    // per window
-  constexpr int NP = (LM_SC * BAND + LM_THREADS - 1) / LM_THREADS;     // w1
-  constexpr int NQ = (3 * LM_SC + LM_THREADS - 1) / LM_THREADS;        // b1 | bn_a | bn_b
-  constexpr int CPG = LM_SC / 32;                                      // chunks per group
+  constexpr int NW = (LM_UR * SC + LM_THREADS - 1) / LM_THREADS;    // per window
+  constexpr int NP = (SC * BAND + LM_THREADS - 1) / LM_THREADS;     // w1
+  constexpr int NQ = (3 * SC + LM_THREADS - 1) / LM_THREADS;        // b1 | bn_a | bn_b
+  constexpr int CPG = SC / 32;                                      // chunks per group
   const int nk = cp / 32;
   const int kc0 = sp * nk / ksplit, kc1 = (sp + 1) * nk / ksplit;
   float vc_[NW], va_[NW], vw_[NP], vq_[NQ];
   typedef typename LmFrag<ET>::frag EF;
   EF ef[BAND];
-  // Index space uses the fixed group width LM_SC (constant divisors); channels past
+  // Index space uses the fixed group width SC (constant divisors); channels past
   // c or past the group read 0.
 #define LM_LOAD_GROUP(CS)                                                                                      \
   {                                                                                                            \
-    const int cs_ = (CS), nsc_ = cp - cs_ < LM_SC ? cp - cs_ : LM_SC;                                          \
+    const int cs_ = (CS), nsc_ = cp - cs_ < SC ? cp - cs_ : SC;                                          \
     _Pragma("unroll") for (int u = 0; u < NW; ++u) {                                                           \
-      const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC, gc = cs_ + ch;                    \
+      const int e = tid + u * LM_THREADS, r = e / SC, ch = e - r * SC, gc = cs_ + ch;                    \
       const int gx = w0 - HALF_BAND + r, gy = h0 - HALF_BAND + r;                                              \
       const bool ok = r < LM_UR && ch < nsc_ && gc < c;                                                        \
       vc_[u] = (ok && gx >= 0 && gx < w) ? colm_n[(uint32_t)(gx * c + gc)] : 0.f;                              \
@@ -271,7 +275,7 @@ __device__ __forceinline__ void lcsa_mask_block(const float* arow, const float* 
       vw_[u] = (e < nsc_ * BAND && cs_ * BAND + e < c * BAND) ? w1[cs_ * BAND + e] : 0.f;                      \
     }                                                                                                          \
     _Pragma("unroll") for (int u = 0; u < NQ; ++u) {                                                           \
-      const int e = tid + u * LM_THREADS, which = e / LM_SC, ch = e - which * LM_SC, gc = cs_ + ch;            \
+      const int e = tid + u * LM_THREADS, which = e / SC, ch = e - which * SC, gc = cs_ + ch;            \
       vq_[u] = (which < 3 && ch < nsc_ && gc < c) ? (which == 0 ? b1 : which == 1 ? bna : bnb)[gc] : 0.f;      \
     }                                                                                                          \
   }
@@ -283,17 +287,17 @@ __device__ __forceinline__ void lcsa_mask_block(const float* arow, const float* 
   // logit biases, read in the epilogue after many barriers; loaded first, so that their LDS
   // store waits for this load only, not for the group's and the E fragments' loads behind it
   const float ebv = tid < 9 ? ebias[tid] : 0.f;
-  LM_LOAD_GROUP((kc0 / CPG) * LM_SC);
+  LM_LOAD_GROUP((kc0 / CPG) * SC);
   LM_LOAD_E(kc0);
   if (tid < 16) s_eb[tid] = ebv;
   for (int kc = kc0; kc < kc1; ++kc) {
-    const int g = kc / CPG, c0 = (kc - g * CPG) * 32, cs = g * LM_SC;
+    const int g = kc / CPG, c0 = (kc - g * CPG) * 32, cs = g * SC;
     if (c0 == 0 || kc == kc0) {  // first chunk of a group (or of the split): stage it, request the next one
-      const int nsc = cp - cs < LM_SC ? cp - cs : LM_SC;
+      const int nsc = cp - cs < SC ? cp - cs : SC;
       LM_LDS_BARRIER();  // the previous group's LDS data is consumed
 #pragma unroll
       for (int u = 0; u < NW; ++u) {
-        const int e = tid + u * LM_THREADS, r = e / LM_SC, ch = e - r * LM_SC;
+        const int e = tid + u * LM_THREADS, r = e / SC, ch = e - r * SC;
         if (r < LM_UR) {
           s_col[r][ch] = vc_[u];
           s_a[r][ch] = va_[u];
@@ -302,11 +306,11 @@ __device__ __forceinline__ void lcsa_mask_block(const float* arow, const float* 
 #pragma unroll
       for (int u = 0; u < NP; ++u) {
         const int e = tid + u * LM_THREADS;
-        if (e < LM_SC * BAND) s_w1[e] = vw_[u];
+        if (e < SC * BAND) s_w1[e] = vw_[u];
       }
 #pragma unroll
       for (int u = 0; u < NQ; ++u) {
-        const int e = tid + u * LM_THREADS, which = e / LM_SC, ch = e - which * LM_SC;
+        const int e = tid + u * LM_THREADS, which = e / SC, ch = e - which * SC;
         if (which < 3) (which == 0 ? s_b1 : which == 1 ? s_bna : s_bnb)[ch] = vq_[u];
       }
       LM_LDS_BARRIER();
@@ -315,8 +319,8 @@ __device__ __forceinline__ void lcsa_mask_block(const float* arow, const float* 
       // means its 4 columns need in registers and forms the 4 sliding sums.  The staged column
       // means are 0 outside the image, so only S needs the in-image mask.
       static_assert(LM_TW == 16, "four column quarters");
-      for (int e = tid; e < 4 * LM_SC; e += LM_THREADS) {
-        const int qc = e / LM_SC, ch = e - qc * LM_SC;
+      for (int e = tid; e < 4 * SC; e += LM_THREADS) {
+        const int qc = e / SC, ch = e - qc * SC;
         float wk[BAND], cm[4 + BAND - 1];
 #pragma unroll
         for (int k = 0; k < BAND; ++k) wk[k] = s_w1[ch * BAND + k];
@@ -353,7 +357,7 @@ __device__ __forceinline__ void lcsa_mask_block(const float* arow, const float* 
           s_beta[col][ch] = ok ? bna * (B + bb) + bnb : 0.f;
         }
       }
-      if ((g + 1) * CPG < kc1) LM_LOAD_GROUP(cs + LM_SC);  // after the coefficients: fewer live registers there
+      if ((g + 1) * CPG < kc1) LM_LOAD_GROUP(cs + SC);  // after the coefficients: fewer live registers there
     }
     LM_LDS_BARRIER();  // alpha / beta ready; the previous chunk's MFMAs are done with us
     // u = relu(alpha * a + beta): thread (column, 8-channel group) fixed, rows r0, r0 + 4, ...;
@@ -442,8 +446,8 @@ struct LcsaGroup {
   int count;
 };
 
-template <typename ET>
-__global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_group_kernel(LcsaGroup grp) {
+template <typename ET, int SC>
+__global__ __launch_bounds__(LM_THREADS, SC == 32 ? 3 : 2) void lcsa_mask_group_kernel(LcsaGroup grp) {
   const int id = blockIdx.x;
   int p = 0;
 #pragma unroll
@@ -452,8 +456,8 @@ __global__ __launch_bounds__(LM_THREADS, 2) void lcsa_mask_group_kernel(LcsaGrou
   const kad_lcsa_args& a = grp.a[p];
   const int local = id - grp.start[p];
   const int tx = ceil_div(a.w, LM_TW), ty = ceil_div(a.h, LM_TH);
-  lcsa_mask_block<ET>(a.arow, a.colm, a.params, (const ET*)a.emat, a.ebias, a.mask, a.c, a.h, a.w,
-                      round_up(a.c, 32), 1, nullptr, local % tx, (local / tx) % ty, local / (tx * ty), a.n);
+  lcsa_mask_block<ET, SC>(a.arow, a.colm, a.params, (const ET*)a.emat, a.ebias, a.mask, a.c, a.h, a.w,
+                          round_up(a.c, 32), 1, nullptr, local % tx, (local / tx) % ty, local / (tx * ty), a.n);
 }
 
 // The axial means of several problems in one launch: grid (max H + W, max N, count).
@@ -643,10 +647,16 @@ extern "C" int kad_lcsa_mask_group(const kad_lcsa_args* a, int count, int emat_d
   KAD_CHECK_ARG(blocks < (1ll << 31), "kad_lcsa_mask_group: too many blocks");
   for (int p = count; p <= KAD_LCSA_GROUP_MAX; ++p) grp.start[p] = (int)blocks;
   hipStream_t st = (hipStream_t)stream;
-  if (emat_dtype == KAD_F32)
-    hipLaunchKernelGGL(kad::lcsa_mask_group_kernel<float>, dim3((unsigned)blocks), dim3(kad::LM_THREADS), 0, st, grp);
+  bool one_chunk = true;  // every problem's channels in one 32-channel chunk: the narrow staging
+  for (int p = 0; p < count; ++p) one_chunk = one_chunk && a[p].c <= 32;
+  if (emat_dtype == KAD_F32 && one_chunk)
+    hipLaunchKernelGGL((kad::lcsa_mask_group_kernel<float, 32>), dim3((unsigned)blocks), dim3(kad::LM_THREADS), 0, st, grp);
+  else if (emat_dtype == KAD_F32)
+    hipLaunchKernelGGL((kad::lcsa_mask_group_kernel<float, kad::LM_SC>), dim3((unsigned)blocks), dim3(kad::LM_THREADS), 0, st, grp);
+  else if (emat_dtype == KAD_F16 && one_chunk)
+    hipLaunchKernelGGL((kad::lcsa_mask_group_kernel<half_t, 32>), dim3((unsigned)blocks), dim3(kad::LM_THREADS), 0, st, grp);
   else if (emat_dtype == KAD_F16)
-    hipLaunchKernelGGL(kad::lcsa_mask_group_kernel<half_t>, dim3((unsigned)blocks), dim3(kad::LM_THREADS), 0, st, grp);
+    hipLaunchKernelGGL((kad::lcsa_mask_group_kernel<half_t, kad::LM_SC>), dim3((unsigned)blocks), dim3(kad::LM_THREADS), 0, st, grp);
   else
     return fail(KAD_EINVAL, "kad_lcsa_mask_group: emat dtype must be KAD_F32 or KAD_F16");
   return check_launch("kad_lcsa_mask_group");

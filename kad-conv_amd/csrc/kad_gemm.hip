@@ -418,7 +418,7 @@ constexpr int GH_WAVES = 4;   // waves per block
 // memory path, which bounded the big launches).
 template <typename T, int NB, bool WLDS>
 __global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args a, int P, int tiles_px, int co_blocks,
-                                                                 int total, int cin_pad) {
+                                                                 int total, int cin_pad, int stage) {
   typedef typename GemmOps<T>::frag frag;
   extern __shared__ __align__(16) char gh_smem[];  // WLDS: [NB][nk][64 lanes][16 bytes]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -520,6 +520,49 @@ __global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args 
   // ---- epilogue: bias, activation, 8-byte stores of 4 channels; zero the pad channels ----------
   const int cpad = round_up(a.cout, 8) < a.out_cs ? round_up(a.cout, 8) : a.out_cs;
   T* out = (T*)a.out + (int64_t)n * P * a.out_cs;
+  if constexpr (WLDS) {
+    if (stage) {
+      // Through the wave's own LDS tile [64 pixels][16 NB (+ 8 pad)]: a lane's 8-byte pieces (4
+      // channels of one pixel, 16 pixels per store) left the output lines partly written, and the
+      // memory side wrote about twice the output bytes; read back, consecutive lanes store
+      // consecutive 16-byte pieces of each pixel's channel run.  out_cs % 8 == 0, 16-byte aligned.
+      constexpr int OBS = 16 * NB + 8;
+      T* stg = (T*)(gh_smem + NB * nk * 1024) + wave * 64 * OBS;
+      auto stage_tile = [&](auto act_tag) {
+        constexpr int ACT = decltype(act_tag)::value;
+#pragma unroll
+        for (int f = 0; f < NB; ++f) {
+          const int co = co0 + 16 * f + 4 * g;
+          float b[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) b[i] = (a.bias && co + i < a.cout) ? a.bias[co + i] : 0.f;
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            T o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float v = acc[m][f][i] + b[i];
+              if constexpr (ACT == 1) v = v * sigmoidf_(v);
+              o[i] = from_f32<T>(co + i < a.cout ? v : 0.f);
+            }
+            *(half4_t*)(stg + (16 * m + c) * OBS + 16 * f + 4 * g) = __builtin_bit_cast(half4_t, o);
+          }
+        }
+      };
+      if (a.act == 1) stage_tile(std::integral_constant<int, 1>{});
+      else stage_tile(std::integral_constant<int, 0>{});
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int nch = cpad - co0 < 16 * NB ? cpad - co0 : 16 * NB;  // a multiple of 8
+      const int ppp = nch >> 3;                                       // 16-byte pieces per pixel
+      for (int i = lane; i < 64 * ppp; i += 64) {
+        const int px = i / ppp, j = i - px * ppp;
+        if (p0 + px < P) *(intx4*)(out + (int64_t)(p0 + px) * a.out_cs + co0 + 8 * j) = *(const intx4*)(stg + px * OBS + 8 * j);
+      }
+      return;
+    }
+  }
   auto epilogue = [&](auto act_tag) {  // activation as a template argument: no per-value branch
     constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
@@ -565,6 +608,9 @@ static bool nhwc_fast_ok(const kad_gemm_args& a) {
 #ifndef KAD_GH_WLDS_KB
 #define KAD_GH_WLDS_KB 64
 #endif
+#ifndef KAD_GH_STAGE
+#define KAD_GH_STAGE 1
+#endif
 template <typename T, int NB>
 static void launch_gemm_nhwc_nb(const kad_gemm_args& a, hipStream_t st) {
   const int P = a.h * a.w, cin_pad = round_up(a.cin, 32);
@@ -572,12 +618,20 @@ static void launch_gemm_nhwc_nb(const kad_gemm_args& a, hipStream_t st) {
   const int total = a.n * tiles_px * co_blocks;
   const size_t wlds = (size_t)NB * (cin_pad / 32) * 1024;  // the block's weight fragments
   if (wlds <= (size_t)KAD_GH_WLDS_KB * 1024) {
-    allow_lds(gemm_nhwc_kernel<T, NB, true>, wlds);
+    // The output staged through LDS when 16-byte pieces line up (one tile per wave behind the
+    // weights) and the extra LDS keeps the blocks per CU that the registers allow (three at NB <= 4,
+    // two at NB = 5): staging that cost a block per CU measured slower (360 -> 128 @100^2: 51 -> 71
+    // us) than the writes it saves.
+    const size_t stg = (size_t)GH_WAVES * 64 * (16 * NB + 8) * sizeof(T);
+    const int stage = KAD_GH_STAGE && a.out_cs % 8 == 0 && ((uintptr_t)a.out & 15) == 0 &&
+                      (wlds + stg) * (NB <= 4 ? 3 : 2) <= 160 * 1024;
+    const size_t lds = wlds + (stage ? stg : 0);
+    allow_lds(gemm_nhwc_kernel<T, NB, true>, lds);
     hipLaunchKernelGGL((gemm_nhwc_kernel<T, NB, true>), dim3(co_blocks * round_up(ceil_div(a.n * tiles_px, GH_WAVES), 8)),
-                       dim3(64 * GH_WAVES), wlds, st, a, P, tiles_px, co_blocks, total, cin_pad);
+                       dim3(64 * GH_WAVES), lds, st, a, P, tiles_px, co_blocks, total, cin_pad, stage);
   } else {
     hipLaunchKernelGGL((gemm_nhwc_kernel<T, NB, false>), dim3(ceil_div(total, GH_WAVES)), dim3(64 * GH_WAVES), 0, st,
-                       a, P, tiles_px, co_blocks, total, cin_pad);
+                       a, P, tiles_px, co_blocks, total, cin_pad, 0);
   }
 }
 

@@ -34,13 +34,27 @@ __global__ __launch_bounds__(256) void resample_nhwc_kernel(kad_resample_args a)
   const T* src = (const T*)a.x;
   T* dst = (T*)a.out;
   const float inv_area = 1.f / (float)(a.k * a.k);
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(i % cv) * VEC;
-    const int64_t pix = i / cv;
-    const int ox = (int)(pix % a.wo);
-    const int64_t t = pix / a.wo;
-    const int oy = (int)(t % a.ho);
-    const int n = (int)(t / a.ho);
+  // XCD-aware order (gridDim.x a multiple of 8): XCD b % 8 takes a contiguous eighth of the items,
+  // so the input rows that neighbouring output rows share (pool windows, nearest-upsample sources)
+  // are fetched into one L2 instead of several
+  const int64_t bq = (int64_t)(blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const bool i32 = total < ((int64_t)1 << 32);
+  for (int64_t i = bq * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    int c, ox, oy, n;
+    if (i32) {
+      const uint32_t ii = (uint32_t)i, pix = ii / (uint32_t)cv, t = pix / (uint32_t)a.wo;
+      c = (int)(ii - pix * (uint32_t)cv) * VEC;
+      ox = (int)(pix - t * (uint32_t)a.wo);
+      n = (int)(t / (uint32_t)a.ho);
+      oy = (int)(t - (uint32_t)n * (uint32_t)a.ho);
+    } else {
+      c = (int)(i % cv) * VEC;
+      const int64_t pix = i / cv;
+      ox = (int)(pix % a.wo);
+      const int64_t t = pix / a.wo;
+      oy = (int)(t % a.ho);
+      n = (int)(t / a.ho);
+    }
     const T* base = src + (int64_t)n * a.h * a.w * a.x_cs + c;
     float acc[VEC];
     if (MODE == RS_NEAREST) {
@@ -77,7 +91,7 @@ __global__ __launch_bounds__(256) void resample_nhwc_kernel(kad_resample_args a)
 template <typename T, int VEC>
 static int launch_resample(const kad_resample_args& a, hipStream_t st) {
   const int64_t total = (int64_t)a.n * a.ho * a.wo * (a.c / VEC);
-  const int blocks = (int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536);
+  const int blocks = round_up((int)((total + 255) / 256 < 65536 ? (total + 255) / 256 : 65536), 8);
   switch (a.mode) {
     case KAD_RS_AVG: hipLaunchKernelGGL((resample_nhwc_kernel<T, VEC, RS_AVG>), dim3(blocks), dim3(256), 0, st, a); break;
     case KAD_RS_MAX: hipLaunchKernelGGL((resample_nhwc_kernel<T, VEC, RS_MAX>), dim3(blocks), dim3(256), 0, st, a); break;

@@ -526,8 +526,11 @@ __global__ __launch_bounds__(64 * GH_WAVES) void gemm_nhwc_kernel(kad_gemm_args 
       // channels of one pixel, 16 pixels per store) left the output lines partly written, and the
       // memory side wrote about twice the output bytes; read back, consecutive lanes store
       // consecutive 16-byte pieces of each pixel's channel run.  out_cs % 8 == 0, 16-byte aligned.
+      // stage 1: the tiles behind the weights; 2: in the weights' place, once every wave of the
+      // block is done with them (waves without a tile have ended and are not waited for).
       constexpr int OBS = 16 * NB + 8;
-      T* stg = (T*)(gh_smem + NB * nk * 1024) + wave * 64 * OBS;
+      T* stg = (T*)(gh_smem + (stage == 1 ? NB * nk * 1024 : 0)) + wave * 64 * OBS;
+      if (stage == 2) __syncthreads();
       auto stage_tile = [&](auto act_tag) {
         constexpr int ACT = decltype(act_tag)::value;
 #pragma unroll
@@ -622,10 +625,11 @@ static void launch_gemm_nhwc_nb(const kad_gemm_args& a, hipStream_t st) {
     // weights) and the extra LDS keeps the blocks per CU that the registers allow (three at NB <= 4,
     // two at NB = 5): staging that cost a block per CU measured slower (360 -> 128 @100^2: 51 -> 71
     // us) than the writes it saves.
+    // Where the weights take at least as much LDS as the tiles, the tiles reuse it after a barrier.
     const size_t stg = (size_t)GH_WAVES * 64 * (16 * NB + 8) * sizeof(T);
-    const int stage = KAD_GH_STAGE && a.out_cs % 8 == 0 && ((uintptr_t)a.out & 15) == 0 &&
-                      (wlds + stg) * (NB <= 4 ? 3 : 2) <= 160 * 1024;
-    const size_t lds = wlds + (stage ? stg : 0);
+    const bool aligned = KAD_GH_STAGE && a.out_cs % 8 == 0 && ((uintptr_t)a.out & 15) == 0;
+    const int stage = !aligned ? 0 : wlds >= stg ? 2 : (wlds + stg) * (NB <= 4 ? 3 : 2) <= 160 * 1024 ? 1 : 0;
+    const size_t lds = wlds + (stage == 1 ? stg : 0);
     allow_lds(gemm_nhwc_kernel<T, NB, true>, lds);
     hipLaunchKernelGGL((gemm_nhwc_kernel<T, NB, true>), dim3(co_blocks * round_up(ceil_div(a.n * tiles_px, GH_WAVES), 8)),
                        dim3(64 * GH_WAVES), lds, st, a, P, tiles_px, co_blocks, total, cin_pad, stage);

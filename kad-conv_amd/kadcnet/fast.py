@@ -151,8 +151,8 @@ class _KADConvOp:
         self.dim = self.plan.dim
 
     def __call__(self, x, out=None):
-        """x: dense NHWC [N, H, W, dim] -> NHWC [N, H, W, dim] (dense, or out: an NHWC channel
-        slice of a wider buffer)."""
+        """x: NHWC [N, H, W, dim], dense or a channel slice of a wider buffer -> NHWC [N, H, W, dim]
+        (dense, or out: an NHWC channel slice of a wider buffer)."""
         y = self.plan.forward(x.permute(0, 3, 1, 2), None if out is None else out.permute(0, 3, 1, 2))
         return y.permute(0, 2, 3, 1)
 
@@ -166,12 +166,25 @@ class _RepNCSP:
         self.cv3 = _ConvOp.from_conv_module(m.cv3)
         self.m = [_KADConvOp(b) for b in m.m]
         self.c_ = self.cv1.cout
+        # cv1 and cv2 read the same input: one GEMM with stacked weights writes [cv1(x) | cv2(x)]
+        # into the concat buffer; the first block reads cv1(x) from there, the last overwrites it
+        # (two or more blocks: the last block's input is then another tensor)
+        self.cv12 = None
+        if len(self.m) >= 2:
+            try:
+                self.cv12 = _ConvOp.stacked([self.cv1, self.cv2])
+            except ValueError:
+                self.cv12 = None
 
     def __call__(self, x, out=None):
         N, H, W = x.shape[:3]
         cat = x.new_empty(N, H, W, 2 * self.c_)
-        self.cv2(x, cat[..., self.c_:])
-        y = self.cv1(x)
+        if self.cv12 is not None:
+            self.cv12(x, cat)
+            y = cat[..., :self.c_]
+        else:
+            self.cv2(x, cat[..., self.c_:])
+            y = self.cv1(x)
         if not self.m:
             _copy(y, cat)
         for i, blk in enumerate(self.m):  # the last block writes the concat's first half itself

@@ -457,7 +457,7 @@ def pyramid_proj(x, in_layout, cin, branches):
         N, C, H, W = x.shape
         cs = C
     else:
-        N, H, W, cs = x.shape
+        N, H, W, cs = _nhwc_cs(x)   # x may be a channel slice of a wider NHWC buffer
     if not 1 <= len(branches) <= 3:
         raise ValueError('kad_pyramid_proj takes 1..3 branches')
     a = PyramidArgs()

@@ -177,6 +177,16 @@ class DSCPlan:
         return self.run(y, n, h, w, out, _ext.KAD_NCHW, x_nchw=x if x.is_contiguous() else None)
 
 
+def _channels_last_view(x):
+    """x is channels-last memory (NCHW-shaped view), dense or a channel slice of a wider buffer
+    (pixel stride >= C); a dense NCHW tensor is not."""
+    if x.dim() != 4 or x.is_contiguous():
+        return False
+    N, C, H, W = x.shape
+    return (x.stride(1) == 1 and x.stride(3) >= C and x.stride(2) == x.stride(3) * W
+            and (N == 1 or x.stride(0) == x.stride(2) * H))
+
+
 class _Branch:
     def __init__(self, conv, fc, scale, c_off):
         proj, dsc, bn = conv[0], conv[1], conv[2]
@@ -254,7 +264,7 @@ class KADConvPlan:
         """(x view for the kernels, its layout, out, out view, out layout).  out: for a channels-last
         x, an NCHW-shaped view of channels-last memory whose pixel stride may exceed C (a channel
         slice of a wider buffer, e.g. a concat), written in place."""
-        nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
+        nhwc = _channels_last_view(x)
         if nhwc:
             if out is None:
                 out = torch.empty_like(x, memory_format=torch.channels_last)

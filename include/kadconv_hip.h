@@ -438,6 +438,9 @@ int kad_stem_conv_fwd(const kad_dcn_args *a, void *stream);
 #define KAD_RS_AVG 0      /* average pool, zero padding counted (count_include_pad=True) */
 #define KAD_RS_MAX 1      /* max pool, padding ignored */
 #define KAD_RS_NEAREST 2  /* nearest upsample by the integer factor s: out[y][x] = in[y / s][x / s] */
+#define KAD_RS_MAX3 3     /* SPPELAN's chain of three max pools (k odd, s = 1, p = k / 2, ho = h, wo = w):
+                             out channels [0, c) = pool(x), [c, 2c) = pool(pool(x)), [2c, 3c) =
+                             pool(pool(pool(x))) in one call (out_cs >= 3 c) */
 
 typedef struct kad_resample_args {
   const void *x;         /* NHWC [N][H][W][x_cs], dtype (channels [0, c) used) */

@@ -100,6 +100,57 @@ static int launch_resample(const kad_resample_args& a, hipStream_t st) {
   return check_launch("kad_nhwc_resample");
 }
 
+// SPPELAN's three chained k x k max pools (stride 1, padding k / 2) of one 8-channel group of one
+// image, the map held in LDS: a max pool applied j times is one max pool of radius j r (r = k / 2,
+// padding never wins a max), so row maxima of radius r, 2 r, 3 r come from one another (radius
+// 2 r at x = the larger of radius r at x - r and at x + r, indices clamped to the row: the clamped
+// window stays inside the wanted one), then each output takes its column window over them.  One
+// launch and one read of the map instead of three pools that each re-read the previous output.
+template <typename T>
+__global__ __launch_bounds__(256) void maxpool3_nhwc_kernel(kad_resample_args a) {
+  typedef Vec8<T> V;  // 16-byte aligned: one 16-byte LDS / memory access per 8 channels
+  extern __shared__ __align__(16) char mp_smem[];
+  const int hw = a.h * a.w, r = a.k / 2;
+  V* xs = (V*)mp_smem;  // [4][h][w]: the map, then row maxima of radius r, 2 r, 3 r
+  const int g = blockIdx.x, n = blockIdx.y;
+  const T* src = (const T*)a.x + (int64_t)n * hw * a.x_cs + 8 * g;
+  auto vmax = [](const V& p, const V& q) {
+    V o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o.v[e] = from_f32<T>(fmaxf(to_f32(p.v[e]), to_f32(q.v[e])));
+    return o;
+  };
+  for (int i = threadIdx.x; i < hw; i += 256) xs[i] = *(const V*)(src + (int64_t)i * a.x_cs);
+  __syncthreads();
+  for (int i = threadIdx.x; i < hw; i += 256) {
+    const int y = i / a.w, x = i - y * a.w;
+    const int x0 = x - r < 0 ? 0 : x - r, x1 = x + r >= a.w ? a.w - 1 : x + r;
+    V m = xs[y * a.w + x0];
+    for (int xx = x0 + 1; xx <= x1; ++xx) m = vmax(m, xs[y * a.w + xx]);
+    xs[hw + i] = m;
+  }
+  for (int j = 2; j <= 3; ++j) {
+    __syncthreads();
+    const V* prev = xs + (j - 1) * hw;
+    for (int i = threadIdx.x; i < hw; i += 256) {
+      const int y = i / a.w, x = i - y * a.w;
+      const int xl = x - r < 0 ? 0 : x - r, xr = x + r >= a.w ? a.w - 1 : x + r;
+      xs[j * hw + i] = vmax(prev[y * a.w + xl], prev[y * a.w + xr]);
+    }
+  }
+  __syncthreads();
+  T* dst = (T*)a.out + (int64_t)n * hw * a.out_cs + 8 * g;
+  for (int e = threadIdx.x; e < 3 * hw; e += 256) {
+    const int j = e / hw, i = e - j * hw;  // output j + 1: column window of radius (j + 1) r
+    const int y = i / a.w, x = i - y * a.w, rad = (j + 1) * r;
+    const int y0 = y - rad < 0 ? 0 : y - rad, y1 = y + rad >= a.h ? a.h - 1 : y + rad;
+    const V* rm = xs + (j + 1) * hw;
+    V m = rm[y0 * a.w + x];
+    for (int yy = y0 + 1; yy <= y1; ++yy) m = vmax(m, rm[yy * a.w + x]);
+    *(V*)(dst + (int64_t)i * a.out_cs + j * a.c) = m;
+  }
+}
+
 template <typename T>
 static int dispatch_resample(const kad_resample_args& a, hipStream_t st) {
   constexpr int V = 16 / (int)sizeof(T);
@@ -290,8 +341,44 @@ extern "C" int kad_nhwc_resample(const kad_resample_args* a, void* stream) {
                 "kad_nhwc_resample: bad shape n=%d c=%d %dx%d -> %dx%d", a->n, a->c, a->h, a->w, a->ho, a->wo);
   KAD_CHECK_ARG(a->x_cs >= a->c && a->out_cs >= a->c, "kad_nhwc_resample: channel strides %d / %d < c=%d", a->x_cs,
                 a->out_cs, a->c);
-  KAD_CHECK_ARG(a->mode == KAD_RS_AVG || a->mode == KAD_RS_MAX || a->mode == KAD_RS_NEAREST,
+  KAD_CHECK_ARG(a->mode == KAD_RS_AVG || a->mode == KAD_RS_MAX || a->mode == KAD_RS_NEAREST ||
+                    a->mode == KAD_RS_MAX3,
                 "kad_nhwc_resample: unknown mode %d", a->mode);
+  if (a->mode == KAD_RS_MAX3) {
+    KAD_CHECK_ARG(a->k >= 1 && a->k % 2 == 1 && a->s == 1 && a->p == a->k / 2 && a->ho == a->h && a->wo == a->w,
+                  "kad_nhwc_resample: KAD_RS_MAX3 needs an odd k, s = 1, p = k / 2 and ho, wo = h, w");
+    KAD_CHECK_ARG(a->out_cs >= 3 * a->c, "kad_nhwc_resample: KAD_RS_MAX3 writes 3 c channels (out_cs %d < %d)",
+                  a->out_cs, 3 * a->c);
+    hipStream_t st = (hipStream_t)stream;
+    const size_t lds = (size_t)4 * a->h * a->w * 16;
+    if (a->dtype != KAD_F32 && a->c % 8 == 0 && a->x_cs % 8 == 0 && a->out_cs % 8 == 0 &&
+        ((uintptr_t)a->x & 15) == 0 && ((uintptr_t)a->out & 15) == 0 && lds <= 64 * 1024) {
+      const dim3 grid(a->c / 8, a->n);
+      if (a->dtype == KAD_F16) hipLaunchKernelGGL(maxpool3_nhwc_kernel<half_t>, grid, dim3(256), lds, st, *a);
+      else hipLaunchKernelGGL(maxpool3_nhwc_kernel<bf16_t>, grid, dim3(256), lds, st, *a);
+      return check_launch("kad_nhwc_resample");
+    }
+    // otherwise three max pools, each reading the previous output slice
+    kad_resample_args b = *a;
+    b.mode = KAD_RS_MAX;
+    const int esz = a->dtype == KAD_F32 ? 4 : 2;
+    for (int j = 0; j < 3; ++j) {
+      if (j > 0) {
+        b.x = (const char*)a->out + (size_t)(j - 1) * a->c * esz;
+        b.x_cs = a->out_cs;
+      }
+      b.out = (char*)a->out + (size_t)j * a->c * esz;
+      int rc;
+      switch (a->dtype) {
+        case KAD_F32: rc = dispatch_resample<float>(b, st); break;
+        case KAD_F16: rc = dispatch_resample<half_t>(b, st); break;
+        case KAD_BF16: rc = dispatch_resample<bf16_t>(b, st); break;
+        default: return fail(KAD_EINVAL, "kad_nhwc_resample: unknown dtype %d", a->dtype);
+      }
+      if (rc) return rc;
+    }
+    return KAD_OK;
+  }
   if (a->mode == KAD_RS_NEAREST) {
     KAD_CHECK_ARG(a->s >= 1 && a->ho == a->h * a->s && a->wo == a->w * a->s,
                   "kad_nhwc_resample: nearest upsample needs ho = h * s, wo = w * s (s=%d)", a->s);

@@ -245,10 +245,13 @@ class _SPPELAN:
         c = self.cv1.cout
         cat = x.new_empty(N, H, W, 4 * c)
         self.cv1(x, cat[..., :c])
-        for i, k in enumerate(self.k):
-            k = k if isinstance(k, int) else k[0]
-            _ext.nhwc_resample(cat[..., i * c:(i + 1) * c], cat[..., (i + 1) * c:(i + 2) * c], c, _ext.KAD_RS_MAX,
-                               k=k, s=1, p=k // 2)
+        ks = [k if isinstance(k, int) else k[0] for k in self.k]
+        if ks[0] == ks[1] == ks[2] and ks[0] % 2 == 1:  # the three chained pools in one launch
+            _ext.nhwc_resample(cat[..., :c], cat[..., c:], c, _ext.KAD_RS_MAX3, k=ks[0], s=1, p=ks[0] // 2)
+        else:
+            for i, k in enumerate(ks):
+                _ext.nhwc_resample(cat[..., i * c:(i + 1) * c], cat[..., (i + 1) * c:(i + 2) * c], c, _ext.KAD_RS_MAX,
+                                   k=k, s=1, p=k // 2)
         return self.cv5(cat, out)
 
 

@@ -684,7 +684,7 @@ def branch_merge(out, layout, branches, residual=None, gate=None, channels=None)
 
 # ---------------------------------------------------------------------------- network ops (KAD-CNet-S)
 KAD_ACT_NONE, KAD_ACT_RELU, KAD_ACT_SILU = 0, 1, 2
-KAD_RS_AVG, KAD_RS_MAX, KAD_RS_NEAREST = 0, 1, 2
+KAD_RS_AVG, KAD_RS_MAX, KAD_RS_NEAREST, KAD_RS_MAX3 = 0, 1, 2, 3
 
 
 def _nhwc_cs(t):
@@ -746,7 +746,8 @@ def stem_conv_fwd(x_nchw, wpack, cout, out_nhwc, *, stride=2, bias=None, act=KAD
 
 def nhwc_resample(x_nhwc, out_nhwc, c, mode, k=1, s=1, p=0):
     """Pool (KAD_RS_AVG / KAD_RS_MAX, kernel k, stride s, padding p), nearest upsample
-    (KAD_RS_NEAREST, factor s) or copy (AVG with k = s = 1) of channels [0, c)."""
+    (KAD_RS_NEAREST, factor s) or copy (AVG with k = s = 1) of channels [0, c); KAD_RS_MAX3:
+    three chained max pools (s = 1, p = k // 2) into channels [0, c), [c, 2c), [2c, 3c) of out."""
     _need_gpu(x_nhwc, out_nhwc)
     N, H, W, cs = _nhwc_cs(x_nhwc)
     No, Ho, Wo, ocs = _nhwc_cs(out_nhwc)

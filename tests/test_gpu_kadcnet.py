@@ -64,6 +64,29 @@ def test_nhwc_resample(dt, mode, k, s, p):
     assert err <= tol, f'{mode} {dt}: max|d| = {err}'
 
 
+@pytest.mark.parametrize('dt,N,H,W,C,k', [('f16', 2, 25, 25, 16, 5), ('bf16', 3, 13, 20, 24, 5), ('f16', 1, 25, 25, 8, 3),
+                                          ('f16', 2, 40, 40, 16, 5), ('f32', 2, 25, 25, 8, 5)])
+def test_maxpool3_chain(dt, N, H, W, C, k):
+    """KAD_RS_MAX3: SPPELAN's three chained max pools (stride 1, padding k // 2) written into three
+    consecutive channel slices, against F.max_pool2d applied 1, 2, 3 times (exact: max does not
+    round).  16-bit maps that fit LDS take the one-launch kernel; 40 x 40 and fp32 the three-pool
+    path; the input is itself a channel slice and the slices around the outputs stay untouched."""
+    from kadconv import _ext
+    dtype, dev = DT[dt], 'cuda'
+    g = torch.Generator().manual_seed(H * 7 + C + k)
+    xs = torch.randn(N, H, W, C + 8, generator=g).to(dtype)
+    out = torch.full((N, H, W, 3 * C + 16), 7.0, dtype=dtype, device=dev)
+    print(f'maxpool3 {dt} {N}x{H}x{W}x{C} k{k}', flush=True)
+    _ext.nhwc_resample(xs.to(dev)[..., 8:8 + C], out[..., 8:8 + 3 * C], C, _ext.KAD_RS_MAX3, k=k, s=1, p=k // 2)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert (got[..., :8] == 7.0).all() and (got[..., 8 + 3 * C:] == 7.0).all()
+    ref = xs[..., 8:8 + C].permute(0, 3, 1, 2).float()
+    for j in range(3):
+        ref = F.max_pool2d(ref, k, 1, k // 2)
+        assert torch.equal(got[..., 8 + j * C:8 + (j + 1) * C].permute(0, 3, 1, 2).float(), ref), f'pool {j + 1}'
+
+
 @pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
 @pytest.mark.parametrize('cin,cout,stride,groups,act', [(3, 40, 2, 1, 'silu'), (72, 144, 2, 1, 'silu'),
                                                         (32, 32, 1, 1, 'silu'), (64, 64, 1, 4, 'silu'),

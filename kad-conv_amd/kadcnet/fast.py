@@ -99,6 +99,25 @@ class _ConvOp:
         op.cout, op.act, op._packed = op.w.shape[0], first.act, {}
         return op
 
+    @classmethod
+    def block_diagonal(cls, ops):
+        """One 1x1 conv over the concatenated inputs of several 1x1 convs, producing their
+        concatenated outputs (each reads only its own input channels)."""
+        first = ops[0]
+        if any(o.k != 1 or o.act != first.act for o in ops):
+            raise ValueError('block-diagonal convs must be 1x1 with one activation')
+        op = object.__new__(cls)
+        op.k, op.stride, op.pad = 1, 1, 0
+        op.cin, op.cout = sum(o.cin for o in ops), sum(o.cout for o in ops)
+        op.w = torch.zeros(op.cout, op.cin, 1, 1, device=first.w.device)
+        r = c = 0
+        for o in ops:
+            op.w[r:r + o.cout, c:c + o.cin] = o.w
+            r, c = r + o.cout, c + o.cin
+        op.b = torch.cat([o.b for o in ops]).contiguous()
+        op.act, op._packed = first.act, {}
+        return op
+
     def out_hw(self, h, w):
         if self.k == 1:
             return h, w
@@ -294,19 +313,23 @@ class _DDetect:
             b0, b1, b2 = m.cv2[i]
             c0, c1, c2 = m.cv3[i]
             first = _ConvOp.stacked([_ConvOp.from_conv_module(b0), _ConvOp.from_conv_module(c0)])
-            self.levels.append((first, _ConvOp.from_conv_module(b1), _ConvOp(b2), _ConvOp.from_conv_module(c1),
-                                _ConvOp(c2)))
+            ob1, oc1 = _ConvOp.from_conv_module(b1), _ConvOp.from_conv_module(c1)
+            self.levels.append((first, ob1, oc1, _ConvOp.block_diagonal([_ConvOp(b2), _ConvOp(c2)])))
         self.head_cs = (self.box_ch + self.nc + 7) // 8 * 8
 
     def __call__(self, xs):
         heads = []
-        for x, (first, b1, b2, c1, c2) in zip(xs, self.levels):
+        for x, (first, b1, c1, bc2) in zip(xs, self.levels):
             N, H, W = x.shape[:3]
             t = first(x)
             nb = b1.cin
+            # the two branches' middle convs write one buffer, whose box and class 1x1 convs run
+            # as one block-diagonal GEMM straight into the [box | cls] map
+            mid = x.new_empty(N, H, W, b1.cout + c1.cout)
+            b1(t[..., :nb], mid[..., :b1.cout])
+            c1(t[..., nb:], mid[..., b1.cout:])
             head = x.new_empty(N, H, W, self.head_cs)
-            b2(b1(t[..., :nb]), head[..., :self.box_ch])
-            c2(c1(t[..., nb:]), head[..., self.box_ch:self.box_ch + self.nc])
+            bc2(mid, head[..., :self.box_ch + self.nc])
             heads.append(head)
         A = sum(h.shape[1] * h.shape[2] for h in heads)
         y = heads[0].new_empty(heads[0].shape[0], 4 + self.nc, A)

@@ -804,7 +804,10 @@ template <typename T>
 __global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, int npix, int ngroups) {
   typedef Vec8<T> V;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int p = blockIdx.x * 64 + (int)(threadIdx.x & 63);
+  // XCD-aware order (gridDim.x a multiple of 8): XCD b % 8 takes a contiguous run of pixels, so the
+  // low-resolution rows that neighbouring output rows upsample from are fetched into one L2
+  const int bq = (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
+  const int p = bq * 64 + (int)(threadIdx.x & 63);
   if (p >= npix) return;
   const int x = p % a.w, t = p / a.w;
   const int y = t % a.h, n = t / a.h;
@@ -1463,7 +1466,7 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
              (int64_t)a->n * a->h * a->w < ((int64_t)1 << 31) - 64) {
     const int npix = a->n * a->h * a->w;
     const int ngroups = (a->c_end - a->c_begin) / 8;
-    const int blocks = ceil_div(npix, 64);
+    const int blocks = round_up(ceil_div(npix, 64), 8);
     switch (a->dtype) {
       case KAD_F32: hipLaunchKernelGGL(merge_nhwc_vec_kernel<float>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;
       case KAD_F16: hipLaunchKernelGGL(merge_nhwc_vec_kernel<half_t>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;

@@ -103,12 +103,16 @@ __global__ __launch_bounds__(CV_THREADS, NBW <= 2 ? 2 : 1) void conv3x3_ig_kerne
   __shared__ __align__(16) char wsm[9 * BN * 64];
   __shared__ __align__(16) float s_par[3][BN];  // shift (bias * mul + add), mul, post_scale per column
 
-  const int q = (blockIdx.x & 7) * (g.grid_x >> 3) + (blockIdx.x >> 3);
-  if (q >= a.n * g.tiles) return;  // whole block, before any barrier
+  // XCD-aware order over (patch, column block), column blocks fastest: XCD b % 8 takes a contiguous
+  // run, so a patch's column blocks stage its footprint from one L2, one after another
+  const int ncb = ceil_div(a.cout, BN);
+  const int qq = (blockIdx.x & 7) * (g.grid_x >> 3) + (blockIdx.x >> 3);
+  if (qq >= a.n * g.tiles * ncb) return;  // whole block, before any barrier
+  const int q = qq / ncb, cb = qq - q * ncb;
   const int n = q / g.tiles, tile = q - n * g.tiles;
   const int tyi = tile / g.tiles_x;
   const int ty0 = tyi * g.th, tx0 = (tile - tyi * g.tiles_x) * g.tw;
-  const int co0 = blockIdx.y * BN;
+  const int co0 = cb * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, row = lane & 15, grp = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
   const int fy0 = ty0 * S - a.pad, fx0 = tx0 * S - a.pad;
@@ -352,13 +356,15 @@ int cv_pick_nbw(int cout, long tiles, int stride) {
 template <typename T, int S>
 int launch_nbw(const kad_dcn_args& a, const CvGeom& g, int nbw, hipStream_t st) {
   const dim3 block(CV_THREADS);
-  const dim3 grid(g.grid_x, ceil_div(a.cout, 32 * nbw), 1);
+  CvGeom gl = g;  // one grid dimension over (patch, column block)
+  gl.grid_x = round_up(a.n * g.tiles * ceil_div(a.cout, 32 * nbw), 8);
+  const dim3 grid(gl.grid_x, 1, 1);
   switch (nbw) {
-    case 1: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 1, S>), grid, block, 0, st, a, g); break;
-    case 2: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 2, S>), grid, block, 0, st, a, g); break;
-    case 3: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 3, S>), grid, block, 0, st, a, g); break;
-    case 4: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 4, S>), grid, block, 0, st, a, g); break;
-    default: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 5, S>), grid, block, 0, st, a, g); break;
+    case 1: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 1, S>), grid, block, 0, st, a, gl); break;
+    case 2: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 2, S>), grid, block, 0, st, a, gl); break;
+    case 3: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 3, S>), grid, block, 0, st, a, gl); break;
+    case 4: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 4, S>), grid, block, 0, st, a, gl); break;
+    default: hipLaunchKernelGGL((conv3x3_ig_kernel<T, 5, S>), grid, block, 0, st, a, gl); break;
   }
   return check_launch("kad_conv_fwd");
 }

@@ -789,8 +789,8 @@ __global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
   }
 }
 
-// NHWC output, channel window and pixel strides multiples of 8.  A block takes 64 pixels; its wave w the
-// 8-channel groups w, w + 4, ... of them, a lane per pixel, so the group -- which branches cover it,
+// NHWC output, channel window and pixel strides multiples of 8.  A block takes 64 pixels with one wave
+// per 8-channel group (up to 8 waves; wave w takes groups w, w + 8, ...), a lane per pixel, so the group -- which branches cover it,
 // at which channel offset -- is the same across the wave (scalar branches, no divergence), while
 // the block's other waves read the other groups of the same pixels' lines.  16-byte loads of the
 // residual and 16-byte stores.  Each channel takes its value from the branch whose window holds it;
@@ -801,7 +801,7 @@ __global__ __launch_bounds__(256) void merge_nhwc_kernel(kad_merge_args a) {
 // read only when it holds a channel of the window, so it lies in a mapped page); others element by
 // element.  Lets a channels-last KAD-Conv merge all its branches in one launch.
 template <typename T>
-__global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, int npix, int ngroups) {
+__global__ __launch_bounds__(512) void merge_nhwc_vec_kernel(kad_merge_args a, int npix, int ngroups) {
   typedef Vec8<T> V;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   // XCD-aware order (gridDim.x a multiple of 8): XCD b % 8 takes a contiguous run of pixels, so the
@@ -811,7 +811,8 @@ __global__ __launch_bounds__(256) void merge_nhwc_vec_kernel(kad_merge_args a, i
   if (p >= npix) return;
   const int x = p % a.w, t = p / a.w;
   const int y = t % a.h, n = t / a.h;
-  for (int grp = wave; grp < ngroups; grp += 4) {
+  const int nwaves = (int)(blockDim.x >> 6);  // one per group up to 8 (no wave takes two of a block's)
+  for (int grp = wave; grp < ngroups; grp += nwaves) {
     const int c0 = a.c_begin + 8 * grp;
     const int64_t oi = (int64_t)p * a.out_cs + c0;
     float v[8];
@@ -1467,10 +1468,11 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
     const int npix = a->n * a->h * a->w;
     const int ngroups = (a->c_end - a->c_begin) / 8;
     const int blocks = round_up(ceil_div(npix, 64), 8);
+    const int threads = 64 * (ngroups < 8 ? ngroups : 8);
     switch (a->dtype) {
-      case KAD_F32: hipLaunchKernelGGL(merge_nhwc_vec_kernel<float>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;
-      case KAD_F16: hipLaunchKernelGGL(merge_nhwc_vec_kernel<half_t>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;
-      case KAD_BF16: hipLaunchKernelGGL(merge_nhwc_vec_kernel<bf16_t>, dim3(blocks), dim3(256), 0, st, *a, npix, ngroups); break;
+      case KAD_F32: hipLaunchKernelGGL(merge_nhwc_vec_kernel<float>, dim3(blocks), dim3(threads), 0, st, *a, npix, ngroups); break;
+      case KAD_F16: hipLaunchKernelGGL(merge_nhwc_vec_kernel<half_t>, dim3(blocks), dim3(threads), 0, st, *a, npix, ngroups); break;
+      case KAD_BF16: hipLaunchKernelGGL(merge_nhwc_vec_kernel<bf16_t>, dim3(blocks), dim3(threads), 0, st, *a, npix, ngroups); break;
       default: return fail(KAD_EINVAL, "kad_branch_merge: unknown dtype %d", a->dtype);
     }
   } else {

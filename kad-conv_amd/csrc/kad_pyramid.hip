@@ -21,6 +21,8 @@
 
 namespace kad {
 
+int band_pyramid(const kad_pyramid_args& a, hipStream_t st);  // kad_band.hip; 1 = not its case
+
 constexpr int PY_TR = 4, PY_TC = 32, PY_TILE = PY_TR * PY_TC;
 constexpr int PY_THREADS = 256;
 
@@ -825,6 +827,8 @@ extern "C" int kad_pyramid_proj(const kad_pyramid_args* a, void* stream) {
   }
   const int cin_pad = round_up(a->cin, 32);
   hipStream_t st = (hipStream_t)stream;
+  const int band = band_pyramid(*a, st);  // 16-bit NCHW KADConv shapes: one block per 4-row band
+  if (band != 1) return band;
   switch (a->dtype) {
     case KAD_F32: return dispatch_pyramid<float>(*a, cin_pad, maxcols, st);
     case KAD_F16: return dispatch_pyramid<half_t>(*a, cin_pad, maxcols, st);

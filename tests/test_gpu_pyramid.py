@@ -9,6 +9,10 @@ and the slices must add up to the branch output's row and column sums.
 Shapes cover ragged tiles: (21, 70) has a last tile row band with no pooled row of
 branch 1 (its column partials must be zeros); (13, 66) has a last tile column with no
 column of branch 2 (its row partial must be written, as zero).
+The 16-bit band shapes (H and W multiples of 4, W <= 100 with 4 W mod 128 <= 16) run the
+one-block-per-4-row-band kernel: W = 100 has three full 128-pixel groups and a 16-pixel tail, 96
+three groups, 36 one group and a tail, 64 and 32 whole groups; C = 40, 96 and 160 give K loops of
+2, 3 and 5 steps (padded to multiples of three), C = 256 the KADConv(256) metric's eight.
 Tolerances: fp32 1e-4 relative; fp16/bf16 1e-2 (outputs) and 2e-2 relative
 (sums of up to W values)."""
 import pytest
@@ -23,7 +27,9 @@ DT = {'f32': torch.float32, 'f16': torch.float16, 'bf16': torch.bfloat16}
 
 
 @pytest.mark.parametrize('dt', ['f32', 'f16', 'bf16'])
-@pytest.mark.parametrize('shape', [(2, 48, 37, 29), (1, 40, 21, 70), (2, 24, 8, 8), (1, 24, 13, 66)])
+@pytest.mark.parametrize('shape', [(2, 48, 37, 29), (1, 40, 21, 70), (2, 24, 8, 8), (1, 24, 13, 66),
+                                   (2, 256, 8, 100), (1, 96, 12, 96), (2, 40, 4, 36), (1, 160, 8, 64),
+                                   (1, 48, 8, 32)])
 def test_pyramid_proj_and_partial_sums(dt, shape):
     from kadconv import _ext
     dtype = DT[dt]

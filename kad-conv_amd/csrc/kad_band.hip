@@ -42,7 +42,7 @@ namespace kad {
 constexpr int BD_WAVES = 4, BD_THREADS = 64 * BD_WAVES;  // one wave per SIMD: up to 512 registers each
 constexpr int BD_SLOT = 512;                         // pixels per channel in an x stage (4 rows x W, W <= 128)
 constexpr int BD_XS = 32 * BD_SLOT;                  // elements per x stage (32 KB)
-constexpr int BD_XSA = BD_XS + 2048;                 // allocated per stage: the epilogue stages outputs there too
+constexpr int BD_XSA = BD_XS + 4096;                 // allocated per stage: the epilogue stages outputs there too
 constexpr int BD_P2 = 32 * 128;                      // 2 x 2 means: [32 ch][2 pooled rows x 64]
 constexpr int BD_P4 = 32 * 32;                       // 4 x 4 means: [32 ch][32]
 
@@ -301,8 +301,8 @@ __global__ __launch_bounds__(BD_THREADS, 1) void band_pyramid_kernel(kad_pyramid
   // in every NHWC output), then form the LCSA partial sums from the rounded values in the layout of
   // kad_pyramid_tiles: row sums per column slice of 32 >> b columns (ntx slices), column sums over the
   // band's rows (slice `band` of nty).  Staging: branch-0 pixel p at [(p - 128 q) cs0] of object
-  // q = min(p / 128, 2) (xsA, xsB, xsC: the tail after group 2 in xsC); branch-1 pooled row r at
-  // [128 cs0 + c cs1] of xsA / xsB; branch 2 at [max(4 W - 256, 0) cs0 + c cs2] of xsC.
+  // q = min(p / 128, 2) (xsA, xsB, xsC: the tail after group 2 in xsC); branch 1 (both pooled rows) at
+  // [128 cs0 + (r W / 2 + c) cs1] of xsA; branch 2 at [max(4 W - 256, 0) cs0 + c cs2] of xsC.
   const int cs0 = a.out_cs[0], cs1 = a.out_cs[1], cs2 = a.out_cs[2];
   auto obj = [&](int q) __attribute__((always_inline)) -> T* {  // q wave-uniform
     return q == 0 ? xsA : (q == 1 ? xsB : xsC);
@@ -314,7 +314,8 @@ __global__ __launch_bounds__(BD_THREADS, 1) void band_pyramid_kernel(kad_pyramid
     const int q = min(__builtin_amdgcn_readfirstlane(r * W + x0) >> 7, 2);
     return obj(q) + (r * W + x - 128 * q) * cs0;
   };
-  auto zat1 = [&](int r, int, int x) __attribute__((always_inline)) -> T* { return (r ? xsB : xsA) + 128 * cs0 + x * cs1; };
+  T* const z1s = xsA + 128 * cs0;
+  auto zat1 = [&](int r, int, int x) __attribute__((always_inline)) -> T* { return z1s + (r * W1 + x) * cs1; };
   T* const z2s = xsC + max(bandpx - 256, 0) * cs0;
   auto zat2 = [&](int, int, int x) __attribute__((always_inline)) -> T* { return z2s + x * cs2; };
   auto bias4 = [&](int b, int m) __attribute__((always_inline)) -> floatx4 {  // channels 16 m + 4 g ..
@@ -355,7 +356,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void band_pyramid_kernel(kad_pyramid
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int pc = 8 * (cl & 7) + j;
-        if (pc < W1) put4((pr ? xsB : xsA) + 128 * cs0 + pc * cs1 + 16 * m + 4 * g, acc[m][j], bv);
+        if (pc < W1) put4(z1s + (pr * W1 + pc) * cs1 + 16 * m + 4 * g, acc[m][j], bv);
       }
     }
     if (x_tail && cl < tail) {  // branch-0 tail, pixel 128 ngrp + c
@@ -385,8 +386,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void band_pyramid_kernel(kad_pyramid
       if (npx > 0) copy(obj(q), o0 + 128 * q * cs0, npx * cs0 / 8);
     }
     T* o1 = (T*)a.out[1] + ((int64_t)n * (a.h >> 1) + 2 * band) * W1 * cs1;
-    copy(xsA + 128 * cs0, o1, W1 * cs1 / 8);
-    copy(xsB + 128 * cs0, o1 + W1 * cs1, W1 * cs1 / 8);
+    copy(z1s, o1, 2 * W1 * cs1 / 8);
     T* o2 = (T*)a.out[2] + ((int64_t)n * (a.h >> 2) + band) * W2 * cs2;
     copy(z2s, o2, W2 * cs2 / 8);
   }
@@ -485,8 +485,8 @@ int band_pyramid(const kad_pyramid_args& a, hipStream_t st) {
   for (int b = 0; b < 3; ++b)
     if (a.out_cs[b] > 32 * mh) return 1;
   // epilogue staging: 128 branch-0 pixels per stage object (the last also the tail, then branch 2),
-  // a pooled row of branch 1 behind the first two
-  if (128 * a.out_cs[0] + (a.w / 2) * a.out_cs[1] > BD_XSA ||
+  // branch 1 behind the first
+  if (128 * a.out_cs[0] + a.w * a.out_cs[1] > BD_XSA ||
       max(4 * a.w - 256, 0) * a.out_cs[0] + (a.w / 4) * a.out_cs[2] > BD_XSA)
     return 1;
   if (a.dtype == KAD_F16) {

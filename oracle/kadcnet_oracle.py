@@ -74,6 +74,12 @@ def _gelan(sd, p, x, kadc):
     return _conv(sd, p + 'cv4.', torch.cat(y, 1))
 
 
+def _aconv(sd, p, x, eps=BN_EPS):
+    """2 x 2 average pool, stride 1, no padding (count_include_pad), then the 3x3 stride-2 Conv cv1
+    (common.py:60-67)."""
+    return _conv(sd, p + 'cv1.', F.avg_pool2d(x, 2, 1, 0, False, True), s=2, eps=eps)
+
+
 def _sppelan(sd, p, x):
     y = [_conv(sd, p + 'cv1.', x)]
     for _ in range(3):
@@ -132,7 +138,7 @@ def kadcnet_forward(sd, cfg, x, eps=BN_EPS, layers=None):
         if m == 'Conv':
             cur = _conv(sd, p, cur, s=args[2] if len(args) > 2 else 1, eps=eps)
         elif m == 'AConv':
-            cur = _conv(sd, p + 'cv1.', F.avg_pool2d(cur, 2, 1, 0, False, True), s=2, eps=eps)
+            cur = _aconv(sd, p, cur, eps=eps)
         elif m == 'ELAN1':
             cur = _gelan(sd, p, cur, kadc=False)
         elif m == 'RepNCSPELAN4_KADC':

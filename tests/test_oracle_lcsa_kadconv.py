@@ -5,10 +5,14 @@ with explicit numpy loops: with a[h] = mean_w x[h, :], b[w] = mean_h x[:, w],
 the 1x11 depthwise conv of a[h] + b[w] equals a[h] * S(w) + B(w) + bias where
 S(w) sums the in-image taps and B(w) is the 1-D conv of b.  KADConv is checked
 for n=1 against a composition from torch modules built with the reference's
-module list (kad_conv.py:100-110) and state-dict keys."""
+module list (kad_conv.py:100-110) and state-dict keys.  KADDown (builder-defined)
+is pinned on linear inputs: block means and the bilinear resize are exact on
+lines, so each branch has a closed form whose border clamping fixes its pool
+factor and resize rule; one-hot mixture logits fix the logit / branch pairing."""
 import math
 
 import numpy as np
+import pytest
 import torch
 import torch.nn as nn
 
@@ -146,6 +150,40 @@ def test_kaddown_collapses_to_single_conv_on_blockwise_constant_input():
 
 def _sigmoid(v):
     return 1.0 / (1.0 + np.exp(-v))
+
+
+@pytest.mark.parametrize('istar', [0, 1, 2])
+def test_kaddown_ramp_pins_pool_factor_resize_rule_and_branch_order(istar):
+    """Branch i of KADDown averages 2^(i+1) x 2^(i+1) blocks and resizes the result bilinearly
+    (align_corners=False) to (H/2, W/2).  On a linear input x_c = a_c + b_c h + d_c w both steps
+    are exact on lines: a block mean samples the line at the block centre, and the resize places
+    output row j at source position 2 j + 0.5 of the full-resolution grid, clamped to the centre
+    range [e_i, H - 1 - e_i] of the pooled samples, e_i = (2^(i+1) - 1) / 2.  So branch i at
+    (j, k) is W_i L(clamp(2 j + 0.5, e_i, H - 1 - e_i), clamp(2 k + 0.5, e_i, W - 1 - e_i)) + b_i,
+    computed here with numpy.  One-hot mixture logits (+-30) select branch istar, and each branch
+    has its own weights: a wrong pool factor (2^i), align_corners=True, a swapped logit / branch
+    pairing or a missing gate each move the result by more than the 1e-9 bound."""
+    c1, c2, H, W = 3, 4, 32, 40
+    sd = S.make_kaddown_state(c1, c2, seed=11, dtype=torch.float64)
+    sd['alpha'] = torch.full((3,), -30.0, dtype=torch.float64)
+    sd['alpha'][istar] = 30.0
+    g = torch.Generator().manual_seed(12)
+    a = torch.rand(c1, generator=g, dtype=torch.float64)
+    b = torch.rand(c1, generator=g, dtype=torch.float64) * 0.3
+    d = torch.rand(c1, generator=g, dtype=torch.float64) * 0.3 - 0.15
+    hh = torch.arange(H, dtype=torch.float64).view(1, H, 1)
+    ww = torch.arange(W, dtype=torch.float64).view(1, 1, W)
+    x = (a.view(c1, 1, 1) + b.view(c1, 1, 1) * hh + d.view(c1, 1, 1) * ww).unsqueeze(0)
+    got = O.kaddown_forward(sd, x)[0].numpy()
+    e = (2 ** (istar + 1) - 1) / 2
+    ph = np.clip(2 * np.arange(H // 2) + 0.5, e, H - 1 - e)
+    pw = np.clip(2 * np.arange(W // 2) + 0.5, e, W - 1 - e)
+    lines = a.numpy()[:, None, None] + b.numpy()[:, None, None] * ph[None, :, None] + d.numpy()[:, None, None] * pw[None, None, :]
+    wi = sd[f'proj.{istar}.weight'].numpy().reshape(c2, c1)
+    ref = np.einsum('oc,chw->ohw', wi, lines) + sd[f'proj.{istar}.bias'].numpy()[:, None, None]
+    ref = ref / (1.0 + np.exp(-sd['gate'].numpy()))[:, None, None]
+    assert got.shape == (c2, H // 2, W // 2)
+    assert np.abs(got - ref).max() <= 1e-9, np.abs(got - ref).max()
 
 
 def test_kadconv_three_branches_zero_dsc_weights_give_constant_branches():

@@ -1,8 +1,18 @@
-"""KAD-CNet building blocks with the reference's class names, constructor
-arguments and attribute names (KAD-CNet/models/common.py), so that state dicts
-and module trees line up with the reference's DetectionModel.  Forward passes
-are the plain PyTorch compositions the reference defines; they run on CPU or
-GPU.  The HIP network forward lives in kadcnet.fast.
+"""KAD-CNet building blocks.
+
+What has to match the reference (KAD-CNet/models/common.py) is the module tree: class names,
+constructor arguments, attribute names and the order submodules are created in (so state dicts,
+class-name discovery and seeded initialisation line up).  The forwards are written here from the
+blocks' math:
+
+  Conv     act(BN(conv_k,s,g,d(x))), 'same' padding d (k - 1) / 2; after fusion BN is gone
+  AConv    Conv_3x3,s2(mean over each 2 x 2 window, stride 1, no padding)
+  SPPELAN  t0 = cv1(x), t_{i+1} = maxpool_5x5,s1,pad2(t_i) for i < 3, cv5([t0 t1 t2 t3])
+  ELAN1    h = cv1(x) split into halves a | b (a the larger for odd widths, as torch.chunk),
+           c = cv2(b), d = cv3(c), cv4([a b c d])
+  DFL      expected bin index under a softmax over each side's c1 logits
+
+The HIP network forward lives in kadcnet.fast.
 """
 import math
 
@@ -12,50 +22,56 @@ import torch.nn.functional as F
 
 
 def make_divisible(x, divisor):
-    """Round x up to a multiple of divisor (KAD-CNet/utils/general.py:660-664)."""
-    return math.ceil(x / divisor) * divisor
+    """The smallest multiple of divisor that is >= x (KAD-CNet/utils/general.py:660-664)."""
+    return int(math.ceil(x / divisor)) * divisor
 
 
-def autopad(k, p=None, d=1):
-    """'same' padding for an odd kernel (common.py:34-40)."""
-    if d > 1:
-        k = d * (k - 1) + 1 if isinstance(k, int) else [d * (x - 1) + 1 for x in k]
-    if p is None:
-        p = k // 2 if isinstance(k, int) else [x // 2 for x in k]
-    return p
+def _same_padding(k, p, d):
+    """Explicit padding p, or the padding that keeps the size at stride 1: half the dilated
+    kernel extent d (k - 1) (per dimension for a tuple k)."""
+    if p is not None:
+        return p
+    if isinstance(k, int):
+        return d * (k - 1) // 2
+    return [d * (e - 1) // 2 for e in k]
+
+
+def _activation(act):
+    if act is True:
+        return nn.SiLU()
+    return act if isinstance(act, nn.Module) else nn.Identity()
 
 
 class Conv(nn.Module):
-    """conv (no bias) -> BatchNorm -> SiLU (common.py:43-57).  After ``fuse``
-    the BN is folded into a biased conv and ``forward_fuse`` runs."""
-    default_act = nn.SiLU()
+    """Convolution without bias, BatchNorm, activation (SiLU unless act says otherwise).
+    DetectionModel.fuse folds the BatchNorm into a biased convolution and removes ``bn``."""
 
     def __init__(self, c1, c2, k=1, s=1, p=None, g=1, d=1, act=True):
         super().__init__()
-        self.conv = nn.Conv2d(c1, c2, k, s, autopad(k, p, d), groups=g, dilation=d, bias=False)
+        self.conv = nn.Conv2d(c1, c2, k, stride=s, padding=_same_padding(k, p, d), dilation=d, groups=g,
+                              bias=False)
         self.bn = nn.BatchNorm2d(c2)
-        self.act = self.default_act if act is True else act if isinstance(act, nn.Module) else nn.Identity()
+        self.act = _activation(act)
 
     def forward(self, x):
-        return self.act(self.bn(self.conv(x)))
-
-    def forward_fuse(self, x):
-        return self.act(self.conv(x))
+        y = self.conv(x)
+        bn = getattr(self, 'bn', None)
+        return self.act(y if bn is None else bn(y))
 
 
 class AConv(nn.Module):
-    """2x2 / stride-1 average pool, then a 3x3 stride-2 Conv (common.py:60-67)."""
+    """Downsampler: 2 x 2 window mean at stride 1, then a 3 x 3 stride-2 Conv."""
 
     def __init__(self, c1, c2):
         super().__init__()
         self.cv1 = Conv(c1, c2, 3, 2, 1)
 
     def forward(self, x):
-        return self.cv1(F.avg_pool2d(x, 2, 1, 0, False, True))
+        return self.cv1(F.avg_pool2d(x, kernel_size=2, stride=1))
 
 
 class SP(nn.Module):
-    """Max pool, stride 1, 'same' padding (common.py:187-193)."""
+    """Max pool, stride 1, 'same' padding."""
 
     def __init__(self, k=3, s=1):
         super().__init__()
@@ -66,16 +82,18 @@ class SP(nn.Module):
 
 
 class Concat(nn.Module):
+    """Concatenation of a list of maps along dimension ``d``."""
+
     def __init__(self, dimension=1):
         super().__init__()
         self.d = dimension
 
     def forward(self, x):
-        return torch.cat(x, self.d)
+        return torch.cat(list(x), dim=self.d)
 
 
 class SPPELAN(nn.Module):
-    """cv1, three chained 5x5 max pools, concat of all four, cv5 (common.py:563-577)."""
+    """Spatial pyramid pooling: cv1, three chained 5 x 5 max pools, the four maps side by side, cv5."""
 
     def __init__(self, c1, c2, c3):
         super().__init__()
@@ -87,13 +105,27 @@ class SPPELAN(nn.Module):
         self.cv5 = Conv(4 * c3, c2, 1, 1)
 
     def forward(self, x):
-        y = [self.cv1(x)]
-        y.extend(m(y[-1]) for m in [self.cv2, self.cv3, self.cv4])
-        return self.cv5(torch.cat(y, 1))
+        t = self.cv1(x)
+        pyramid = [t]
+        for pool in (self.cv2, self.cv3, self.cv4):
+            t = pool(t)
+            pyramid.append(t)
+        return self.cv5(torch.cat(pyramid, dim=1))
+
+
+def elan_forward(cv1, stage_a, stage_b, cv4, x):
+    """The ELAN pattern shared by ELAN1 and RepNCSPELAN4_KADC: h = cv1(x) split into a | b
+    (a = the first ceil(C / 2) channels), c = stage_a(b), d = stage_b(c), cv4([a b c d])."""
+    h = cv1(x)
+    k = (h.shape[1] + 1) // 2
+    a, b = h[:, :k], h[:, k:]
+    c = stage_a(b)
+    d = stage_b(c)
+    return cv4(torch.cat((a, b, c, d), dim=1))
 
 
 class ELAN1(nn.Module):
-    """cv1 split in two halves; cv2, cv3 chained on the second; concat; cv4 (common.py:580-598)."""
+    """ELAN with two plain 3 x 3 Convs on the second half of cv1's output."""
 
     def __init__(self, c1, c2, c3, c4):
         super().__init__()
@@ -101,27 +133,29 @@ class ELAN1(nn.Module):
         self.cv1 = Conv(c1, c3, 1, 1)
         self.cv2 = Conv(c3 // 2, c4, 3, 1)
         self.cv3 = Conv(c4, c4, 3, 1)
-        self.cv4 = Conv(c3 + (2 * c4), c2, 1, 1)
+        self.cv4 = Conv(c3 + 2 * c4, c2, 1, 1)
 
     def forward(self, x):
-        y = list(self.cv1(x).chunk(2, 1))
-        y.extend(m(y[-1]) for m in [self.cv2, self.cv3])
-        return self.cv4(torch.cat(y, 1))
+        return elan_forward(self.cv1, self.cv2, self.cv3, self.cv4, x)
 
 
 class DFL(nn.Module):
-    """Distribution focal loss integral: softmax over c1 bins, expectation of the
-    bin index (common.py:232-244)."""
+    """Box side distance from c1 bin logits: sum_k k softmax(l)_k.  The bin values are the weights
+    of a frozen 1 x 1 conv (0, 1, ..., c1 - 1), as in the reference's state dict."""
 
     def __init__(self, c1=17):
         super().__init__()
-        self.conv = nn.Conv2d(c1, 1, 1, bias=False).requires_grad_(False)
-        self.conv.weight.data[:] = torch.arange(c1, dtype=torch.float).view(1, c1, 1, 1)
         self.c1 = c1
+        self.conv = nn.Conv2d(c1, 1, 1, bias=False).requires_grad_(False)
+        with torch.no_grad():
+            self.conv.weight.copy_(torch.arange(c1, dtype=torch.float32).view(1, c1, 1, 1))
 
     def forward(self, x):
-        b, _, a = x.shape
-        return self.conv(x.view(b, 4, self.c1, a).transpose(2, 1).softmax(1)).view(b, 4, a)
+        """x [B, 4 c1, A] -> [B, 4, A]."""
+        b, _, n = x.shape
+        p = x.view(b, 4, self.c1, n).softmax(dim=2)
+        bins = self.conv.weight.view(1, 1, self.c1, 1).to(p.dtype)
+        return (p * bins).sum(dim=2)
 
 
 def fuse_conv_and_bn(conv, bn):

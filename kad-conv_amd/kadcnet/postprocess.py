@@ -1,31 +1,39 @@
-"""Detection post-processing: non_max_suppression with the reference's
-signature and steps (KAD-CNet/utils/general.py:881-990), its IoU suppression on
-the GPU through the HIP kad_nms kernels (the reference calls
-torchvision.ops.nms, which this image does not ship).
+"""Detection post-processing on the GPU: candidate selection, class-aware greedy NMS (the HIP
+kad_nms kernels stand in for torchvision.ops.nms, which this image does not ship).
 
-Candidate filtering, the best-class pick and the score sort are tensor
-indexing on the prediction's device.  The sort is stable (ties keep anchor
-order), so the kept indices are deterministic.
+``non_max_suppression`` keeps the reference's call signature and result format
+(KAD-CNet/utils/general.py:881-990: per image a [k, 6] tensor of x1, y1, x2, y2, score, class in
+descending score order).  What it does, per image:
+
+  1. candidates: anchors whose best class probability exceeds conf_thres (every (anchor, class)
+     pair above it with multi_label), optionally only the listed classes;
+  2. boxes (cx, cy, w, h) -> corners;
+  3. order by score, descending, stable (ties keep anchor order), at most 30000;
+  4. class-aware NMS: a box is suppressed by a higher-scoring kept box of the same class whose IoU
+     with it exceeds iou_thres (classes are kept apart by shifting every box by 7680 px per
+     class index, wider than any input, unless agnostic);
+  5. at most max_det survivors.
+
+The reference's ``labels`` (autolabelling: prepend known boxes) and ``nm`` (mask coefficients) are
+not supported: nothing on the KAD-CNet inference path uses them.
 """
 import torch
 
 from kadconv import _ext
 
+_CLASS_SHIFT = 7680   # px per class index: boxes of different classes never overlap
+_MAX_CANDIDATES = 30000
+
 
 def xywh2xyxy(x):
-    """(cx, cy, w, h) -> (x1, y1, x2, y2) (utils/general.py xywh2xyxy)."""
-    y = x.clone()
-    y[..., 0] = x[..., 0] - x[..., 2] / 2
-    y[..., 1] = x[..., 1] - x[..., 3] / 2
-    y[..., 2] = x[..., 0] + x[..., 2] / 2
-    y[..., 3] = x[..., 1] + x[..., 3] / 2
-    return y
+    """(cx, cy, w, h, ...) -> (x1, y1, x2, y2, ...) along the last dimension (other columns kept)."""
+    centre, size = x[..., :2], x[..., 2:4]
+    return torch.cat((centre - size / 2, centre + size / 2, x[..., 4:]), dim=-1)
 
 
 def nms(boxes, scores, iou_threshold):
-    """Indices of the boxes kept by greedy NMS, by descending score (the contract of
-    torchvision.ops.nms): a box is dropped when its IoU with a kept box of higher
-    score exceeds iou_threshold.  GPU tensors only."""
+    """Indices (descending score) of the boxes greedy NMS keeps: a box is dropped when its IoU with
+    a kept box of higher score exceeds iou_threshold (the torchvision.ops.nms contract).  GPU only."""
     if not boxes.is_cuda:
         raise ValueError('kadcnet.postprocess.nms runs on the GPU (HIP kad_nms)')
     if boxes.shape[0] == 0:
@@ -37,49 +45,42 @@ def nms(boxes, scores, iou_threshold):
     return order[keep.bool()]
 
 
+def _candidates(p, conf_thres, multi_label, classes):
+    """[k, 6] (x1, y1, x2, y2, score, class) of one image's prediction p [4 + nc, A]."""
+    boxes = xywh2xyxy(p[:4].t())
+    probs = p[4:].t()
+    if multi_label and probs.shape[1] > 1:
+        a, c = (probs > conf_thres).nonzero(as_tuple=True)
+        rows = torch.cat((boxes[a], probs[a, c, None], c[:, None].to(p.dtype)), 1)
+    else:
+        score, c = probs.max(1)
+        keep = score > conf_thres
+        rows = torch.cat((boxes[keep], score[keep, None], c[keep, None].to(p.dtype)), 1)
+    if classes is not None:
+        rows = rows[torch.isin(rows[:, 5], torch.as_tensor(classes, dtype=rows.dtype, device=rows.device))]
+    return rows
+
+
 def non_max_suppression(prediction, conf_thres=0.25, iou_thres=0.45, classes=None, agnostic=False,
                         multi_label=False, labels=(), max_det=300, nm=0):
-    """Per image: candidates whose best class score exceeds conf_thres, xywh ->
-    xyxy, best class (or every class above conf_thres with multi_label), sort by
-    score (at most 30000), class-offset boxes (7680 px per class unless
-    agnostic), NMS at iou_thres, at most max_det.  Returns a list of [k, 6 + nm]
-    tensors (x1, y1, x2, y2, conf, cls).  As general.py:881-990 without its
-    wall-clock time limit and merge-NMS (off there)."""
+    """Per image of ``prediction`` [N, 4 + nc, A] (or a tuple whose first entry it is): the list of
+    [k, 6] detections described in the module docstring."""
     if isinstance(prediction, (list, tuple)):
         prediction = prediction[0]
-    assert 0 <= conf_thres <= 1 and 0 <= iou_thres <= 1
-    bs = prediction.shape[0]
-    nc = prediction.shape[1] - nm - 4
-    mi = 4 + nc
-    xc = prediction[:, 4:mi].amax(1) > conf_thres
-    max_wh, max_nms = 7680, 30000
-    multi_label &= nc > 1
-    output = [torch.zeros((0, 6 + nm), device=prediction.device)] * bs
-    for xi, x in enumerate(prediction):
-        x = x.T[xc[xi]]
-        if labels and len(labels[xi]):
-            lb = labels[xi]
-            v = torch.zeros((len(lb), nc + nm + 5), device=x.device)
-            v[:, :4] = lb[:, 1:5]
-            v[range(len(lb)), lb[:, 0].long() + 4] = 1.0
-            x = torch.cat((x, v), 0)
-        if not x.shape[0]:
-            continue
-        box, cls, mask = x.split((4, nc, nm), 1)
-        box = xywh2xyxy(box)
-        if multi_label:
-            i, j = (cls > conf_thres).nonzero(as_tuple=False).T
-            x = torch.cat((box[i], x[i, 4 + j, None], j[:, None].float(), mask[i]), 1)
+    if not (0 <= conf_thres <= 1 and 0 <= iou_thres <= 1):
+        raise ValueError(f'conf_thres {conf_thres} and iou_thres {iou_thres} must lie in [0, 1]')
+    if nm or any(len(lb) for lb in labels):
+        raise NotImplementedError('non_max_suppression: labels and mask coefficients (nm) are not supported')
+    out = []
+    for p in prediction:
+        # 16-bit predictions are processed in fp32: the class shift (up to 7680 nc px) exceeds fp16's range
+        p = p if p.dtype == torch.float64 else p.float()
+        rows = _candidates(p, conf_thres, multi_label, classes)
+        if rows.shape[0]:
+            rows = rows[torch.sort(rows[:, 4], descending=True, stable=True).indices[:_MAX_CANDIDATES]]
+            shift = rows[:, 5:6] * (0 if agnostic else _CLASS_SHIFT)
+            rows = rows[nms(rows[:, :4] + shift, rows[:, 4], iou_thres)[:max_det]]
         else:
-            conf, j = cls.max(1, keepdim=True)
-            x = torch.cat((box, conf, j.float(), mask), 1)[conf.view(-1) > conf_thres]
-        if classes is not None:
-            x = x[(x[:, 5:6] == torch.tensor(classes, device=x.device)).any(1)]
-        n = x.shape[0]
-        if not n:
-            continue
-        x = x[torch.sort(x[:, 4], descending=True, stable=True).indices[:max_nms]]
-        c = x[:, 5:6] * (0 if agnostic else max_wh)
-        i = nms(x[:, :4] + c, x[:, 4], iou_thres)
-        output[xi] = x[i[:max_det]]
-    return output
+            rows = torch.zeros((0, 6), dtype=p.dtype, device=p.device)
+        out.append(rows)
+    return out

@@ -1,13 +1,18 @@
-"""KAD-CNet detection model: DDetect head, model builder and DetectionModel,
-following KAD-CNet/models/yolo.py (DDetect :78-136, BaseModel :533-599,
-DetectionModel :602-659, parse_model :744-819) and
-KAD-CNet/utils/tal/anchor_generator.py:8-32 (make_anchors, dist2bbox).
+"""KAD-CNet detection model: the DDetect head, the layer builder and DetectionModel.
 
-The builder reads the same model dictionary as the reference's YAML files
-(``nc``, ``depth_multiple``, ``width_multiple``, ``backbone`` and ``head`` rows of
-[from, number, module, args]); ``DIOR_S_BASE`` / ``DIOR_S_MGL`` are the two
-KAD-CNet-S configurations (KAD-CNet/configs/dior_s_{base,mgl}.yaml).  Modules are
-looked up by name in a registry (the reference evals the strings).
+Kept from the reference (KAD-CNet/models/yolo.py, utils/tal/anchor_generator.py:8-32) because state
+dicts, the channel plan and the decoded boxes depend on them: class and attribute names, the
+order submodules are created in, DDetect's branch widths, the ``model.{i}`` layer numbering with
+its ``from`` indices, and the box formulas.  The code is this package's:
+
+  anchors      cell centres (x + 0.5, y + 0.5) of every level, row-major, levels in order
+  dist2bbox    (l, t, r, b) distances around an anchor -> (cx, cy, w, h) or (x1, y1, x2, y2)
+  DDetect      per level cat(box branch, class branch); inference: DFL distances -> boxes times
+               the level stride, class sigmoid
+  parse_model  widths of the width-scaled blocks rounded up to multiples of 8, repeats scaled by
+               depth, Concat widths summed, DDetect given its inputs' widths
+
+``DIOR_S_BASE`` / ``DIOR_S_MGL`` restate the rows of KAD-CNet/configs/dior_s_{base,mgl}.yaml.
 """
 import copy
 import math
@@ -20,113 +25,108 @@ from .kadc import RepNCSPELAN4_KADC
 
 
 def make_anchors(feats, strides, grid_cell_offset=0.5):
-    """Cell centres (x + 0.5, y + 0.5) of every level, row-major, and their
-    strides (anchor_generator.py:8-21)."""
-    points, stride_t = [], []
-    dtype, device = feats[0].dtype, feats[0].device
-    for i, stride in enumerate(strides):
-        _, _, h, w = feats[i].shape
-        sx = torch.arange(w, device=device, dtype=dtype) + grid_cell_offset
-        sy = torch.arange(h, device=device, dtype=dtype) + grid_cell_offset
-        sy, sx = torch.meshgrid(sy, sx, indexing='ij')
-        points.append(torch.stack((sx, sy), -1).view(-1, 2))
-        stride_t.append(torch.full((h * w, 1), float(stride), dtype=dtype, device=device))
-    return torch.cat(points), torch.cat(stride_t)
+    """(points [A, 2] as (x, y), stride per point [A, 1]) over the levels' maps, each level's cells
+    in row-major order."""
+    points, per_point = [], []
+    for f, s in zip(feats, strides):
+        h, w = f.shape[-2:]
+        xs = torch.arange(w, dtype=f.dtype, device=f.device) + grid_cell_offset
+        ys = torch.arange(h, dtype=f.dtype, device=f.device) + grid_cell_offset
+        points.append(torch.stack((xs.repeat(h), ys.repeat_interleave(w)), dim=1))
+        per_point.append(torch.full((h * w, 1), float(s), dtype=f.dtype, device=f.device))
+    return torch.cat(points), torch.cat(per_point)
 
 
 def dist2bbox(distance, anchor_points, xywh=True, dim=-1):
-    """(left, top, right, bottom) distances -> xywh or xyxy boxes (anchor_generator.py:24-32)."""
-    lt, rb = torch.split(distance, 2, dim)
-    x1y1 = anchor_points - lt
-    x2y2 = anchor_points + rb
+    """Side distances (left, top, right, bottom) along ``dim`` around anchor points -> boxes."""
+    near, far = distance.chunk(2, dim)
+    lo, hi = anchor_points - near, anchor_points + far
     if xywh:
-        return torch.cat(((x1y1 + x2y2) / 2, x2y2 - x1y1), dim)
-    return torch.cat((x1y1, x2y2), dim)
+        return torch.cat(((lo + hi) / 2, hi - lo), dim)
+    return torch.cat((lo, hi), dim)
 
 
 class DDetect(nn.Module):
-    """Anchor-free detection head (yolo.py:78-136): per level a box branch
-    (3x3 Conv, grouped 3x3 Conv, grouped 1x1 -> 4 x reg_max) and a class branch
-    (3x3 Conv, 3x3 Conv, 1x1 -> nc); inference decodes DFL distances into xywh
-    boxes times the level stride and applies the class sigmoid."""
-    dynamic = False
-    export = False
-    shape = None
-    anchors = torch.empty(0)
-    strides = torch.empty(0)
+    """Anchor-free head.  Level i: box branch cv2[i] = (3 x 3 Conv, 3 x 3 Conv in 4 groups, 1 x 1 conv
+    in 4 groups -> 4 reg_max bin logits), class branch cv3[i] = (3 x 3 Conv, 3 x 3 Conv, 1 x 1 conv
+    -> nc logits).  Training returns the per-level maps; inference returns (y [N, 4 + nc, A], maps)
+    with y = (cx, cy, w, h) in input pixels and the class probabilities."""
+    dynamic = False   # recompute the anchors on every call
+    export = False    # inference returns y alone
 
     def __init__(self, nc=80, ch=(), inplace=True):
         super().__init__()
         self.nc = nc
         self.nl = len(ch)
         self.reg_max = 16
-        self.no = nc + self.reg_max * 4
+        self.no = nc + 4 * self.reg_max
         self.inplace = inplace
         self.stride = torch.zeros(self.nl)
-        c2 = make_divisible(max((ch[0] // 4, self.reg_max * 4, 16)), 4)
-        c3 = max((ch[0], min((self.nc * 2, 128))))
-        self.cv2 = nn.ModuleList(
-            nn.Sequential(Conv(x, c2, 3), Conv(c2, c2, 3, g=4), nn.Conv2d(c2, 4 * self.reg_max, 1, groups=4))
-            for x in ch)
-        self.cv3 = nn.ModuleList(
-            nn.Sequential(Conv(x, c3, 3), Conv(c3, c3, 3), nn.Conv2d(c3, self.nc, 1)) for x in ch)
+        box_w = make_divisible(max(ch[0] // 4, 4 * self.reg_max, 16), 4)
+        cls_w = max(ch[0], min(2 * nc, 128))
+        self.cv2 = nn.ModuleList([nn.Sequential(Conv(c, box_w, 3), Conv(box_w, box_w, 3, g=4),
+                                                nn.Conv2d(box_w, 4 * self.reg_max, 1, groups=4)) for c in ch])
+        self.cv3 = nn.ModuleList([nn.Sequential(Conv(c, cls_w, 3), Conv(cls_w, cls_w, 3), nn.Conv2d(cls_w, nc, 1))
+                                  for c in ch])
         self.dfl = DFL(self.reg_max) if self.reg_max > 1 else nn.Identity()
+        self.shape, self.anchors, self.strides = None, torch.empty(0), torch.empty(0)
 
     def forward(self, x):
-        shape = x[0].shape
-        for i in range(self.nl):
-            x[i] = torch.cat((self.cv2[i](x[i]), self.cv3[i](x[i])), 1)
+        maps = [torch.cat((box(f), cls(f)), 1) for f, box, cls in zip(x, self.cv2, self.cv3)]
         if self.training:
-            return x
-        if self.dynamic or self.shape != shape:
-            self.anchors, self.strides = (t.transpose(0, 1) for t in make_anchors(x, self.stride, 0.5))
-            self.shape = shape
-        box, cls = torch.cat([xi.view(shape[0], self.no, -1) for xi in x], 2).split((self.reg_max * 4, self.nc), 1)
-        dbox = dist2bbox(self.dfl(box), self.anchors.unsqueeze(0), xywh=True, dim=1) * self.strides
-        y = torch.cat((dbox, cls.sigmoid()), 1)
-        return y if self.export else (y, x)
+            return maps
+        if self.dynamic or self.shape != maps[0].shape:
+            pts, st = make_anchors(maps, self.stride, 0.5)
+            self.anchors, self.strides, self.shape = pts.t(), st.t(), maps[0].shape
+        flat = torch.cat([m.flatten(2) for m in maps], 2)                      # [N, no, A]
+        nb = 4 * self.reg_max
+        boxes = dist2bbox(self.dfl(flat[:, :nb]), self.anchors.unsqueeze(0), xywh=True, dim=1) * self.strides
+        y = torch.cat((boxes, flat[:, nb:].sigmoid()), 1)
+        return y if self.export else (y, maps)
 
     def bias_init(self):
-        """Box logits 1.0; class logits log(5 / nc / (640 / s)^2) (yolo.py:129-136)."""
-        for a, b, s in zip(self.cv2, self.cv3, self.stride):
-            a[-1].bias.data[:] = 1.0
-            b[-1].bias.data[:self.nc] = math.log(5 / self.nc / (640 / s) ** 2)
+        """Initial biases: box logits 1; class logits log(5 / nc) - 2 log(640 / stride), a prior of
+        about 5 objects per 640 x 640 image spread over the level's cells and the classes."""
+        for box, cls, s in zip(self.cv2, self.cv3, self.stride):
+            box[-1].bias.data.fill_(1.0)
+            cls[-1].bias.data[:self.nc] = math.log(5 / self.nc) - 2 * math.log(640 / float(s))
 
 
 MODULES = {'Conv': Conv, 'AConv': AConv, 'ELAN1': ELAN1, 'SPPELAN': SPPELAN, 'RepNCSPELAN4_KADC': RepNCSPELAN4_KADC,
            'Concat': Concat, 'nn.Upsample': nn.Upsample, 'DDetect': DDetect}
-_WIDTH_SCALED = {Conv, AConv, ELAN1, SPPELAN, RepNCSPELAN4_KADC}
+_WIDTH_SCALED = (Conv, AConv, ELAN1, SPPELAN, RepNCSPELAN4_KADC)
+
+
+def _arg(a, nc):
+    return nc if a == 'nc' else (None if a == 'None' else a)
 
 
 def parse_model(d, ch):
-    """Build the layer list from a model dictionary (yolo.py:744-819):
-    output widths of the listed block types are scaled by width_multiple and
-    rounded up to a multiple of 8; repeats by depth_multiple; Concat sums its
-    inputs' widths; DDetect receives its inputs' widths.  Returns
-    (nn.Sequential of layers with .i / .f / .type attributes, save list)."""
-    nc, gd, gw = d['nc'], d['depth_multiple'], d['width_multiple']
-    layers, save, c2 = [], [], ch[-1]
-    for i, (f, n, m, args) in enumerate(d['backbone'] + d['head']):
-        name = m
-        m = MODULES[m]
-        args = [nc if a == 'nc' else None if a == 'None' else a for a in args]
-        n = max(round(n * gd), 1) if n > 1 else n
-        if m in _WIDTH_SCALED:
-            c1, c2 = ch[f], make_divisible(args[0] * gw, 8)
-            args = [c1, c2, *args[1:]]
-        elif m is Concat:
-            c2 = sum(ch[x] for x in f)
-        elif m is DDetect:
-            args.append([ch[x] for x in f])
+    """(nn.Sequential of the layers, each tagged with .i / .f / .type, sorted list of the layer
+    indices whose outputs later layers read) from a model dictionary; ``ch`` = [input channels]."""
+    nc, depth, width = d['nc'], d['depth_multiple'], d['width_multiple']
+    widths = []                                     # output width of each layer built so far
+    layers, save = [], set()
+    for i, (f, n, name, args) in enumerate(d['backbone'] + d['head']):
+        cls = MODULES[name]
+        args = [_arg(a, nc) for a in args]
+        width_of = (lambda j: widths[j]) if widths else (lambda j: ch[j])
+        reps = max(round(n * depth), 1) if n > 1 else n
+        if cls in _WIDTH_SCALED:
+            c_out = make_divisible(args[0] * width, 8)
+            args = [width_of(f), c_out] + args[1:]
+        elif cls is Concat:
+            c_out = sum(width_of(j) for j in f)
+        elif cls is DDetect:
+            args = args + [[width_of(j) for j in f]]
+            c_out = None
         else:
-            c2 = ch[f]
-        m_ = nn.Sequential(*(m(*args) for _ in range(n))) if n > 1 else m(*args)
-        m_.i, m_.f, m_.type = i, f, name
-        save.extend(x % i for x in ([f] if isinstance(f, int) else f) if x != -1)
-        layers.append(m_)
-        if i == 0:
-            ch = []
-        ch.append(c2)
+            c_out = width_of(f)
+        block = cls(*args) if reps == 1 else nn.Sequential(*[cls(*args) for _ in range(reps)])
+        block.i, block.f, block.type = i, f, name
+        save.update(j % i for j in ([f] if isinstance(f, int) else f) if j != -1)
+        layers.append(block)
+        widths.append(c_out)
     return nn.Sequential(*layers), sorted(save)
 
 
@@ -169,11 +169,11 @@ DIOR_S_BASE = {
 
 
 def _mgl(cfg):
-    """The MGL variant: KADC4_m (hidden >= 64) in every KAD-Conv block."""
+    """The MGL configuration: every KAD-Conv block built with KADC4_m (hidden >= 64)."""
     d = copy.deepcopy(cfg)
     for row in d['backbone'] + d['head']:
         if row[2] == _KADC_ELAN:
-            row[3] = row[3] + ['KADC4_m']
+            row[3] = list(row[3]) + ['KADC4_m']
     d['mgl_encoder_channels'] = [40, 72, 144, 216, 288]
     return d
 
@@ -182,27 +182,26 @@ DIOR_S_MGL = _mgl(DIOR_S_BASE)
 
 
 class DetectionModel(nn.Module):
-    """KAD-CNet detection model (yolo.py:533-659): layers from parse_model, the
-    forward threads earlier outputs to multi-input layers by their 'from'
-    indices, strides come from a 256 x 256 probe, BN eps 1e-3 / momentum 0.03
-    (utils/torch_utils.py:208-217).  The MGL decoders (training only) are not
-    built."""
+    """The detector: ``model`` (layers from parse_model), ``save``, ``stride`` (from a 256 x 256
+    probe forward at construction), the DDetect bias prior, and BatchNorm eps 1e-3 / momentum 0.03
+    (KAD-CNet/utils/torch_utils.py:208-217).  The MGL decoders (training only) are not built."""
 
     def __init__(self, cfg=DIOR_S_BASE, ch=3, nc=None):
         super().__init__()
         self.yaml = copy.deepcopy(cfg)
-        ch = self.yaml['ch'] = self.yaml.get('ch', ch)
+        in_ch = self.yaml.setdefault('ch', ch)
         if nc and nc != self.yaml['nc']:
             self.yaml['nc'] = nc
-        self.model, self.save = parse_model(copy.deepcopy(self.yaml), ch=[ch])
-        self.names = [str(i) for i in range(self.yaml['nc'])]
+        self.model, self.save = parse_model(copy.deepcopy(self.yaml), ch=[in_ch])
+        self.names = [str(k) for k in range(self.yaml['nc'])]
         self.inplace = self.yaml.get('inplace', True)
-        m = self.model[-1]
-        s = 256
-        m.inplace = self.inplace
-        m.stride = torch.tensor([s / x.shape[-2] for x in self.forward(torch.zeros(1, ch, s, s))])
-        self.stride = m.stride
-        m.bias_init()
+        head = self.model[-1]
+        head.inplace = self.inplace
+        probe = 256
+        maps = self.forward(torch.zeros(1, in_ch, probe, probe))   # training mode: the head returns its maps
+        head.stride = torch.tensor([probe / m.shape[-2] for m in maps])
+        self.stride = head.stride
+        head.bias_init()
         for mod in self.modules():
             if type(mod) is nn.BatchNorm2d:
                 mod.eps, mod.momentum = 1e-3, 0.03
@@ -210,29 +209,29 @@ class DetectionModel(nn.Module):
                 mod.inplace = True
 
     def forward(self, x):
-        y = []
-        for m in self.model:
-            if m.f != -1:
-                x = y[m.f] if isinstance(m.f, int) else [x if j == -1 else y[j] for j in m.f]
-            x = m(x)
-            y.append(x)
+        outputs = {}
+        for layer in self.model:
+            f = layer.f
+            if f != -1:
+                x = outputs[f] if isinstance(f, int) else [x if j == -1 else outputs[j] for j in f]
+            x = layer(x)
+            outputs[layer.i] = x
         return x
 
     def fuse(self):
-        """Fold every Conv's BatchNorm into its convolution (yolo.py:574-585)."""
-        for m in self.model.modules():
-            if isinstance(m, Conv) and hasattr(m, 'bn'):
-                m.conv = fuse_conv_and_bn(m.conv, m.bn)
-                delattr(m, 'bn')
-                m.forward = m.forward_fuse
+        """Fold every Conv's BatchNorm into a biased convolution (eval-mode statistics)."""
+        for mod in self.model.modules():
+            if isinstance(mod, Conv) and hasattr(mod, 'bn'):
+                mod.conv = fuse_conv_and_bn(mod.conv, mod.bn)
+                del mod.bn
         return self
 
     def _apply(self, fn):
-        self = super()._apply(fn)
-        m = self.model[-1]
-        m.stride = fn(m.stride)
-        m.anchors = fn(m.anchors)
-        m.strides = fn(m.strides)
+        super()._apply(fn)
+        head = self.model[-1]
+        for name in ('stride', 'anchors', 'strides'):
+            setattr(head, name, fn(getattr(head, name)))
+        self.stride = head.stride
         return self
 
 

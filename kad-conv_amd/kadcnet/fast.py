@@ -231,7 +231,7 @@ class _GELAN:
         ctot = self.c3 + 2 * self.c4
         cat = x.new_empty(N, H, W, ctot)
         self.cv1(x, cat[..., :self.c3])
-        src = cat[..., self.c3 // 2:self.c3]
+        src = cat[..., (self.c3 + 1) // 2:self.c3]  # the second half as the module splits it (first = ceil(c3 / 2))
         off = self.c3
         for csp, conv in self.stages:
             t = csp(src) if csp is not None else src
@@ -256,7 +256,12 @@ class _AConv:
 class _SPPELAN:
     def __init__(self, m):
         self.cv1 = _ConvOp.from_conv_module(m.cv1)
-        self.k = [sp.m.kernel_size for sp in (m.cv2, m.cv3, m.cv4)]
+        self.k = []
+        for sp in (m.cv2, m.cv3, m.cv4):
+            k, st, pd = (v if isinstance(v, int) else v[0] for v in (sp.m.kernel_size, sp.m.stride, sp.m.padding))
+            if st != 1 or pd != k // 2 or k % 2 != 1:
+                raise NotImplementedError('SPPELAN: the HIP path covers odd max pools with stride 1 and padding k // 2')
+            self.k.append(k)
         self.cv5 = _ConvOp.from_conv_module(m.cv5)
 
     def __call__(self, x, out=None):
@@ -264,8 +269,8 @@ class _SPPELAN:
         c = self.cv1.cout
         cat = x.new_empty(N, H, W, 4 * c)
         self.cv1(x, cat[..., :c])
-        ks = [k if isinstance(k, int) else k[0] for k in self.k]
-        if ks[0] == ks[1] == ks[2] and ks[0] % 2 == 1:  # the three chained pools in one launch
+        ks = self.k
+        if ks[0] == ks[1] == ks[2]:  # the three chained pools in one launch
             _ext.nhwc_resample(cat[..., :c], cat[..., c:], c, _ext.KAD_RS_MAX3, k=ks[0], s=1, p=ks[0] // 2)
         else:
             for i, k in enumerate(ks):
@@ -417,7 +422,9 @@ class KADCNetPlan:
         """From one forward's layer outputs: ({layer i: (Concat layer k, channel offset, channels)},
         {k: buffer shape}) for every Concat whose inputs can all be written straight into its buffer
         (each input layer feeding no other Concat), so that later forwards of the same input shape
-        skip the copies.  Other consumers of such an input read its channel slice of the buffer."""
+        skip the copies.  Other consumers of such an input read its channel slice of the buffer, so
+        every slot must start at a multiple of 8 channels (16-byte pieces); a Concat with another
+        offset keeps its copies."""
         slots, shapes = {}, {}
         for k, (f, op) in enumerate(self.layers):
             if not isinstance(op, _Concat) or not isinstance(f, (list, tuple)):
@@ -427,11 +434,13 @@ class KADCNetPlan:
                     or not all(isinstance(self.layers[j][1], (_ConvOp, _GELAN, _AConv, _SPPELAN, _Upsample))
                                for j in ins)):
                 continue
-            off = 0
+            offs = [0]
             for j in ins:
-                c = ys[j].shape[3]
-                slots[j] = (k, off, c)
-                off += c
+                offs.append(offs[-1] + ys[j].shape[3])
+            if any(o % 8 for o in offs[:-1]):  # consumers of a slice need a 16-byte aligned channel base
+                continue
+            for j, o in zip(ins, offs):
+                slots[j] = (k, o, ys[j].shape[3])
             shapes[k] = tuple(ys[k].shape)
         return slots, shapes
 

@@ -399,13 +399,93 @@ def test_kadcnet_fast_switch_and_graph_replay():
     assert 'forward' not in vars(m)
 
 
+def _kept_anchors(y, max_det=300):
+    """One image's prediction y [4 + nc, A] (float32, CPU) through the steps of the oracle's
+    non_max_suppression at conf_thres 0 and IoU 0.45, keeping track of the anchors: every anchor
+    with a positive best-class probability is a candidate with that class; candidates in
+    descending score order (stable); greedy NMS on class-offset corner boxes; max_det survivors.
+    Returns (kept anchors, their rows (x1, y1, x2, y2, score, class), per-anchor score, class,
+    rank in the score order, corner boxes)."""
+    x = y.t()
+    box = torch.stack((x[:, 0] - x[:, 2] / 2, x[:, 1] - x[:, 3] / 2, x[:, 0] + x[:, 2] / 2, x[:, 1] + x[:, 3] / 2), 1)
+    score, cls = x[:, 4:].max(1)
+    cand = torch.nonzero(score > 0).view(-1)
+    order = cand[torch.from_numpy(np.argsort(-score[cand].numpy(), kind='stable'))]
+    rank = torch.full_like(score, float('inf'), dtype=torch.float64)
+    rank[order] = torch.arange(order.numel(), dtype=torch.float64)
+    shifted = box[order] + cls[order, None].to(box.dtype) * 7680
+    keep = KO.nms(shifted.numpy(), score[order].numpy(), 0.45)[:max_det]
+    anchors = order[torch.as_tensor(keep, dtype=torch.long)]
+    rows = torch.cat((box, score[:, None], cls[:, None].to(box.dtype)), 1)[anchors]
+    return anchors.tolist(), rows, score, cls, rank, box
+
+
+def _iou(b, others):
+    lt = torch.maximum(b[:2], others[:, :2])
+    rb = torch.minimum(b[2:], others[:, 2:])
+    inter = (rb - lt).clamp(min=0).prod(1)
+    area = lambda t: (t[..., 2] - t[..., 0]) * (t[..., 3] - t[..., 1])  # noqa: E731
+    return inter / (area(b) + area(others) - inter)
+
+
+def _unexplained(kh, ko, ph, po, max_det=300):
+    """The detections (anchor, class) kept by one prediction only that no decision differing
+    between the two predictions accounts for.  ph / po = (score, class, rank, box) of the HIP and
+    oracle predictions.  The decisions of the NMS steps are: an anchor's best class; the score
+    order of two same-class anchors whose IoU exceeds the threshold in either prediction; that IoU
+    comparison itself; whether the higher-ranked of such a pair is kept (recursively); and the
+    max_det cut (the anchor ranks at or beyond the first dropped survivor in either prediction)."""
+    (sh, ch, rh, bh), (so, co, ro, bo) = ph, po
+    set_h, set_o = set(kh), set(ko)
+    det_h = {a: c for a, c in zip(kh, ch[kh].tolist())}
+    det_o = {a: c for a, c in zip(ko, co[ko].tolist())}
+    diff = {(a, c) for a, c in det_h.items() if det_o.get(a) != c} | \
+           {(a, c) for a, c in det_o.items() if det_h.get(a) != c}
+    status_differs = {a for a, _ in diff}
+    cut_h = rh[kh[-1]].item() if len(kh) == max_det else float('inf')
+    cut_o = ro[ko[-1]].item() if len(ko) == max_det else float('inf')
+    explained = set()
+    changed = True
+    while changed:
+        changed = False
+        for a, c in diff:
+            if (a, c) in explained:
+                continue
+            ok = ch[a].item() != co[a].item() or rh[a].item() >= cut_h or ro[a].item() >= cut_o
+            if not ok:
+                nb = torch.nonzero((ch == c) | (co == c)).view(-1)
+                nb = nb[nb != a]
+                iou_h, iou_o = _iou(bh[a], bh[nb]), _iou(bo[a], bo[nb])
+                near = (iou_h > 0.45) | (iou_o > 0.45)
+                for b, ih, io in zip(nb[near].tolist(), iou_h[near].tolist(), iou_o[near].tolist()):
+                    above_h, above_o = rh[b].item() < rh[a].item(), ro[b].item() < ro[a].item()
+                    if (above_h or above_o) and ((ih > 0.45) != (io > 0.45) or above_h != above_o
+                                                 or ch[b].item() != co[b].item() or b in status_differs
+                                                 and any(d in explained for d in diff if d[0] == b)):
+                        ok = True
+                        break
+            if ok:
+                explained.add((a, c))
+                changed = True
+    return sorted(diff - explained), len(diff)
+
+
 def test_kadcnet_config5_full_size():
-    """batch 16, 3 x 800 x 800 ~U[0, 1], fp16, fused model.  The
-    batch runs on the HIP plan; images 0 and 15 are checked against the float32
-    CPU oracle (every computation is per image).  NMS (conf_thres 0, the class
-    logits of a random-init head sit near -10) then runs on both y's: the HIP NMS
-    on the HIP y must keep exactly what the oracle NMS keeps on that y, and the top
-    100 detections of the HIP path and of the oracle agree by anchor and class."""
+    """batch 16, 3 x 800 x 800 ~U[0, 1], fp16, fused model.  The batch runs on
+    the HIP plan; images 0 and 15 are checked against the float32 CPU oracle (every computation is
+    per image).
+
+    * Heads and boxes: max |d| <= 1e-2 max |ref| (the head logits reach |18| and the boxes 800 px,
+      where half an fp16 ulp is 7.8e-3 and 0.25: an absolute 1e-2 is below the format's resolution).
+      Class probabilities (values in (0, 1)): max |d| = e <= 1e-2 absolute.
+    * The HIP NMS kernel on the HIP prediction keeps exactly what the oracle NMS keeps on it.
+    * Detections, end to end: the HIP NMS on the HIP prediction against the oracle NMS on the
+      oracle's own prediction, by (anchor, class), at conf_thres 0 (a random-init head's class
+      probabilities sit near 1e-4), IoU 0.45, max_det 300.  A detection kept by one side only must
+      follow from a decision that the two predictions take differently (best class, score order or
+      IoU comparison of an overlapping same-class pair, the status of the suppressor, the max_det
+      cut); each such flip is a comparison whose margin is below the measured error e (scores) or
+      the measured corner error (IoU)."""
     import kadcnet
     dtype = torch.float16
     m, sd = _model(dtype, seed=0, fuse=True)
@@ -424,17 +504,21 @@ def test_kadcnet_config5_full_size():
             r = _rel(a[img:img + 1].double().cpu(), b.double())
             print(f'  head {l}: rel {r:.2e}', flush=True)
             assert r <= 1e-2
-        assert _rel(y[img:img + 1, :4].double().cpu(), yo[:, :4].double()) <= 1e-2
-        # NMS: the HIP kernels against the oracle's NMS on the same (HIP) prediction
+        yh = y[img].float().cpu()
+        assert _rel(yh[:4].double(), yo[0, :4].double()) <= 1e-2
+        e = (yh[4:].double() - yo[0, 4:].double()).abs().max().item()
+        assert e <= 1e-2
+        # the HIP NMS kernels against the oracle's NMS on the same (HIP) prediction
         det = kadcnet.non_max_suppression(y[img:img + 1].float(), conf_thres=0.0, iou_thres=0.45, max_det=300)[0]
-        det_ref = KO.non_max_suppression(y[img:img + 1].float().cpu(), conf_thres=0.0, iou_thres=0.45, max_det=300)[0]
+        det_ref = KO.non_max_suppression(yh[None], conf_thres=0.0, iou_thres=0.45, max_det=300)[0]
         assert det.shape == det_ref.shape and torch.equal(det.cpu(), det_ref), 'HIP NMS differs from the oracle NMS'
-        # end to end: the strongest detections of both paths
-        top = torch.argsort(y[img, 4:].float().amax(0).cpu(), descending=True, stable=True)[:100]
-        top_ref = torch.argsort(yo[0, 4:].amax(0), descending=True, stable=True)[:100]
-        overlap = len(set(top.tolist()) & set(top_ref.tolist()))
-        print(f'  top-100 anchors shared: {overlap}', flush=True)
-        assert overlap >= 90
-        cls = y[img, 4:].float().argmax(0).cpu()[top_ref]
-        cls_ref = yo[0, 4:].argmax(0)[top_ref]
-        assert (cls == cls_ref).float().mean() >= 0.95
+        # end to end, by anchor: the HIP side's anchors reproduce the product's rows
+        kh, rows_h, *ph = _kept_anchors(yh)
+        assert torch.equal(rows_h, det_ref)
+        ko, rows_o, *po = _kept_anchors(yo[0].float())
+        assert torch.equal(rows_o, KO.non_max_suppression(yo.float(), conf_thres=0.0, iou_thres=0.45, max_det=300)[0])
+        bad, ndiff = _unexplained(kh, ko, ph, po)
+        q = (ph[3] - po[3]).abs().max().item()
+        print(f'  detections: {len(kh)} / {len(ko)} kept, {ndiff} differ by anchor or class, '
+              f'{len(bad)} unexplained; e = {e:.2e}, corner error {q:.2e} px', flush=True)
+        assert not bad, f'detections differ beyond a flipped decision: {bad[:5]}'

@@ -61,6 +61,19 @@ def test_dsc_noalloc_matches_dsc_fwd(dt):
         _case(n, c, h, w, dtype, seed=n * 100 + c)
 
 
+@pytest.mark.parametrize('dt', ['f16', 'bf16'])
+def test_dsc_noalloc_narrow_path(dt):
+    """16-bit, Cout <= 64 and at least 384 tile blocks: kad_dsc_fwd_noalloc takes the narrow
+    two-blocks-per-CU kernel, whose fused SE keeps its partials and counters in the same library
+    scratch; two calls in a row, the second smaller."""
+    from kadconv import _ext
+    dtype = {'f16': torch.float16, 'bf16': torch.bfloat16}[dt]
+    for n, c, h, w in [(16, 16, 64, 64), (12, 24, 72, 60)]:
+        assert n * _ext.dcn_tiles(h, w) >= 384
+        print(f'dsc noalloc narrow {dt} n={n} c={c} {h}x{w}', flush=True)
+        _case(n, c, h, w, dtype, seed=n * 10 + c)
+
+
 def test_dsc_noalloc_rejects_oversize():
     """Beyond the scratch limit (N x tiles x Cout > 2^20 partials) the entry point
     returns KAD_EINVAL before any launch."""

@@ -16,8 +16,10 @@
  *    calls are capturable into a HIP graph;
  *  - return 0 on success or a negative KAD_E* code; the message for the last
  *    failure on the calling thread is returned by kad_last_error();
- *  - no mutable global state: calls from different host threads on different
- *    streams do not interfere.
+ *  - no mutable global state, with one exception: kad_dsc_fwd_noalloc keeps its
+ *    scratch in a file-scope device array and a per-device address table (see
+ *    its declaration).  Every other call, from any host thread on any stream,
+ *    touches only the buffers the caller passes, so such calls do not interfere.
  */
 #ifndef KADCONV_HIP_H_
 #define KADCONV_HIP_H_

@@ -424,7 +424,8 @@ def counters_from(trace_csv, fetch_csv, write_csv, sq_csv):
     rows = []
     for k in f:
         name, grid = k
-        if not name.startswith(('_ZN3kad', 'kad::', 'void kad::')) or 'pack_kernel' in name or k not in dur:
+        if not (name.startswith(('_ZN3kad', 'kad::', 'void kad::')) or 'scale_residual' in name) or 'pack_kernel' in name \
+                or k not in dur:
             continue
         us = statistics.median(dur[k])
         rd = statistics.median(f[k]['FETCH_SIZE']) * 1024.0 * sf

@@ -381,6 +381,13 @@ int kad_channel_scale(const void *x, const float *att, void *out, int n, int c, 
  * counterpart; this is the entry used when a caller hands over NCHW tensors. */
 int kad_to_nhwc(const void *x, void *out, int n, int c, int h, int w, int out_cs, int dtype, void *stream);
 
+/* Channels-last [N][H][W] with pixel stride x_cs (>= c; a channel slice of a
+ * wider buffer, or a dense tensor whose C is not a multiple of 8) -> NHWC with
+ * channel stride out_cs (a multiple of 8), channels >= c written 0.  Replaces the two passes (a dense copy, then kad_to_nhwc) that a
+ * channels-last input of C % 8 != 0 needed.  Like kad_to_nhwc it has no
+ * counterpart in the reference, which keeps NCHW. */
+int kad_nhwc_pad(const void *x, int x_cs, void *out, int out_cs, int n, int c, int h, int w, int dtype, void *stream);
+
 #define KAD_MAX_BRANCHES 4
 
 typedef struct kad_merge_args {

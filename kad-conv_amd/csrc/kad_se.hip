@@ -974,6 +974,26 @@ __global__ __launch_bounds__(256) void to_nhwc_v8_kernel(const T* x, T* out, int
   }
 }
 
+// ---- channels-last with pixel stride x_cs -> NHWC with channel stride cs (pad channels 0) ----
+// One thread per output piece of 8 channels of one pixel: the input piece is read as
+// elements (x_cs and c need not be multiples of 8), the output written as one vector (16 bytes for 16-bit data).  Consecutive
+// threads cover consecutive pieces, so both sides are coalesced along the pixel rows.
+template <typename T>
+__global__ __launch_bounds__(256) void nhwc_pad_kernel(const T* x, T* out, int c, int x_cs, int cs, int64_t pixels) {
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  const int pieces = cs >> 3;
+  const int64_t total = pixels * pieces;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t p = i / pieces;
+    const int c0 = (int)(i - p * pieces) * 8;
+    const T* src = x + p * x_cs + c0;
+    v8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = c0 + j < c ? src[j] : from_f32<T>(0.f);
+    *(v8*)(out + p * cs + c0) = o;
+  }
+}
+
 static int grid_for(int64_t total) {
   int64_t b = (total + 255) / 256;
   return (int)(b < 65536 ? (b > 0 ? b : 1) : 65536);
@@ -1485,6 +1505,29 @@ extern "C" int kad_branch_merge(const kad_merge_args* a_in, void* stream) {
     }
   }
   return check_launch("kad_branch_merge");
+}
+
+extern "C" int kad_nhwc_pad(const void* x, int x_cs, void* out, int out_cs, int n, int c, int h, int w, int dtype,
+                            void* stream) {
+  KAD_CHECK_ARG(x && out, "kad_nhwc_pad: null pointer");
+  KAD_CHECK_ARG(n > 0 && c > 0 && h > 0 && w > 0 && x_cs >= c && out_cs >= c && out_cs % 8 == 0,
+                "kad_nhwc_pad: bad shape (n %d, c %d, %dx%d, x_cs %d, out_cs %d: need x_cs, out_cs >= c, out_cs %% 8 == 0)",
+                n, c, h, w, x_cs, out_cs);
+  KAD_CHECK_ARG(dtype == KAD_F16 || dtype == KAD_BF16 || dtype == KAD_F32, "kad_nhwc_pad: unknown dtype %d", dtype);
+  KAD_CHECK_ARG((uintptr_t)out % 16 == 0, "kad_nhwc_pad: out must be 16-byte aligned");
+  const int64_t pixels = (int64_t)n * h * w;
+  hipStream_t st = (hipStream_t)stream;
+  const int grid = grid_for(pixels * (out_cs / 8));
+  if (dtype == KAD_F16)
+    hipLaunchKernelGGL(nhwc_pad_kernel<half_t>, dim3(grid), dim3(256), 0, st, (const half_t*)x, (half_t*)out, c, x_cs,
+                       out_cs, pixels);
+  else if (dtype == KAD_F32)
+    hipLaunchKernelGGL(nhwc_pad_kernel<float>, dim3(grid), dim3(256), 0, st, (const float*)x, (float*)out, c, x_cs,
+                       out_cs, pixels);
+  else
+    hipLaunchKernelGGL(nhwc_pad_kernel<bf16_t>, dim3(grid), dim3(256), 0, st, (const bf16_t*)x, (bf16_t*)out, c, x_cs,
+                       out_cs, pixels);
+  return check_launch("kad_nhwc_pad");
 }
 
 extern "C" int kad_to_nhwc(const void* x, void* out, int n, int c, int h, int w, int out_cs, int dtype,

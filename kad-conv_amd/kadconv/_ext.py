@@ -144,6 +144,7 @@ SIGNATURES = {
     'kad_se_scale': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_channel_scale': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_to_nhwc': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_nhwc_pad': (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_branch_merge': (c_int, [ctypes.POINTER(MergeArgs), c_vp]),
     'kad_conv_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
     'kad_stem_conv_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
@@ -627,6 +628,21 @@ def to_nhwc(x, out):
     N, C, H, W = x.shape
     _check(load().kad_to_nhwc(_ptr(x), _ptr(out), N, C, H, W, out.shape[-1], kad_dtype(x.dtype), _stream()),
            'kad_to_nhwc')
+    return out
+
+
+def nhwc_pad(x, out):
+    """x: an NHWC view [N,H,W,C] with channel stride 1 and pixel stride >= C ->
+    out NHWC [N,H,W,cs] dense, cs % 8 == 0, channels >= C zeroed; one launch."""
+    _need_gpu(x, out)
+    N, H, W, C = x.shape
+    xs = x.stride()
+    if xs[3] != 1 or xs[2] < C or xs[1] != xs[2] * W or xs[0] != xs[1] * H:
+        raise ValueError('nhwc_pad wants channels-last pixels of one stride')
+    if not out.is_contiguous() or tuple(out.shape[:3]) != (N, H, W) or out.dtype != x.dtype:
+        raise ValueError('nhwc_pad: out must be dense [N, H, W, cs] of x\'s dtype')
+    _check(load().kad_nhwc_pad(_ptr(x), xs[2], _ptr(out), out.shape[3], N, C, H, W, kad_dtype(x.dtype), _stream()),
+           'kad_nhwc_pad')
     return out
 
 

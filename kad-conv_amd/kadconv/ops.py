@@ -24,9 +24,13 @@ def _nhwc_view(x):
     if x.is_contiguous(memory_format=torch.channels_last) and C % 8 == 0 and C > 1:
         return x.permute(0, 2, 3, 1), C
     cs = (C + 7) // 8 * 8
-    xc = x.contiguous()
     out = torch.empty(N, H, W, cs, dtype=x.dtype, device=x.device)
-    _ext.to_nhwc(xc, out)
+    v = x.permute(0, 2, 3, 1)
+    vs = v.stride()
+    if (vs[3] == 1 and vs[2] >= C and vs[1] == vs[2] * W and vs[0] == vs[1] * H):
+        _ext.nhwc_pad(v, out)        # channels-last (or a channel slice of one): one padding pass
+    else:
+        _ext.to_nhwc(x.contiguous(), out)
     return out, cs
 
 

@@ -368,6 +368,18 @@ int kad_se_hidden(const float *partial, int tiles, float inv_count, const float 
 int kad_se_scale(const void *x, const float *hidden, const float *w2, const float *b2, float *att, void *out, int n,
                  int c, int h, int w, int hid, int dtype, void *stream);
 
+/* The whole SE block over an NCHW x in two launches, x read from HBM once:
+ *   g = mean_hw(x), hidden = relu(W1 g + b1), att = sigmoid(W2 hidden + b2), out = x * att.
+ * Launch 1: plane means and each 32-channel block's share of W1 g (hpart: n * (C / 32) * 64
+ * floats, caller-owned); launch 2: every block forms hidden from its image's shares, then att of
+ * its channels (also written to att [n][C]) and the scale, its planes re-read from the L2 of the
+ * XCD that read them first.  Fixed-order sums; no state kept between calls.  Needs
+ * kad_se_nchw_fits (C % 32 == 0, hid <= 64, H W >= 8).  The reference's k_gap_partial + k_se_mlp
+ * + k_apply_tiled (acceleration/kadc_fused_sm75.py:1203-1217,1518-1542) for kad_conv.py:105-109. */
+int kad_se_nchw_fits(int n, int c, int h, int w, int hid);
+int kad_se_nchw(const void *x, void *out, const float *w1, const float *b1, const float *w2, const float *b2,
+                float *att, float *hpart, int n, int c, int h, int w, int hid, int dtype, void *stream);
+
 /* out = x * att[n][c] (NCHW, or NHWC with channel stride x_cs).
  * Reference k_apply_tiled (acceleration/kadc_fused_sm75.py:1203-1217). */
 int kad_channel_scale(const void *x, const float *att, void *out, int n, int c, int h, int w, int layout, int x_cs,

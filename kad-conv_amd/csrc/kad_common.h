@@ -52,6 +52,18 @@ __device__ __forceinline__ float sigmoidf_(float v) {
   return d == __builtin_inff() ? 0.0f : q;
 }
 
+// Cross-block exchange inside one kernel (8 XCDs, each with its own L2): a relaxed device-scope
+// atomic load or exchange is performed at the memory-side coherence point, so it neither returns
+// a stale line of the reader's L2 nor leaves the value in the writer's.  rmw_store uses the
+// returning form and consumes the result, so the thread's wait for it covers the store.
+__device__ __forceinline__ float dev_load(const float* p) {
+  return __uint_as_float(__hip_atomic_load((const unsigned*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void rmw_store(float* p, float v) {
+  const unsigned old = __hip_atomic_exchange((unsigned*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("" ::"v"(old));
+}
+
 // Raw buffer access: a load at a byte offset at or past the descriptor's size
 // returns 0 (no fault), so out-of-range pieces need no branch.  Offsets are
 // 32-bit: callers keep the addressed range below 2^31 bytes, which keeps

@@ -605,13 +605,7 @@ __device__ __forceinline__ void offset_conv16(floatx4 (&oacc)[DCN_WM][2], __amdg
 // s + nsl, ...; the slices are then added in order), so the result does not
 // depend on which block came last; then att = sigmoid(W2 relu(W1 g + b1) + b2)
 // with 4 lanes per output and a shuffle reduction.  lds: Cout + hid + THREADS floats.
-__device__ __forceinline__ float dev_load(const float* p) {
-  return __uint_as_float(__hip_atomic_load((const unsigned*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-}
-__device__ __forceinline__ void rmw_store(float* p, float v) {
-  const unsigned old = __hip_atomic_exchange((unsigned*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  asm volatile("" ::"v"(old));  // the returning form: the thread's wait covers it
-}
+// (dev_load / rmw_store: kad_common.h)
 
 template <int THREADS>
 __device__ __forceinline__ void se_tail(const float* __restrict__ partial, const float* __restrict__ w1,

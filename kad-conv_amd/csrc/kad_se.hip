@@ -994,6 +994,182 @@ __global__ __launch_bounds__(256) void nhwc_pad_kernel(const T* x, T* out, int c
   }
 }
 
+// ---- SE over NCHW in two launches (C % 32 == 0, hid <= 64) ---------------------------------
+// Both launches give block b the 32 planes [32 b, 32 b + 32) (channels 32 (b % (C / 32)) .. of one
+// image) and the same grid, so block b runs on the same XCD in both: the second launch re-reads
+// the block's planes from that XCD's L2 (4 MB each: a 20 MB activation is 2.6 MB per XCD).
+//  se_pool_l1: plane means, 16 lanes per plane over the 16-byte pieces that overlap it (a piece
+//    shared with the neighbour plane is read by both, each adding only its own elements), then the
+//    block's share of layer 1, hpart[n][b'][j] = sum over its 32 channels c of W1[j][c] g_c.
+//  se_scale_l2: hidden[n] = relu(b1 + sum over the C / 32 shares) (every block of the image forms
+//    it from the shares, 8 KB for C = 1024: no cross-block exchange inside a launch), att of the
+//    block's 32 channels (16 lanes per channel, shuffle-reduced), then out = x * att, one thread
+//    per piece.
+// Every sum has a fixed order, so the result does not depend on the grid's timing.
+constexpr int SEP_PLANES = 32, SEP_T = 512, SEP_KU = 8, SEP_HID = 64;
+
+// sum of the elements [lo, hi) of an 8-element piece (fp32 accumulation)
+template <typename T> struct PieceSum;
+template <> struct PieceSum<half_t> {
+  typedef half_t t8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ float all(const t8& v, float acc) {
+    const half2_t one = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_fdot2((half2_t){v[2 * k], v[2 * k + 1]}, one, acc, false);
+    return acc;
+  }
+};
+template <> struct PieceSum<bf16_t> {
+  typedef bf16_t t8 __attribute__((ext_vector_type(8)));
+  typedef bf16_t b2 __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ float all(const t8& v, float acc) {
+    const b2 one = {(bf16_t)1.0f, (bf16_t)1.0f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_fdot2_f32_bf16((b2){v[2 * k], v[2 * k + 1]}, one, acc, false);
+    return acc;
+  }
+};
+template <> struct PieceSum<float> {
+  typedef float t8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ float all(const t8& v, float acc) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc += v[k];
+    return acc;
+  }
+};
+template <typename T, typename V>
+__device__ __forceinline__ float piece_sum(const V& v, int lo, int hi, float acc) {
+  if (lo == 0 && hi == 8) return PieceSum<T>::all(v, acc);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc += (k >= lo && k < hi) ? to_f32(v[k]) : 0.f;
+  return acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(SEP_T) void se_pool_l1_kernel(const T* __restrict__ x, const float* __restrict__ w1,
+                                                           float* __restrict__ hpart, int c, int hw, int hid) {
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  __shared__ float s_g[SEP_PLANES];
+  const int tid = threadIdx.x;
+  const int nb = c / SEP_PLANES, b = blockIdx.x, cb = b % nb;
+  // layer-1 weights of this thread (unit u = tid / 8, channels 4 q .. 4 q + 3 of the block), early
+  const int u1 = tid >> 3, q = tid & 7;
+  float wv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wv[i] = u1 < hid ? w1[(int64_t)u1 * c + cb * SEP_PLANES + 4 * q + i] : 0.f;
+  const T* xb = x + (int64_t)b * SEP_PLANES * hw;
+  const int g = tid >> 4, jl = tid & 15;          // plane g of the block, lane jl of its 16
+  const int e_lo = g * hw, e_hi = e_lo + hw;
+  const int f = e_lo >> 3, l = (e_hi - 1) >> 3;   // pieces overlapping the plane
+  float acc = 0.f;
+  for (int p0 = f + jl; p0 <= l; p0 += 16 * SEP_KU) {
+    t8 xv[SEP_KU];
+#pragma unroll
+    for (int k = 0; k < SEP_KU; ++k)
+      if (p0 + 16 * k <= l) xv[k] = *(const t8*)(xb + (int64_t)(p0 + 16 * k) * 8);
+#pragma unroll
+    for (int k = 0; k < SEP_KU; ++k) {
+      const int p = p0 + 16 * k;
+      if (p > l) continue;
+      const int lo = e_lo - 8 * p > 0 ? e_lo - 8 * p : 0, hi = e_hi - 8 * p < 8 ? e_hi - 8 * p : 8;
+      acc = piece_sum<T>(xv[k], lo, hi, acc);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o);
+  if (jl == 0) s_g[g] = acc / (float)hw;
+  __syncthreads();
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a += wv[i] * s_g[4 * q + i];
+  a += __shfl_xor(a, 1);
+  a += __shfl_xor(a, 2);
+  a += __shfl_xor(a, 4);
+  if (q == 0 && u1 < hid) hpart[(int64_t)b * SEP_HID + u1] = a;
+}
+
+template <typename T>
+__global__ __launch_bounds__(SEP_T) void se_scale_l2_kernel(const T* __restrict__ x, const float* __restrict__ hpart,
+                                                            const float* __restrict__ b1, const float* __restrict__ w2,
+                                                            const float* __restrict__ b2, float* __restrict__ att,
+                                                            T* __restrict__ out, int c, int hw, int hid) {
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  __shared__ float s_att[SEP_PLANES];
+  __shared__ float s_h[8][SEP_HID];
+  const int tid = threadIdx.x;
+  const int nb = c / SEP_PLANES, b = blockIdx.x, n = b / nb, c0 = (b - n * nb) * SEP_PLANES;
+  const int npc = SEP_PLANES * hw / 8;  // pieces of the block
+  const T* xb = x + (int64_t)b * SEP_PLANES * hw;
+  T* ob = out + (int64_t)b * SEP_PLANES * hw;
+  t8 xv[SEP_KU];
+#pragma unroll
+  for (int k = 0; k < SEP_KU; ++k)
+    if (tid + SEP_T * k < npc) xv[k] = *(const t8*)(xb + (int64_t)(tid + SEP_T * k) * 8);
+  // hidden[n]: unit u = tid % 64, slice sl = tid / 64 adds shares sl, sl + 8, ... (loads first)
+  {
+    const int u = tid & 63, sl = tid >> 6;
+    const float* hp = hpart + (int64_t)n * nb * SEP_HID + u;
+    float h = 0.f;
+    for (int k0 = sl; k0 < nb; k0 += 8 * 8) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (u < hid && k0 + 8 * i < nb) ? hp[(int64_t)(k0 + 8 * i) * SEP_HID] : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) h += v[i];
+    }
+    s_h[sl][u] = h;
+  }
+  // this thread's W2 slice: channel c0 + tid / 16, hidden units 4 (tid % 16) .. + 3
+  const int cl = tid >> 4, q = tid & 15;
+  float wv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) wv[i] = 4 * q + i < hid ? w2[(int64_t)(c0 + cl) * hid + 4 * q + i] : 0.f;
+  __syncthreads();
+  if (tid < SEP_HID) {
+    float t = s_h[0][tid];
+#pragma unroll
+    for (int k = 1; k < 8; ++k) t += s_h[k][tid];
+    s_h[0][tid] = tid < hid ? fmaxf(t + (b1 ? b1[tid] : 0.f), 0.f) : 0.f;
+  }
+  __syncthreads();
+  {
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a += wv[i] * s_h[0][4 * q + i];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) a += __shfl_xor(a, o);
+    if (q == 0) {
+      const float v = sigmoidf_(a + (b2 ? b2[c0 + cl] : 0.f));
+      s_att[cl] = v;
+      att[(int64_t)n * c + c0 + cl] = v;
+    }
+  }
+  __syncthreads();
+  const float inv_hw = 1.f / (float)hw;
+  for (int v0 = tid; v0 < npc; v0 += SEP_T * SEP_KU) {
+    if (v0 != tid) {
+#pragma unroll
+      for (int k = 0; k < SEP_KU; ++k)
+        if (v0 + SEP_T * k < npc) xv[k] = *(const t8*)(xb + (int64_t)(v0 + SEP_T * k) * 8);
+    }
+#pragma unroll
+    for (int k = 0; k < SEP_KU; ++k) {
+      const int v = v0 + SEP_T * k;
+      if (v >= npc) continue;
+      const int e0 = v * 8;
+      int p0 = (int)((float)e0 * inv_hw);  // e0 < 2^24: within one of the true quotient
+      p0 -= p0 * hw > e0;
+      p0 += (p0 + 1) * hw <= e0;
+      const int nfirst = (p0 + 1) * hw - e0;
+      const float s0 = s_att[p0], s1 = nfirst < 8 ? s_att[p0 + 1] : s0;
+      t8 o;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) o[kk] = from_f32<T>(to_f32(xv[k][kk]) * (kk < nfirst ? s0 : s1));
+      *(t8*)(ob + (int64_t)e0) = o;
+    }
+  }
+}
+
 static int grid_for(int64_t total) {
   int64_t b = (total + 255) / 256;
   return (int)(b < 65536 ? (b > 0 ? b : 1) : 65536);
@@ -1261,6 +1437,42 @@ extern "C" int kad_se_hidden(const float* partial, int tiles, float inv_count, c
   hipLaunchKernelGGL(se_mlp_l1_kernel, dim3(ceil_div(hid, 4), ceil_div(n, 4)), dim3(256), 0, (hipStream_t)stream,
                      partial, tiles, inv_count, w1, b1, hidden, n, c, hid);
   return check_launch("kad_se_hidden");
+}
+
+extern "C" int kad_se_nchw_fits(int n, int c, int h, int w, int hid) {
+  return n > 0 && c > 0 && c % SEP_PLANES == 0 && hid > 0 && hid <= SEP_HID && h > 0 && w > 0 && h * w >= 8 &&
+         (int64_t)h * w * SEP_PLANES < (1 << 24) && (int64_t)n * c * h * w < (1ll << 31);
+}
+
+extern "C" int kad_se_nchw(const void* x, void* out, const float* w1, const float* b1, const float* w2,
+                           const float* b2, float* att, float* hpart, int n, int c, int h, int w, int hid, int dtype,
+                           void* stream) {
+  KAD_CHECK_ARG(x && out && w1 && w2 && att && hpart, "kad_se_nchw: null pointer");
+  KAD_CHECK_ARG(kad_se_nchw_fits(n, c, h, w, hid),
+                "kad_se_nchw: needs C %% 32 == 0, hidden <= 64, H W >= 8 (n %d, c %d, %dx%d, hid %d)", n, c, h, w, hid);
+  const int vb = 8 * dtype_size(dtype);
+  KAD_CHECK_ARG((uintptr_t)x % vb == 0 && (uintptr_t)out % vb == 0, "kad_se_nchw: x / out not %d-byte aligned", vb);
+  const int hw = h * w, grid = n * (c / SEP_PLANES);
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case KAD_F32:
+      hipLaunchKernelGGL(se_pool_l1_kernel<float>, dim3(grid), dim3(SEP_T), 0, st, (const float*)x, w1, hpart, c, hw, hid);
+      hipLaunchKernelGGL(se_scale_l2_kernel<float>, dim3(grid), dim3(SEP_T), 0, st, (const float*)x, hpart, b1, w2, b2, att,
+                         (float*)out, c, hw, hid);
+      break;
+    case KAD_F16:
+      hipLaunchKernelGGL(se_pool_l1_kernel<half_t>, dim3(grid), dim3(SEP_T), 0, st, (const half_t*)x, w1, hpart, c, hw, hid);
+      hipLaunchKernelGGL(se_scale_l2_kernel<half_t>, dim3(grid), dim3(SEP_T), 0, st, (const half_t*)x, hpart, b1, w2, b2,
+                         att, (half_t*)out, c, hw, hid);
+      break;
+    case KAD_BF16:
+      hipLaunchKernelGGL(se_pool_l1_kernel<bf16_t>, dim3(grid), dim3(SEP_T), 0, st, (const bf16_t*)x, w1, hpart, c, hw, hid);
+      hipLaunchKernelGGL(se_scale_l2_kernel<bf16_t>, dim3(grid), dim3(SEP_T), 0, st, (const bf16_t*)x, hpart, b1, w2, b2,
+                         att, (bf16_t*)out, c, hw, hid);
+      break;
+    default: return fail(KAD_EINVAL, "kad_se_nchw: unknown dtype %d", dtype);
+  }
+  return check_launch("kad_se_nchw");
 }
 
 extern "C" int kad_se_scale(const void* x, const float* hidden, const float* w2, const float* b2, float* att,

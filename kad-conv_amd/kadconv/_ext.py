@@ -144,6 +144,9 @@ SIGNATURES = {
     'kad_se_scale': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_channel_scale': (c_int, [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_to_nhwc': (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
+    'kad_se_nchw_fits': (c_int, [c_int, c_int, c_int, c_int, c_int]),
+    'kad_se_nchw': (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int,
+                            c_vp]),
     'kad_nhwc_pad': (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_vp]),
     'kad_branch_merge': (c_int, [ctypes.POINTER(MergeArgs), c_vp]),
     'kad_conv_fwd': (c_int, [ctypes.POINTER(DcnArgs), c_vp]),
@@ -598,6 +601,26 @@ def se_hidden(partial, tiles, inv_count, w1, b1, hidden, n, c, hid):
     assert hidden.dtype == torch.float32 and hidden.is_contiguous() and hidden.numel() >= n * hid
     _check(load().kad_se_hidden(_ptr(partial), tiles, inv_count, _ptr(w1), _ptr(b1), _ptr(hidden), n, c, hid,
                                 _stream()), 'kad_se_hidden')
+
+
+def se_nchw_fits(n, c, h, w, hid):
+    return bool(load().kad_se_nchw_fits(n, c, h, w, hid))
+
+
+def se_nchw(x, w1, b1, w2, b2, att, out):
+    """kad_se_nchw: the SE block on a dense NCHW x in two launches; att [N, C] fp32 written too."""
+    _need_gpu(x, w1, w2, att, out)
+    N, C, H, W = x.shape
+    hid = w1.shape[0]
+    if not (x.is_contiguous() and out.is_contiguous() and out.dtype == x.dtype and out.shape == x.shape):
+        raise ValueError('se_nchw wants dense NCHW x and out of one shape and dtype')
+    for t in (w1, w2, att) + ((b1,) if b1 is not None else ()) + ((b2,) if b2 is not None else ()):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise TypeError('se_nchw: weights, biases and att are dense float32')
+    hpart = torch.empty(N * (C // 32) * 64, dtype=torch.float32, device=x.device)
+    _check(load().kad_se_nchw(_ptr(x), _ptr(out), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2), _ptr(att), _ptr(hpart), N, C,
+                              H, W, hid, kad_dtype(x.dtype), _stream()), 'kad_se_nchw')
+    return out
 
 
 def se_scale(x, hidden, w2, b2, att, out, hid):

@@ -176,6 +176,10 @@ def squeeze_excitation(x, w1, b1, w2, b2):
     nhwc = x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
     layout = _ext.KAD_NHWC if nhwc else _ext.KAD_NCHW
     xv = x.permute(0, 2, 3, 1) if nhwc else x.contiguous()
+    if not nhwc and _ext.se_nchw_fits(N, C, H, W, hid) and x.dtype in (torch.float16, torch.bfloat16, torch.float32):
+        att = torch.empty(N, C, dtype=torch.float32, device=x.device)
+        return _ext.se_nchw(xv, f32(w1), None if b1 is None else f32(b1), f32(w2), None if b2 is None else f32(b2),
+                            att, torch.empty_like(xv))
     tiles = _ext.se_pool_tiles(H, W, layout)
     partial = torch.empty(N, tiles, C, dtype=torch.float32, device=x.device)
     _ext.se_pool(xv, C, layout, partial)

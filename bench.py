@@ -284,6 +284,40 @@ def config1(steps, warmup, cpu=True):
     return out
 
 
+def kadcnet_flops(hw=800):
+    """Multiply-add FLOPs (2 per MAC) of one KAD-CNet-S image at hw x hw, from forward hooks on
+    the fused model's plain CPU forward of one hw x hw image (about 2 s): every Conv2d (groups
+    honoured; the LCSA strip convs at full resolution, as the kernels form them), every Linear,
+    and each DSC's deformable 3 x 3 (2 * 9 * Cin per output value).  Element-wise work
+    (activations, pooling, resize, merges, decode) is not counted."""
+    import kadcnet
+    import kadconv
+    model = kadcnet.build_kadcnet_s(seed=0).fuse().eval()
+    tot = [0]
+
+    def conv(m, i, o):
+        tot[0] += 2 * (m.in_channels // m.groups) * m.kernel_size[0] * m.kernel_size[1] * o.numel()
+
+    def lin(m, i, o):
+        tot[0] += 2 * m.in_features * o.numel()
+
+    def dsc(m, i, o):
+        tot[0] += 2 * 9 * m.weight.shape[1] * o.numel()
+    hooks = []
+    for mod in model.modules():
+        if isinstance(mod, torch.nn.Conv2d):
+            hooks.append(mod.register_forward_hook(conv))
+        elif isinstance(mod, torch.nn.Linear):
+            hooks.append(mod.register_forward_hook(lin))
+        elif isinstance(mod, kadconv.DSC):
+            hooks.append(mod.register_forward_hook(dsc))
+    with torch.no_grad():
+        model(torch.zeros(1, 3, hw, hw))
+    for h in hooks:
+        h.remove()
+    return tot[0]
+
+
 def kadcnet_s(iterations, warmup, cpu=True, batch=16, hw=800):
     """the whole KAD-CNet-S forward (fused model, random init from
     seed 0, kadcnet.build_kadcnet_s), batch 16, 3 x 800 x 800 ~U[0, 1], fp16,
@@ -301,6 +335,12 @@ def kadcnet_s(iterations, warmup, cpu=True, batch=16, hw=800):
     out = {'img_per_s': round(batch / (us * 1e-6), 1), 'ms_per_batch': round(us / 1e3, 3),
            'trials_ms': [round(t / 1e3, 3) for t in trials], 'batch': batch, 'hw': [hw, hw], 'dtype': 'f16',
            'iterations': iterations, 'warmup': warmup}
+    fl = kadcnet_flops(hw)
+    out['gflop_per_img'] = round(fl / 1e9, 2)
+    out['tflop_per_s'] = round(fl * batch / (us * 1e-6) / 1e12, 1)
+    out['mfma_frac'] = round(fl * batch / (us * 1e-6) / PEAK_MFMA_F16, 4)
+    out['flops_note'] = ('2 x MACs of every convolution, Linear and deformable 3 x 3 (kadcnet_flops), per image; '
+                         'mfma_frac = achieved FLOP/s over the 2516.6 TFLOP/s dense fp16 peak')
     if cpu:
         from oracle import kadcnet_oracle as KO
         sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
@@ -365,6 +405,87 @@ def counters_probe():
             b.copy_(a)
         torch.cuda.synchronize()
     print(json.dumps({'probe': 'done', 'copy_bytes': PROBE_COPY_BYTES}), flush=True)
+
+
+def counters_probe_net():
+    """A short program for the KAD-CNet-S counter table: two eager forwards of config 5 (fused
+    model, bs16, 3 x 800 x 800 fp16; the first builds the plan), then the 64 MiB copy."""
+    import kadcnet
+    m = kadcnet.build_kadcnet_s(seed=0).fuse().to('cuda', torch.float16).eval()
+    kadcnet.enable_fast_inference(m)
+    x = torch.rand(16, 3, 800, 800, generator=torch.Generator().manual_seed(0)).to('cuda', torch.float16)
+    with torch.no_grad():
+        for _ in range(3):
+            m(x)
+            torch.cuda.synchronize()
+            torch.cuda._sleep(1000)  # a spin kernel between forwards: the summary splits the dispatches there
+            torch.cuda.synchronize()
+        a = torch.empty(PROBE_COPY_BYTES, dtype=torch.uint8, device='cuda')
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+    print(json.dumps({'probe': 'done', 'copy_bytes': PROBE_COPY_BYTES, 'forwards': 3}), flush=True)
+
+
+def counters_net_from(trace_csv, fetch_csv, write_csv, sq_csv, forwards=3, top=12):
+    """Per-kernel table of the KAD-CNet-S forward from counters_probe_net(): each kernel's
+    dispatches of forwards 2 .. `forwards` (the first builds the plan) summed and divided by their
+    number (us, MB read / written per forward); MFMA busy over the kernel's own cycles (sum of
+    SQ_VALU_MFMA_BUSY_CYCLES over the sum of GRBM_GUI_ACTIVE / 8 x 1024 SIMDs)."""
+    import collections
+    import csv
+
+    def rows_of(path, counter=None):
+        d = collections.defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            if counter is None or r['Counter_Name'] == counter:
+                d[int(r['Dispatch_Id'])].append(r)
+        return [d[k] for k in sorted(d)]
+
+    def tail(disp):  # dispatches of forwards 2 .. forwards: between the first and the last spin kernel
+        marks = [i for i, rs in enumerate(disp) if 'spin_kernel' in rs[0]['Kernel_Name']]
+        return [rs for rs in disp[marks[0] + 1:marks[-1]] if 'spin_kernel' not in rs[0]['Kernel_Name']]
+    tr = rows_of(trace_csv)
+    f, w, sq = rows_of(fetch_csv, 'FETCH_SIZE'), rows_of(write_csv, 'WRITE_SIZE'), rows_of(sq_csv)
+    cf = [float(rs[0]['Counter_Value']) for rs in f if 'copyBuffer' in rs[0]['Kernel_Name']][-3:]
+    cw = [float(rs[0]['Counter_Value']) for rs in w if 'copyBuffer' in rs[0]['Kernel_Name']][-3:]
+    sf = PROBE_COPY_BYTES / (sorted(cf)[1] * 1024.0)   # the three 64 MiB copies at the end
+    sw = PROBE_COPY_BYTES / (sorted(cw)[1] * 1024.0)
+    nf = forwards - 1
+    agg = collections.defaultdict(lambda: [0, 0.0, 0.0, 0.0, 0.0, 0.0])
+    for rs in tail(tr):
+        r = rs[0]
+        a = agg[r['Kernel_Name']]
+        a[0] += 1
+        a[1] += (int(r['End_Timestamp']) - int(r['Start_Timestamp'])) / 1e3
+    for rs in tail(f):
+        agg[rs[0]['Kernel_Name']][2] += float(rs[0]['Counter_Value']) * 1024.0 * sf
+    for rs in tail(w):
+        agg[rs[0]['Kernel_Name']][3] += float(rs[0]['Counter_Value']) * 1024.0 * sw
+    for rs in tail(sq):
+        v = {r['Counter_Name']: float(r['Counter_Value']) for r in rs}
+        a = agg[rs[0]['Kernel_Name']]
+        a[4] += v.get('SQ_VALU_MFMA_BUSY_CYCLES', 0.0)
+        a[5] += v.get('GRBM_GUI_ACTIVE', 0.0) / 8.0 * 1024.0
+    tot_us = sum(a[1] for a in agg.values()) / nf
+    tot_rd = sum(a[2] for a in agg.values()) / nf
+    tot_wr = sum(a[3] for a in agg.values()) / nf
+    lines = ['| kernel | launches / forward | us / forward | share | read MB | write MB | GB/s | MFMA busy |',
+             '|---|---|---|---|---|---|---|---|']
+    for name, a in sorted(agg.items(), key=lambda kv: -kv[1][1])[:top]:
+        us, rd, wr = a[1] / nf, a[2] / nf / 1e6, a[3] / nf / 1e6
+        short = name if len(name) < 70 else name[:67] + '...'
+        busy = a[4] / a[5] if a[5] else float('nan')
+        lines.append(f'| `{short}` | {a[0] / nf:.0f} | {us:.1f} | {100 * us / tot_us:.1f}% | {rd:.1f} | {wr:.1f} | '
+                     f'{(rd + wr) * 1e6 / (us * 1e-6) / 1e9:.0f} | {100 * busy:.1f}% |')
+    tot_mf = sum(a[4] for a in agg.values())
+    tot_cy = sum(a[5] for a in agg.values())
+    lines.append(f'| all {len(agg)} kernels | {sum(a[0] for a in agg.values()) / nf:.0f} | {tot_us:.1f} | 100% | '
+                 f'{tot_rd / 1e6:.1f} | {tot_wr / 1e6:.1f} | {(tot_rd + tot_wr) / (tot_us * 1e-6) / 1e9:.0f} | '
+                 f'{100 * tot_mf / tot_cy:.1f}% |')
+    print('\n'.join(lines))
+    print(json.dumps({'fetch_scale': sf, 'write_scale': sw, 'forwards_counted': nf}))
 
 
 def traffic_from(fetch_csv, write_csv):
@@ -500,6 +621,10 @@ def main():
                     help='short program for the per-kernel counter table (every forward stage and per-op workload)')
     ap.add_argument('--counters-from', nargs=4, metavar=('TRACE_CSV', 'FETCH_CSV', 'WRITE_CSV', 'SQ_CSV'),
                     help='print the per-kernel counter table from a kernel trace and three --pmc CSVs')
+    ap.add_argument('--counters-probe-net', action='store_true',
+                    help='short program for the KAD-CNet-S counter table (three eager config-5 forwards)')
+    ap.add_argument('--counters-net-from', nargs=4, metavar=('TRACE_CSV', 'FETCH_CSV', 'WRITE_CSV', 'SQ_CSV'),
+                    help='print the KAD-CNet-S per-kernel table from a kernel trace and three --pmc CSVs')
     ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_CSV', 'WRITE_CSV'),
                     help='compute profiles/dsc0_traffic.json from the two --pmc counter CSVs')
     ap.add_argument('--no-kadcnet', action='store_true', help='skip the KAD-CNet-S (config 5) throughput')
@@ -517,6 +642,12 @@ def main():
         return
     if args.counters_from:
         counters_from(*args.counters_from)
+        return
+    if args.counters_net_from:
+        counters_net_from(*args.counters_net_from)
+        return
+    if args.counters_probe_net:
+        counters_probe_net()
         return
     if args.counters_probe:
         counters_probe()

@@ -102,23 +102,39 @@ __global__ __launch_bounds__(KD_THREADS) void kaddown_prep_kernel(const T* __res
     __syncthreads();
   }
   // ---- bilinear resize of p4 (and p8) to Ho x Wo --------------------------------------------------------
+  // A wave walks output rows (its lanes along the row's columns), so a row's source rows and weight
+  // are wave-uniform; each lane's source columns and weights are computed once per column.  Same
+  // formulas and order of operations as per-pixel src_index.
   const float sy4 = (float)H4 / (float)Ho, sx4 = (float)W4 / (float)Wo;
   const float sy8 = (float)H8 / (float)Ho, sx8 = (float)W8 / (float)Wo;
-  for (int i = tid; i < P; i += KD_THREADS) {
-    const int y = i / Wo, xo = i - y * Wo;
-    int y0, y1, x0, x1;
-    float ly, lx;
-    src_index(y, H4, Ho, sy4, y0, y1, ly);
-    src_index(xo, W4, Wo, sx4, x0, x1, lx);
-    float v = (1.f - ly) * ((1.f - lx) * p4[y0 * W4 + x0] + lx * p4[y0 * W4 + x1]) +
-              ly * ((1.f - lx) * p4[y1 * W4 + x0] + lx * p4[y1 * W4 + x1]);
-    ub[(int64_t)C * P + i] = from_f32<T>(v);
-    if (nb > 2) {
-      src_index(y, H8, Ho, sy8, y0, y1, ly);
-      src_index(xo, W8, Wo, sx8, x0, x1, lx);
-      v = (1.f - ly) * ((1.f - lx) * p8[y0 * W8 + x0] + lx * p8[y0 * W8 + x1]) +
-          ly * ((1.f - lx) * p8[y1 * W8 + x0] + lx * p8[y1 * W8 + x1]);
-      ub[(int64_t)2 * C * P + i] = from_f32<T>(v);
+  const int lane = tid & 63, wave = tid >> 6;
+  for (int x0c = 0; x0c < Wo; x0c += 64) {
+    const int xo = x0c + lane;
+    const bool col_ok = xo < Wo;
+    int ax0, ax1, bx0 = 0, bx1 = 0;
+    float alx, blx = 0.f;
+    src_index(col_ok ? xo : 0, W4, Wo, sx4, ax0, ax1, alx);
+    if (nb > 2) src_index(col_ok ? xo : 0, W8, Wo, sx8, bx0, bx1, blx);
+    for (int y = wave; y < Ho; y += KD_THREADS / 64) {
+      int y0, y1;
+      float ly;
+      src_index(y, H4, Ho, sy4, y0, y1, ly);
+      const float* r0 = p4 + y0 * W4;
+      const float* r1 = p4 + y1 * W4;
+      const float v4 = (1.f - ly) * ((1.f - alx) * r0[ax0] + alx * r0[ax1]) +
+                       ly * ((1.f - alx) * r1[ax0] + alx * r1[ax1]);
+      float v8 = 0.f;
+      if (nb > 2) {
+        src_index(y, H8, Ho, sy8, y0, y1, ly);
+        const float* s0 = p8 + y0 * W8;
+        const float* s1 = p8 + y1 * W8;
+        v8 = (1.f - ly) * ((1.f - blx) * s0[bx0] + blx * s0[bx1]) + ly * ((1.f - blx) * s1[bx0] + blx * s1[bx1]);
+      }
+      if (col_ok) {
+        const int i = y * Wo + xo;
+        ub[(int64_t)C * P + i] = from_f32<T>(v4);
+        if (nb > 2) ub[(int64_t)2 * C * P + i] = from_f32<T>(v8);
+      }
     }
   }
 }

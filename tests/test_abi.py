@@ -39,3 +39,19 @@ def test_pure_host_entry_points():
     # argument validation happens before any device work
     assert lib.kad_dcn_fwd(None, None) < 0
     assert b'null' in lib.kad_last_error()
+
+
+def test_se_nchw_fits_rule():
+    """kad_se_nchw_fits: the two-launch NCHW SE takes C % 32 == 0, 1 <= hidden <= 64 and planes of
+    at least 8 pixels (a 16-byte piece meets at most two planes); other shapes keep the
+    pool / MLP / scale launches.  kad_se_nchw itself rejects a shape that does not fit."""
+    from kadconv import _ext
+    lib = _ext.load()
+    assert lib.kad_se_nchw_fits(16, 1024, 25, 25, 64) == 1
+    assert lib.kad_se_nchw_fits(1, 32, 1, 8, 1) == 1
+    assert lib.kad_se_nchw_fits(2, 48, 7, 9, 3) == 0     # C % 32 != 0
+    assert lib.kad_se_nchw_fits(1, 32, 1, 7, 4) == 0     # 7-pixel planes
+    assert lib.kad_se_nchw_fits(1, 64, 8, 8, 65) == 0    # hidden > 64
+    assert lib.kad_se_nchw_fits(0, 64, 8, 8, 4) == 0
+    assert lib.kad_se_nchw(None, None, None, None, None, None, None, None, 1, 64, 8, 8, 4, _ext.KAD_F16, None) < 0
+    assert b'null' in lib.kad_last_error()

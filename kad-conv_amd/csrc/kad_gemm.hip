@@ -205,21 +205,30 @@ __global__ __launch_bounds__(GM_THREADS) void gemm1x1_kernel(kad_gemm_args a, in
 // 4 g + i at pixel 8 c + j, so every lane ends with eight consecutive pixels per
 // output channel: one 16-byte store (two 8-byte stores when P % 8 != 0).
 // Work items are ordered so the channel blocks of one pixel tile run back to
-// back on the same XCD (shared L2).
-constexpr int GN_PX = 128;              // pixels per tile
-constexpr int GN_WCO = 64;              // output channels per wave
-constexpr int GN_XB = 32 * GN_PX * 2;   // input tile bytes per stage
+// back on the same XCD (shared L2).  The 64-pixel tile (PXT below) is the same
+// scheme with runs of 4 pixels: four fragments, 8-byte LDS reads and stores.
+constexpr int GN_WCO = 64;  // output channels per wave
 
-template <typename T> struct Raw16 { typedef half8_t type; };
-template <> struct Raw16<bf16_t> { typedef bf16x8_t type; };
+template <typename T, int JP> struct RawRun;  // JP consecutive 16-bit pixels of one channel row
+template <> struct RawRun<half_t, 8> { typedef half8_t type; };
+template <> struct RawRun<bf16_t, 8> { typedef bf16x8_t type; };
+template <> struct RawRun<half_t, 4> { typedef half_t type __attribute__((ext_vector_type(4))); };
+template <> struct RawRun<bf16_t, 4> { typedef bf16_t type __attribute__((ext_vector_type(4))); };
 
+// PXT = 128: lane runs of 8 pixels, 4 x 8 accumulator tiles per wave, two blocks per CU.
+// PXT = 64: lane runs of 4 pixels (MFMA column c of pixel fragment j is pixel 4 c + j), 4 x 4
+// accumulator tiles per wave, three blocks per CU: half the work per wave, so a launch's last
+// round of blocks is shorter and small launches fill more of the chip.
+template <int PXT> constexpr int gn_min_blocks() { return PXT == 128 ? 2 : 3; }
 
-template <typename T, bool V16, int NW>
-__global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_args a, int P, int tiles_px,
-                                                                    int co_blocks, int total, int cin_pad) {
+template <typename T, bool V16, int NW, int PXT>
+__global__ __launch_bounds__(64 * NW, (8 / NW) * gn_min_blocks<PXT>() / 2) void gemm_nchw_kernel(
+    kad_gemm_args a, int P, int tiles_px, int co_blocks, int total, int cin_pad) {
+  static_assert(PXT == 128 || PXT == 64, "pixel tile");
+  constexpr int JP = PXT / 16;  // pixels per lane run = pixel fragments per wave
   typedef typename GemmOps<T>::frag frag;
-  typedef typename Raw16<T>::type raw_t;
-  constexpr int STAGE = GN_XB;
+  typedef typename RawRun<T, JP>::type raw_t;
+  constexpr int STAGE = 32 * PXT * 2;  // input tile bytes per stage
   // one object per stage: the compiler tracks the loads into each separately
   __shared__ __align__(16) char st0[STAGE];
   __shared__ __align__(16) char st1[STAGE];
@@ -228,7 +237,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_arg
   const int wi = (bid & 7) * (int)(gridDim.x >> 3) + (bid >> 3);  // contiguous band of work per XCD
   if (wi >= total) return;  // whole block, before any barrier
   const int cb = wi % co_blocks, t2 = wi / co_blocks;
-  const int n = t2 / tiles_px, p0 = (t2 - n * tiles_px) * GN_PX;
+  const int n = t2 / tiles_px, p0 = (t2 - n * tiles_px) * PXT;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, g = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar offsets below)
   const int co_w = (cb * NW + wave) * GN_WCO;
@@ -240,13 +249,16 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_arg
   const __amdgpu_buffer_rsrc_t rw =
       make_rsrc((const T*)a.wpack + (int64_t)cout_pk * cin_pad, (uint32_t)((int64_t)cout_pk * cin_pad * 2));
 
-  // Input pieces: wave w stages rows RPW w .. + RPW; its load q covers rows
-  // RPW w + RQ q + lr (lr = lane / 16 for 16-byte pieces, else 0) at pixels
-  // p0 + lpx ..; the row base goes in the wave-uniform soffset, the lane part
-  // (pixels, lr rows) in voffset, which is out of range for pixels past the
-  // image row: such lanes read zeros and no load reaches past the tensor.
-  constexpr int RPW = 32 / NW, RQ = V16 ? 4 : 1, XQ = RPW / RQ;
-  const int lr = V16 ? lane >> 4 : 0, lpx = V16 ? 8 * (lane & 15) : 2 * lane;
+  // Input pieces (PB = 16 bytes when P % 8 == 0, else 4): a tile row of PXT pixels is
+  // LPR lanes of one load, so one load covers RQ = 64 / LPR rows; wave w stages rows
+  // RPW w .. + RPW, its load q rows RPW w + RQ q + lr (lr = lane / LPR) at pixels
+  // p0 + lpx ..  The row base goes in the wave-uniform soffset, the lane part (pixels,
+  // lr rows) in voffset, which is out of range for pixels past the image row or rows
+  // past Cin: such lanes read zeros and no load reaches past the tensor.
+  constexpr int PB = V16 ? 16 : 4, LPR = PXT * 2 / PB, RQ = 64 / LPR;
+  constexpr int RPW = 32 / NW, XQ = RPW / RQ;
+  static_assert(XQ >= 1 && RPW % RQ == 0, "input pieces");
+  const int lr = lane / LPR, lpx = (PB / 2) * (lane % LPR);
   const uint32_t prow = (uint32_t)P * 2u;  // bytes per channel row
   const uint32_t xlane = p0 + lpx < P ? (uint32_t)lr * prow + (uint32_t)(p0 + lpx) * 2u : KAD_OOB;
   const int64_t xrow0 = (int64_t)n * a.cin + RPW * wave;  // first row of this wave's pieces (step 0)
@@ -259,25 +271,29 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_arg
   constexpr int L = XQ + 4;  // loads per wave per step
   // Loads of step kk: input into stage st, weights into w; a step past the last
   // one (or a row past Cin) reads zeros, so every path issues the same loads.
-  // Rows past Cin (or steps past the last) get an out-of-range voffset; soffset
-  // stays the uniform row base (< 2^31, so the sum cannot wrap into range).
+  // soffset stays the uniform row base (< 2^31, so the sum with KAD_OOB cannot
+  // wrap into range).
   auto issue = [&](int kk, char* st, frag (&w)[4]) {
-    if constexpr (V16) {
-#pragma unroll
-      for (int q = 0; q < XQ; ++q) {
-        const bool ok = kk < nk && kk * 32 + RPW * wave + RQ * q + lr < a.cin;
-        dma16(rx, st + (RPW * wave + RQ * q) * GN_PX * 2, ok ? xlane : KAD_OOB,
-              (uint32_t)((xrow0 + kk * 32 + RQ * q) * P * 2));
-      }
-    } else {  // rows are wave-uniform: a short rolled loop keeps the offsets in scalars
+    if constexpr (RQ == 1) {  // one row per load, rows wave-uniform: a short rolled loop keeps the offsets in scalars
       const int rows = kk < nk ? min(a.cin - (kk * 32 + RPW * wave), RPW) : 0;  // valid rows of this wave
       uint32_t soff = (uint32_t)((xrow0 + kk * 32) * P * 2);
-      char* dst = st + RPW * wave * GN_PX * 2;
+      char* dst = st + RPW * wave * PXT * 2;
 #pragma unroll 1
       for (int q = 0; q < XQ; ++q) {
         dma4(rx, dst, q < rows ? xlane : KAD_OOB, soff);
         soff += prow;
-        dst += GN_PX * 2;
+        dst += PXT * 2;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < XQ; ++q) {
+        const bool ok = kk < nk && kk * 32 + RPW * wave + RQ * q + lr < a.cin;
+        char* dst = st + (RPW * wave + RQ * q) * PXT * 2;
+        const uint32_t soff = (uint32_t)((xrow0 + kk * 32 + RQ * q) * P * 2);
+        if constexpr (V16)
+          dma16(rx, dst, ok ? xlane : KAD_OOB, soff);
+        else
+          dma4(rx, dst, ok ? xlane : KAD_OOB, soff);
       }
     }
 #pragma unroll
@@ -287,11 +303,11 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_arg
     }
   };
 
-  floatx4 acc[4][8];
+  floatx4 acc[4][JP];
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[m][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < JP; ++j) acc[m][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   // step kk: wait for this wave's loads of step kk (those of step kk + 1, L per
   // wave, may stay in flight) and for every wave's LDS reads of the previous
@@ -302,12 +318,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_arg
     issue(kk + 2, refill, wrefill);
     raw_t raw[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) raw[r] = *(const raw_t*)(cur + ((8 * g + r) * GN_PX + 8 * c) * 2);
+    for (int r = 0; r < 8; ++r) raw[r] = *(const raw_t*)(cur + ((8 * g + r) * PXT + JP * c) * 2);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < JP; ++j) {
       frag b;
 #pragma unroll
-      for (int r = 0; r < 8; ++r) b[r] = raw[r][j];  // channel 8 g + r of pixel 8 c + j
+      for (int r = 0; r < 8; ++r) b[r] = raw[r][j];  // channel 8 g + r of pixel JP c + j
 #pragma unroll
       for (int m = 0; m < 4; ++m) acc[m][j] = GemmOps<T>::mma(wf[m], b, acc[m][j]);
     }
@@ -325,9 +341,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_arg
   if (nk3 + 1 < nk) step(nk3 + 1, st1, st0, w1, w0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the block
 
-  // ---- epilogue: bias, activation, eight consecutive pixels per channel ----------------------------
-  const int px = p0 + 8 * c;
-  const int nvalid = P - px;  // pixels of this lane's run inside the image (>= 8: full run)
+  // ---- epilogue: bias, activation, JP consecutive pixels per channel ------------------------------
+  const int px = p0 + JP * c;
+  const int nvalid = P - px;  // pixels of this lane's run inside the image (>= JP: full run)
   // every bias first: loads and stores share one in-order counter, so a load
   // issued after a store would make its wait include that store's write
   float bias[4][4];
@@ -348,24 +364,26 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void gemm_nchw_kernel(kad_gemm_arg
         if (co >= a.cout || nvalid <= 0) continue;
         raw_t o;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < JP; ++j) {
           float v = acc[m][j][i] + bias[m][i];
           if constexpr (ACT == 1) v = v * __builtin_amdgcn_rcpf(1.f + __expf(-v));  // SiLU; 16-bit output
           o[j] = from_f32<T>(v);
         }
         T* dst = (T*)a.out + ((int64_t)n * a.cout + co) * P + px;
-        if (nvalid >= 8) {
-          if constexpr (V16) {
+        if (nvalid >= JP) {
+          typedef int intx2 __attribute__((ext_vector_type(2)));
+          if constexpr (JP == 4) {
+            *(intx2*)dst = __builtin_bit_cast(intx2, o);  // P % 4 == 0: 8-byte aligned
+          } else if constexpr (V16) {
             *(intx4*)dst = __builtin_bit_cast(intx4, o);
           } else {
-            typedef int intx2 __attribute__((ext_vector_type(2)));
             const intx4 q = __builtin_bit_cast(intx4, o);
             *(intx2*)dst = intx2{q[0], q[1]};
             *(intx2*)(dst + 4) = intx2{q[2], q[3]};
           }
         } else {
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
+          for (int j = 0; j < JP; ++j)
             if (j < nvalid) dst[j] = o[j];
         }
       }
@@ -687,19 +705,19 @@ static int launch_gemm(const kad_gemm_args& a, hipStream_t st, int hp, int wp) {
   return check_launch("kad_gemm1x1_fwd");
 }
 
-template <typename T, int NW>
+template <typename T, int NW, int PXT>
 static void launch_gemm_nchw_nw(const kad_gemm_args& a, hipStream_t st) {
   const int P = a.h * a.w;
-  const int tiles_px = ceil_div(P, GN_PX), co_blocks = ceil_div(a.cout, NW * GN_WCO);
+  const int tiles_px = ceil_div(P, PXT), co_blocks = ceil_div(a.cout, NW * GN_WCO);
   const int total = a.n * tiles_px * co_blocks;
   const int cin_pad = round_up(a.cin, 32);
   dim3 grid(round_up(total, 8));
   if (P % 8 == 0)
-    hipLaunchKernelGGL((gemm_nchw_kernel<T, true, NW>), grid, dim3(64 * NW), 0, st, a, P, tiles_px, co_blocks, total,
-                       cin_pad);
+    hipLaunchKernelGGL((gemm_nchw_kernel<T, true, NW, PXT>), grid, dim3(64 * NW), 0, st, a, P, tiles_px, co_blocks,
+                       total, cin_pad);
   else
-    hipLaunchKernelGGL((gemm_nchw_kernel<T, false, NW>), grid, dim3(64 * NW), 0, st, a, P, tiles_px, co_blocks, total,
-                       cin_pad);
+    hipLaunchKernelGGL((gemm_nchw_kernel<T, false, NW, PXT>), grid, dim3(64 * NW), 0, st, a, P, tiles_px, co_blocks,
+                       total, cin_pad);
 }
 
 // 4-wave blocks, two per CU: independent blocks drift apart, so one block's LDS
@@ -709,9 +727,18 @@ static void launch_gemm_nchw_nw(const kad_gemm_args& a, hipStream_t st) {
 // CU): ~1.6k cycles per k-step against 0.5k of MFMA per wave, and an epilogue of
 // ~14k cycles that is mostly SiLU (exp and rcp are quarter-rate: ~6k cycles per
 // wave for its 128 values) run by both blocks of a CU at the same time.
+//
+// Pixel tile: 128 for launches of at least two full rounds of 128-pixel blocks (two per CU),
+// else 64 (three blocks per CU, half the work per block).  Measured (MI355X, fp16, us, 128 -> 64):
+// [16,512,50,50] -> 512 + SiLU 43-45 -> 40-42; [8,256,100,100] -> 256 27 -> 25; [2,512,26,26]
+// -> 512 20.5 -> 11.7; [8,768,50,50] -> 512 unchanged (30-33); [8,256,100,100] -> 512 45-46 -> 47.
 template <typename T>
 static int launch_gemm_nchw(const kad_gemm_args& a, hipStream_t st) {
-  launch_gemm_nchw_nw<T, 4>(a, st);
+  const int64_t items128 = (int64_t)a.n * ceil_div(a.h * a.w, 128) * ceil_div(a.cout, 4 * GN_WCO);
+  if (items128 >= 2 * 2 * 256)
+    launch_gemm_nchw_nw<T, 4, 128>(a, st);
+  else
+    launch_gemm_nchw_nw<T, 4, 64>(a, st);
   return check_launch("kad_gemm1x1_fwd");
 }
 
